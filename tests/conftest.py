@@ -1,0 +1,43 @@
+"""Shared fixtures and markers.
+
+``gpu`` tests run the HIP library on a real device; everything else runs on the
+CPU (the oracle against the golden vectors, host-side logic, and the C-ABI
+library's load/export check)."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+GOLDEN = os.path.join(ROOT, "tests", "golden", "kquant_golden.npz")
+TYPES = ["Q2_K", "Q3_K", "Q4_K", "Q6_K"]
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (HIP device) and the built library")
+
+
+def heavy_tailed(nrow, n, seed):
+    """Cubed normals with a per-row U(0.2, 3) scale (the reference's tests/conftest.py:8-13)."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((nrow, n)) ** 3).astype(np.float32)
+    x *= rng.uniform(0.2, 3.0, size=(nrow, 1)).astype(np.float32)
+    return x
+
+
+def correlated_hessian(n, T, seed):
+    """X^T X of correlated Gaussian rows (the reference's tests/test_ef_synthetic.py:12-18)."""
+    rng = np.random.default_rng(seed)
+    mix = rng.standard_normal((n, n)) / np.sqrt(n)
+    mix += 1.5 * np.eye(n)
+    X = rng.standard_normal((T, n)) @ mix.T
+    return (X.T @ X).astype(np.float64)
+
+
+@pytest.fixture(scope="session")
+def golden():
+    return np.load(GOLDEN)

@@ -1,0 +1,198 @@
+"""Pins for the EF oracle (oracle/ef_oracle.py) -- the reference's ef.py cannot be
+imported here (it needs the absent pip ``gguf``), so each function is pinned by a
+closed form, an independent re-derivation, or the reference's own invariants."""
+import numpy as np
+import pytest
+
+from conftest import correlated_hessian, heavy_tailed
+from oracle import ef_oracle as E
+from oracle import kquant_oracle as K
+
+F32 = np.float32
+
+
+def _spectrum_matrix(n, eig, seed=0):
+    rng = np.random.default_rng(seed)
+    Q, _ = np.linalg.qr(rng.standard_normal((n, n)))
+    M = (Q * eig) @ Q.T
+    return (M + M.T) / 2
+
+
+def test_factor_closed_form_first_attempt():
+    """First attempt == chol((inv(H+lI) + inv(H+lI)^T)/2)^T (test_ef_cholesky_robust.py:51-64)."""
+    n = 128
+    rng = np.random.default_rng(5)
+    M = rng.standard_normal((n, n))
+    H = M @ M.T + n * np.eye(n)
+    Hd = H.copy()
+    Hd[np.diag_indices(n)] += 0.01 * float(np.mean(np.diag(Hd))) + 1e-8
+    Hinv = np.linalg.inv(Hd)
+    U_ref = np.linalg.cholesky((Hinv + Hinv.T) / 2).T
+    assert np.array_equal(E.inv_upper_factor(H, 0.01), U_ref)
+
+
+def test_factor_is_upper_inverse_factor():
+    """U upper with U^T U = inv(H + lI): a transposed or lower factor fails this."""
+    H = correlated_hessian(96, 512, seed=1)
+    U = E.inv_upper_factor(H, 0.01)
+    assert np.array_equal(U, np.triu(U)) and np.all(np.diag(U) > 0)
+    Hd = H + (0.01 * np.mean(np.diag(H)) + 1e-8) * np.eye(96)
+    assert np.allclose(U.T @ U @ Hd, np.eye(96), atol=1e-9)
+
+
+def test_factor_escalates_on_negative_eigenvalue(capsys):
+    """Exact spectrum with eig -2 breaks the fixed damp; escalation recovers
+    (test_ef_cholesky_robust.py:36-48)."""
+    n = 256
+    eig = np.linspace(1.0, 100.0, n)
+    eig[0] = -2.0
+    H = _spectrum_matrix(n, eig, seed=1)
+    U = E.inv_upper_factor(H, 0.01)
+    assert np.all(np.isfinite(U)) and np.array_equal(U, np.triu(U))
+    assert "escalated" in capsys.readouterr().err
+
+
+def test_factor_gives_up_after_max_tries():
+    H = -np.eye(8) * 1e6
+    H[0, 0] = 1.0          # mean diag negative -> base 1, shift can never win
+    with pytest.raises(np.linalg.LinAlgError, match="not positive definite"):
+        E.inv_upper_factor(H, 0.01, max_tries=3)
+
+
+@pytest.mark.parametrize("tt", ["Q2_K", "Q3_K", "Q4_K", "Q6_K"])
+def test_grid_and_repack_against_golden(golden, tt):
+    """Decoding the committed grid reproduces the reference decoder; re-packing the
+    decoded codes reproduces the golden bytes."""
+    x = golden["x/heavy"]
+    raw = golden[f"raw/heavy/imat/{tt}"]
+    nrow, n = x.shape
+    dl, ml, lo, hi, sub = E.committed_grid(tt, raw, nrow, n)
+    rec = golden[f"rec/heavy/imat/{tt}"]
+    # recover the signed codes from the reference reconstruction where dl != 0
+    dle = np.repeat(dl, sub, 1)
+    mle = np.repeat(ml, sub, 1) if ml is not None else np.zeros_like(dle)
+    nz = dle != 0
+    codes = np.where(nz, np.rint((rec + mle) / np.where(nz, dle, 1)), 0).astype(np.int32)
+    assert codes.min() >= lo and codes.max() <= hi
+    assert np.array_equal(np.where(nz, dle * codes.astype(F32) - mle, rec), rec)
+    # where dl == 0 the code cannot be read back from rec; take it from the bytes
+    if tt == "Q2_K":
+        packed = K.unpack_2bit(raw.reshape(-1, 84)[:, 16:80]).reshape(nrow, n).astype(np.int32)
+    elif tt == "Q3_K":
+        b = raw.reshape(-1, 110)
+        packed = K.unpack_q3_codes(b[:, 0:32], b[:, 32:96]).reshape(nrow, n)
+    elif tt == "Q4_K":
+        packed = K.unpack_nibbles(raw.reshape(-1, 144)[:, 16:144]).reshape(nrow, n).astype(np.int32)
+    else:
+        b = raw.reshape(-1, 210)
+        packed = K.unpack_q6_codes(b[:, 0:128], b[:, 128:192]).reshape(nrow, n) - 32
+    codes = np.where(nz, codes, packed)
+    assert np.array_equal(E.write_codes(tt, raw, codes, nrow, n), raw)
+
+
+def _scalar_sweep(xp, U, dl, ml, lo, hi, sub, order):
+    """Per-row scalar GPTQ recurrence: an independent restatement of the sweep."""
+    nrow, n = xp.shape
+    codes = np.zeros((nrow, n), np.int32)
+    for r in range(nrow):
+        t = [F32(v) for v in xp[r]]
+        for jj in range(n):
+            j = order[jj]
+            d = F32(dl[r, j // sub])
+            m = F32(ml[r, j // sub]) if ml is not None else F32(0)
+            if d == 0:
+                q, e = 0, F32(0)
+            else:
+                q = int(K.rint_magic(np.array([F32(F32(t[jj] + m) / d)]))[0])
+                q = min(max(q, lo), hi)
+                e = F32(F32(t[jj] - F32(F32(d * F32(q)) - m)) / F32(U[jj, jj]))
+            codes[r, j] = q
+            for k in range(jj + 1, n):
+                t[k] = F32(t[k] - F32(e * U[jj, k]))
+    return codes
+
+
+@pytest.mark.parametrize("tt", ["Q2_K", "Q3_K", "Q4_K", "Q6_K"])
+def test_sweep_matches_scalar_recurrence(tt):
+    n, nrow = 256, 3
+    W = heavy_tailed(nrow, n, seed=7)
+    H = correlated_hessian(n, 1024, seed=2)
+    order = E.act_order(H)
+    U = E.inv_upper_factor(H[np.ix_(order, order)]).astype(F32)
+    raw = K.QUANTIZE[tt](W, (np.diag(H) / 1024).astype(F32))
+    dl, ml, lo, hi, sub = E.committed_grid(tt, raw, nrow, n)
+    xp = W[:, order].copy()
+    got = E.sweep(xp.copy(), U, dl, ml, lo, hi, sub, order)
+    want = _scalar_sweep(xp, U, dl, ml, lo, hi, sub, order)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("tt", ["Q2_K", "Q3_K", "Q4_K", "Q6_K"])
+def test_diagonal_hessian_reduces_to_codec(tt):
+    """With a diagonal H nothing propagates: every superblock whose sub-block steps are
+    all non-zero gets exactly the codec's own requantized bytes."""
+    nrow, n = 6, 512
+    W = heavy_tailed(nrow, n, seed=11)
+    rng = np.random.default_rng(3)
+    H = np.diag(rng.uniform(0.5, 4.0, n))
+    qw = np.diag(H).astype(F32)
+    raw, _ = E.ef_encode(W, tt, qw, H)
+    ref = K.QUANTIZE[tt](W, qw)
+    dl, *_ = E.committed_grid(tt, ref, nrow, n)
+    full = (dl.reshape(nrow * n // 256, -1) != 0).all(1)
+    bp = K.BYTES_PER_SB[tt]
+    assert full.mean() > 0.9
+    assert np.array_equal(raw.reshape(-1, bp)[full], ref.reshape(-1, bp)[full])
+
+
+@pytest.mark.parametrize("tt", ["Q2_K", "Q3_K", "Q4_K"])
+def test_ef_beats_weighted_rtn(tt):
+    """test_ef_synthetic.py:30-46: >= 3 % lower tr(dW H dW^T) than weighted RTN."""
+    n, nrow, T = 512, 24, 4096
+    rng = np.random.default_rng({"Q2_K": 101, "Q3_K": 202, "Q4_K": 303}[tt])
+    W = (rng.standard_normal((nrow, n)) ** 3).astype(F32)
+    H = correlated_hessian(n, T, seed=0)
+    qw = (np.diag(H) / T).astype(F32)
+    rtn = K.roundtrip(W, tt, qw)
+    _, rec = E.ef_encode(W, tt, qw, H)
+    assert E.h_weighted_err(W, rec, H) < 0.97 * E.h_weighted_err(W, rtn, H)
+
+
+@pytest.mark.parametrize("tt", ["Q2_K", "Q4_K"])
+def test_act_order_beats_storage_order(tt):
+    """test_ef_synthetic.py:49-68: importance rising with the column index."""
+    n, nrow, T = 512, 24, 8192
+    rng = np.random.default_rng(7)
+    W = (rng.standard_normal((nrow, n)) ** 3).astype(F32)
+    var = 1.0 + 8.0 * np.arange(n) / n
+    Z = rng.standard_normal((T, n)) * np.sqrt(var)
+    Z += 0.4 * Z[:, [0]]
+    H = Z.T @ Z
+    qw = (np.diag(H) / T).astype(F32)
+    _, rec_a = E.ef_encode(W, tt, qw, H, act_order_on=True)
+    _, rec_s = E.ef_encode(W, tt, qw, H, act_order_on=False)
+    assert E.h_weighted_err(W, rec_a, H) < E.h_weighted_err(W, rec_s, H)
+
+
+def test_rows_are_independent():
+    n, nrow = 512, 8
+    W = heavy_tailed(nrow, n, seed=5)
+    H = correlated_hessian(n, 2048, seed=4)
+    qw = (np.diag(H) / 2048).astype(F32)
+    raw, _ = E.ef_encode(W, "Q2_K", qw, H)
+    p = np.random.default_rng(0).permutation(nrow)
+    raw_p, _ = E.ef_encode(W[p], "Q2_K", qw, H)
+    assert np.array_equal(raw_p, raw[p])
+
+
+def test_hessian_oracle_closed_form():
+    import torch
+    from oracle import hess_oracle as Ho
+    rng = np.random.default_rng(0)
+    X = (rng.standard_normal((2048, 96)) * np.exp(rng.standard_normal(96))).astype(np.float32)
+    H64 = Ho.xtx(X)
+    assert np.array_equal(H64, H64.T)
+    Ht = (torch.from_numpy(X).T @ torch.from_numpy(X)).numpy()
+    assert Ho.rel_fro(Ht, H64) < 1e-6
+    Hb, cnt = Ho.accumulate([X[:1000], X[1000:]])
+    assert cnt == 2048 and Ho.rel_fro(Hb, H64) < 1e-12
