@@ -1,0 +1,90 @@
+"""ctypes binding to libcoldpress_hip.so plus tensor plumbing.
+
+The library is loaded after ``import torch`` so that it binds to the HIP runtime
+torch already loaded (same soname), and device pointers from torch's allocator
+are valid in it. Nothing here computes on the CPU: a missing library or a
+missing GPU raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcoldpress_hip.so")
+
+CP_OK, CP_ERR_SHAPE, CP_ERR_TTYPE, CP_ERR_NOT_PD = 0, -1, -2, -3
+CP_ERR_HIP, CP_ERR_ARG, CP_ERR_ALIGN, CP_ERR_WORKSPACE = -4, -5, -6, -7
+
+TTYPE = {"Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q6_K": 14}
+
+_i64, _i32, _vp, _f64 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_double
+
+# name -> (restype, argtypes); every symbol include/coldpress_hip.h declares
+SIGNATURES = {
+    "cp_last_error": (ctypes.c_char_p, []),
+    "cp_kq_block_bytes": (_i32, [_i32]),
+    "cp_kq_quantize": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "cp_kq_dequantize": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp]),
+}
+
+_lib = None
+
+
+class HipError(RuntimeError):
+    """A HIP runtime failure reported by the library."""
+
+
+def load(require_gpu=True):
+    """The loaded library. Raises if it is not built, or (by default) if no GPU is visible."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run `python -m perm_amd.build` "
+                               f"(there is no CPU fallback)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
+        _lib = lib
+    if require_gpu and not torch.cuda.is_available():
+        raise RuntimeError("perm_amd needs a HIP device (torch.cuda.is_available() is False)")
+    return _lib
+
+
+def check(status, exc_for_shape=ValueError):
+    """Map a cp_status to the exception the reference raises for the same condition."""
+    if status >= 0:
+        return status
+    msg = (_lib.cp_last_error() or b"").decode(errors="replace")
+    if status == CP_ERR_NOT_PD:
+        raise np.linalg.LinAlgError(msg)
+    if status == CP_ERR_SHAPE:
+        raise exc_for_shape(msg)
+    if status == CP_ERR_TTYPE:
+        raise KeyError(msg)
+    if status == CP_ERR_HIP:
+        raise HipError(msg)
+    raise ValueError(f"{msg} (status {status})")
+
+
+def stream_ptr():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def to_device(a, dtype):
+    """(contiguous device tensor of ``dtype``, True if ``a`` came from the host)."""
+    if isinstance(a, torch.Tensor):
+        host = not a.is_cuda
+        t = a.to(device="cuda", dtype=dtype, non_blocking=False)
+        return t.contiguous(), host
+    arr = np.ascontiguousarray(np.asarray(a))
+    return torch.from_numpy(arr).to(device="cuda", dtype=dtype).contiguous(), True
+
+
+def to_host(t):
+    return t.cpu().numpy()

@@ -1,0 +1,99 @@
+// Device-side numerics shared by the k-quant and EF kernels (gfx950).
+//
+// Every routine here reproduces a float32 operation sequence of the numpy
+// encoder in coldpress/kquant.py bit for bit. The library is compiled with
+// -ffp-contract=off (no fused multiply-add), IEEE division and sqrt, and f32
+// denormals preserved, so each C++ expression below rounds exactly where the
+// numpy expression it restates rounds.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cp {
+
+// ggml nearest_int: round half to even via the 1.5*2^23 magic add
+// (kquant.py:25-28). Outside |v| < 2^22 this returns the same deterministic
+// bit pattern as the reference, which callers clip.
+__device__ __forceinline__ int rint_magic(float v) {
+  float s = v + 12582912.0f;
+  return (__float_as_int(s) & 0x7FFFFF) - 0x400000;
+}
+
+__device__ __forceinline__ uint16_t half_bits(float v) {
+  _Float16 h = (_Float16)v;  // v_cvt_f16_f32, round to nearest even
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float half_value(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+
+__device__ __forceinline__ int clampi(int v, int lo, int hi) {
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+
+// numpy's float32 pairwise sum of N contiguous values (8 <= N <= 128, N % 8 == 0):
+// eight interleaved accumulators r[j] = a[j] + a[j+8] + ..., then
+// ((r0+r1)+(r2+r3)) + ((r4+r5)+(r6+r7)); the reduction starts from +0.0.
+template <int N>
+__device__ __forceinline__ float psum(const float (&a)[N]) {
+  static_assert(N % 8 == 0 && N >= 8 && N <= 128, "pairwise block");
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = a[j];
+#pragma unroll
+  for (int i = 8; i < N; i += 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = r[j] + a[i + j];
+  }
+  float s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+  return 0.0f + s;
+}
+
+// The same sum over G lanes (one value per lane, G = 8 or 16) as an xor
+// butterfly: xor 8 forms r[j] = a[j] + a[j+8], then xor 1, 2, 4 build the tree.
+// IEEE addition is commutative, so every lane of the group ends with the
+// identical, numpy-ordered result.
+template <int G>
+__device__ __forceinline__ float gsum(float v) {
+  static_assert(G == 8 || G == 16, "group width");
+  if (G == 16) v = v + __shfl_xor(v, 8);
+  v = v + __shfl_xor(v, 1);
+  v = v + __shfl_xor(v, 2);
+  v = v + __shfl_xor(v, 4);
+  return 0.0f + v;
+}
+
+template <int G>
+__device__ __forceinline__ float gmax(float v) {
+#pragma unroll
+  for (int k = G / 2; k >= 1; k >>= 1) v = fmaxf(v, __shfl_xor(v, k));
+  return v;
+}
+
+// First (lowest lane) value of largest |v| over the group: returns the signed
+// value; |value| in *amax (numpy argmax tie rule).
+template <int G>
+__device__ __forceinline__ float gfirst_absmax(float v, int g, float* amax) {
+  float a = fabsf(v);
+  int idx = g;
+#pragma unroll
+  for (int k = G / 2; k >= 1; k >>= 1) {
+    float ao = __shfl_xor(a, k);
+    float vo = __shfl_xor(v, k);
+    int io = __shfl_xor(idx, k);
+    bool take = (ao > a) || (ao == a && io < idx);
+    a = take ? ao : a;
+    v = take ? vo : v;
+    idx = take ? io : idx;
+  }
+  *amax = a;
+  return v;
+}
+
+template <int G>
+__device__ __forceinline__ float gbcast(float v, int src) {
+  return __shfl(v, src, G);
+}
+
+}  // namespace cp

@@ -1,0 +1,373 @@
+// Sub-block grid fits of the k-quant encoders, on the device.
+//
+// In-lane fits (one lane owns one sub-block of N values in registers):
+//   fit_affine<N>       make_qkx2 / make_qkx3 search      coldpress/kquant.py:42-94
+//   fit_signed<N>       make_qx_quants, rmse_type 1        coldpress/kquant.py:97-133
+//   fit_signed_descent  make_q3_quants                     coldpress/kquant.py:136-179
+// Cross-lane fits (one lane owns one element of a G-wide vector of super-block
+// scales; G = 16 for Q2_K/Q3_K, 8 for Q4_K):
+//   gfit_nonneg<G>      make_qp_quants                     coldpress/kquant.py:182-235
+//   gfit_signed<G>      make_qx_quants on super-scales     coldpress/kquant.py:460
+//
+// Each function evaluates the same float32 expressions, in the same order, as
+// the numpy routine it restates; reductions go through psum / gsum, which
+// reproduce numpy's pairwise summation order.
+#pragma once
+#include "cp_device.h"
+
+namespace cp {
+
+template <int N>
+__device__ __forceinline__ float affine_err(const float (&x)[N], const float (&w)[N],
+                                            const int (&L)[N], float scale, float off,
+                                            bool mad) {
+  float t[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    float r = (scale * (float)L[i] + off) - x[i];
+    r = mad ? fabsf(r) : r * r;
+    t[i] = w[i] * r;
+  }
+  return psum<N>(t);
+}
+
+// Weighted affine fit x ~ scale * L + lo, L in [0, nmax]. Returns scale and -lo
+// (the "min" the containers store); L receives the codes.
+template <int N>
+__device__ __forceinline__ void fit_affine(const float (&x)[N], const float (&w)[N], int nmax,
+                                           float rmin, float rdelta, int nstep, bool mad,
+                                           bool strict_dead, float* scale_out, float* min_out,
+                                           int (&L)[N]) {
+  float hi = x[0], lo = x[0];
+#pragma unroll
+  for (int i = 1; i < N; ++i) {
+    hi = fmaxf(hi, x[i]);
+    lo = fminf(lo, x[i]);
+  }
+  lo = fminf(lo, 0.0f);
+  float t[N];
+  float sw = psum<N>(w);
+#pragma unroll
+  for (int i = 0; i < N; ++i) t[i] = w[i] * x[i];
+  float swx = psum<N>(t);
+  const bool dead = strict_dead ? (hi <= lo) : (hi == lo);
+
+  float inv = (float)nmax / (dead ? 1.0f : hi - lo);
+  float scale = 1.0f / inv;
+#pragma unroll
+  for (int i = 0; i < N; ++i) L[i] = clampi(rint_magic(inv * (x[i] - lo)), 0, nmax);
+  float best = affine_err<N>(x, w, L, scale, lo, mad);
+
+  for (int step = 0; step <= nstep; ++step) {
+    float span = hi - lo;
+    span = span > 0.0f ? span : 1.0f;
+    float inv_c = ((rmin + rdelta * (float)step) + (float)nmax) / span;
+    int Lc[N];
+    float a[N], b[N], c[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      Lc[i] = clampi(rint_magic(inv_c * (x[i] - lo)), 0, nmax);
+      float lf = (float)Lc[i];
+      float wl = w[i] * lf;
+      a[i] = wl;
+      b[i] = wl * lf;
+      c[i] = wl * x[i];
+    }
+    float sl = psum<N>(a);
+    float sl2 = psum<N>(b);
+    float sxl = psum<N>(c);
+    float det = sw * sl2 - sl * sl;
+    float s_c = (sw * sxl - swx * sl) / det;
+    float m_c = (sl2 * swx - sl * sxl) / det;
+    float s_alt = sxl / sl2;
+    if (m_c > 0.0f) {
+      m_c = 0.0f;
+      s_c = s_alt;
+    }
+    float e_c = affine_err<N>(x, w, Lc, s_c, m_c, mad);
+    if (det > 0.0f && e_c < best && !dead) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) L[i] = Lc[i];
+      best = e_c;
+      scale = s_c;
+      lo = m_c;
+    }
+  }
+  if (dead) {
+    scale = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) L[i] = 0;
+  }
+  *scale_out = scale;
+  *min_out = -lo;
+}
+
+// Symmetric signed fit x ~ scale * L, L in [-nmax, nmax-1]; weights w (pass
+// x*x for the unweighted path). L receives codes + nmax.
+template <int N>
+__device__ __forceinline__ float fit_signed(const float (&x)[N], const float (&w)[N], int nmax,
+                                            int (&L)[N]) {
+  float amax = fabsf(x[0]), sext = x[0];
+#pragma unroll
+  for (int i = 1; i < N; ++i) {
+    float a = fabsf(x[i]);
+    if (a > amax) {
+      amax = a;
+      sext = x[i];
+    }
+  }
+  const bool dead = amax < 1e-15f;
+  sext = dead ? 1.0f : sext;
+  float wx[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) wx[i] = w[i] * x[i];
+
+  float inv = -(float)nmax / sext;
+  float p[N], q[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    L[i] = clampi(rint_magic(inv * x[i]), -nmax, nmax - 1);
+    float lf = (float)L[i];
+    p[i] = wx[i] * lf;
+    q[i] = (w[i] * lf) * lf;
+  }
+  float slx = psum<N>(p), sl2 = psum<N>(q);
+  float scale = sl2 != 0.0f ? slx / sl2 : 0.0f;
+  float best = scale * slx;
+  for (int s = -9; s <= 9; ++s) {
+    if (s == 0) continue;
+    float inv_c = -((float)nmax + 0.1f * (float)s) / sext;
+    int Lc[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      Lc[i] = clampi(rint_magic(inv_c * x[i]), -nmax, nmax - 1);
+      float lf = (float)Lc[i];
+      p[i] = wx[i] * lf;
+      q[i] = (w[i] * lf) * lf;
+    }
+    float slx_c = psum<N>(p), sl2_c = psum<N>(q);
+    if (sl2_c > 0.0f && slx_c * slx_c > best * sl2_c && !dead) {
+      float s_c = slx_c / sl2_c;
+#pragma unroll
+      for (int i = 0; i < N; ++i) L[i] = Lc[i];
+      scale = s_c;
+      best = s_c * slx_c;
+    }
+  }
+  if (dead) {
+    scale = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) L[i] = 0;
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) L[i] += nmax;
+  return scale;
+}
+
+// Coordinate descent on fixed-grid codes, elements visited in order, at most 5
+// sweeps, stopping after a sweep without a move (kquant.py:152-174, :208-230).
+// SIGNED selects the make_q3_quants rules (codes clipped to [lo, hi], the new
+// suml2 must stay positive) versus make_qp_quants (codes capped at hi, both
+// partial sums must be positive).
+template <int N, bool SIGNED>
+__device__ __forceinline__ void descend(const float (&x)[N], const float (&w)[N], float (&Lf)[N],
+                                        float* slx_io, float* sl2_io, int lo, int hi,
+                                        bool active) {
+  float slx = *slx_io, sl2 = *sl2_io;
+  for (int sweep = 0; sweep < 5 && active; ++sweep) {
+    bool moved = false;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      float wxi = w[i] * x[i];
+      float slx_o = slx - wxi * Lf[i];
+      float sl2_o = sl2 - (w[i] * Lf[i]) * Lf[i];
+      bool ok = SIGNED ? (slx_o > 0.0f) : (slx_o > 0.0f && sl2_o > 0.0f);
+      int qi = rint_magic((x[i] * sl2_o) / (slx_o == 0.0f ? 1.0f : slx_o));
+      qi = SIGNED ? clampi(qi, lo, hi) : (qi < hi ? qi : hi);
+      float qf = (float)qi;
+      float slx_n = slx_o + wxi * qf;
+      float sl2_n = sl2_o + (w[i] * qf) * qf;
+      bool take = ok && qf != Lf[i] && (slx_n * slx_n) * sl2 > (slx * slx) * sl2_n;
+      if (SIGNED) take = take && sl2_n > 0.0f;
+      if (take) {
+        Lf[i] = qf;
+        slx = slx_n;
+        sl2 = sl2_n;
+        moved = true;
+      }
+    }
+    active = moved;
+  }
+  *slx_io = slx;
+  *sl2_io = sl2;
+}
+
+// make_q3_quants on one 16-value sub-block: returns scale, L receives codes + nmax.
+__device__ __forceinline__ float fit_signed_descent16(const float (&x)[16], int nmax,
+                                                      int (&L)[16]) {
+  float amax = fabsf(x[0]), sext = x[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) {
+    float a = fabsf(x[i]);
+    if (a > amax) {
+      amax = a;
+      sext = x[i];
+    }
+  }
+  const bool dead = amax < 1e-15f;
+  sext = dead ? 1.0f : sext;
+  float inv = -(float)nmax / sext;
+  float w[16], Lf[16], p[16], q[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    w[i] = x[i] * x[i];
+    Lf[i] = (float)clampi(rint_magic(inv * x[i]), -nmax, nmax - 1);
+    p[i] = (w[i] * x[i]) * Lf[i];
+    q[i] = (w[i] * Lf[i]) * Lf[i];
+  }
+  float slx = psum<16>(p), sl2 = psum<16>(q);
+  descend<16, true>(x, w, Lf, &slx, &sl2, -nmax, nmax - 1, !dead);
+  float scale = sl2 > 0.0f ? slx / sl2 : 0.0f;
+  if (dead) scale = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) L[i] = (dead ? 0 : (int)Lf[i]) + nmax;
+  return scale;
+}
+
+// Gather the G values of a lane group into every lane's registers.
+template <int G>
+__device__ __forceinline__ void ggather(float v, float (&out)[G]) {
+#pragma unroll
+  for (int i = 0; i < G; ++i) out[i] = __shfl(v, i, G);
+}
+
+// make_qp_quants over a G-lane vector (lane g holds x[g], w[g]). The candidate
+// search runs lane-parallel with butterfly sums. The descent is sequential, so
+// every lane replays it on gathered copies. Returns d; *Lout receives this
+// lane's code. Lanes with ``run_descent`` false skip the descent (they must
+// not use *Lout).
+template <int G>
+__device__ __forceinline__ float gfit_nonneg_search(float x, float w, int nmax, float* inv_out,
+                                                    bool* dead_out) {
+  float top = gmax<G>(x);
+  const bool dead = top < 1e-15f;
+  top = dead ? 1.0f : top;
+  float inv = (float)nmax / top;
+  float L0 = (float)rint_magic(inv * x);
+  float r = x - (1.0f / inv) * L0;
+  float best = gsum<G>((w * r) * r);
+  for (int s = -4; s <= 4; ++s) {
+    if (s == 0) continue;
+    float inv_c = (0.1f * (float)s + (float)nmax) / top;
+    int li = rint_magic(inv_c * x);
+    float lc = (float)(li < nmax ? li : nmax);
+    float rc = x - (1.0f / inv_c) * lc;
+    float e_c = gsum<G>((w * rc) * rc);
+    if (e_c < best && !dead) {
+      best = e_c;
+      inv = inv_c;
+    }
+  }
+  *inv_out = inv;
+  *dead_out = dead;
+  return top;
+}
+
+// Descent half of make_qp_quants on gathered copies; returns d and fills Lf.
+template <int G>
+__device__ __forceinline__ float nonneg_descent(const float (&xs)[G], const float (&ws)[G],
+                                                float inv, bool dead, int nmax,
+                                                float (&Lf)[G]) {
+  float p[G], q[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    int li = rint_magic(inv * xs[i]);
+    Lf[i] = (float)(li < nmax ? li : nmax);
+    p[i] = (ws[i] * xs[i]) * Lf[i];
+    q[i] = (ws[i] * Lf[i]) * Lf[i];
+  }
+  float slx = psum<G>(p), sl2 = psum<G>(q);
+  descend<G, false>(xs, ws, Lf, &slx, &sl2, 0, nmax, !dead);
+  float d = sl2 > 0.0f ? slx / sl2 : 0.0f;
+  if (dead) {
+    d = 0.0f;
+#pragma unroll
+    for (int i = 0; i < G; ++i) Lf[i] = 0.0f;
+  }
+  return d;
+}
+
+// make_qp_quants for two G-vectors at once (the super-block scales and mins):
+// lanes g < G/2 replay the descent for ``a``, lanes g >= G/2 for ``b``, halving
+// the sequential part. Returns this lane's (d_a, La) and (d_b, Lb).
+template <int G>
+__device__ __forceinline__ void gfit_nonneg_pair(float a, float b, float w, int nmax, int g,
+                                                 float* da, int* La, float* db, int* Lb) {
+  float inv_a, inv_b;
+  bool dead_a, dead_b;
+  gfit_nonneg_search<G>(a, w, nmax, &inv_a, &dead_a);
+  gfit_nonneg_search<G>(b, w, nmax, &inv_b, &dead_b);
+  float as[G], bs[G], ws[G];
+  ggather<G>(a, as);
+  ggather<G>(b, bs);
+  ggather<G>(w, ws);
+  const bool first = g < G / 2;
+  float xs[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) xs[i] = first ? as[i] : bs[i];
+  float Lf[G];
+  float d = nonneg_descent<G>(xs, ws, first ? inv_a : inv_b, first ? dead_a : dead_b, nmax, Lf);
+  // lane 0 holds the result for a, lane G/2 the result for b
+  float mine_a = 0.0f, mine_b = 0.0f;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    float va = __shfl(Lf[i], 0, G);
+    float vb = __shfl(Lf[i], G / 2, G);
+    if (i == g) {
+      mine_a = va;
+      mine_b = vb;
+    }
+  }
+  *da = __shfl(d, 0, G);
+  *db = __shfl(d, G / 2, G);
+  *La = (int)mine_a;
+  *Lb = (int)mine_b;
+}
+
+// make_qx_quants (rmse_type 1) over a G-lane vector with weights w: returns the
+// scale; *L receives this lane's code + nmax.
+template <int G>
+__device__ __forceinline__ float gfit_signed(float x, float w, int nmax, int g, int* Lout) {
+  float amax;
+  float sext = gfirst_absmax<G>(x, g, &amax);
+  const bool dead = amax < 1e-15f;
+  sext = dead ? 1.0f : sext;
+  float wx = w * x;
+  float inv = -(float)nmax / sext;
+  int L = clampi(rint_magic(inv * x), -nmax, nmax - 1);
+  float lf = (float)L;
+  float slx = gsum<G>(wx * lf), sl2 = gsum<G>((w * lf) * lf);
+  float scale = sl2 != 0.0f ? slx / sl2 : 0.0f;
+  float best = scale * slx;
+  for (int s = -9; s <= 9; ++s) {
+    if (s == 0) continue;
+    float inv_c = -((float)nmax + 0.1f * (float)s) / sext;
+    int Lc = clampi(rint_magic(inv_c * x), -nmax, nmax - 1);
+    float lc = (float)Lc;
+    float slx_c = gsum<G>(wx * lc), sl2_c = gsum<G>((w * lc) * lc);
+    if (sl2_c > 0.0f && slx_c * slx_c > best * sl2_c && !dead) {
+      float s_c = slx_c / sl2_c;
+      L = Lc;
+      scale = s_c;
+      best = s_c * slx_c;
+    }
+  }
+  if (dead) {
+    scale = 0.0f;
+    L = 0;
+  }
+  *Lout = L + nmax;
+  return scale;
+}
+
+}  // namespace cp
