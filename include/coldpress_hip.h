@@ -57,6 +57,66 @@ int cp_kq_quantize(int ttype, const float* x, int64_t nrow, int64_t n, const flo
 int cp_kq_dequantize(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, float* y,
                      void* stream);
 
+/* ---- damped inverse-Hessian factor (coldpress/ef.py:46-84, 187-189) ---- */
+
+/* order[z][jj] = column visited jj-th: stable argsort of -diag(H_z) for each of
+ * ``batch`` [n, n] matrices (h_dtype 0 = float32, 1 = float64). Replaces
+ * ef.py:187 ``np.argsort(-np.diag(H))`` (ties broken by index). */
+int cp_act_order(const void* H, int h_dtype, int64_t n, int batch, int32_t* order, void* stream);
+
+/* Workspace bytes cp_chol_inv_upper needs for ``batch`` matrices of size n. */
+size_t cp_chol_ws_bytes(int64_t n, int batch);
+
+/* U_z = chol(inv(Hp_z + lambda I))^T, upper triangular [n, n] with
+ * U^T U = inv(Hp + lambda I), where Hp = H[order][:, order] (identity order when
+ * order is NULL), lambda = damp * mean(diag Hp) + 1e-8 (mean replaced by 1 when
+ * not positive). Computed in float64; stored as float32 (u_dtype 0, what the EF
+ * sweep consumes) or float64 (u_dtype 1). A matrix whose factorization fails is
+ * retried with damp x 10, up to max_tries attempts; damp_used (host array of
+ * ``batch`` doubles, may be NULL) receives the damp that succeeded.
+ * Returns CP_ERR_NOT_PD when a matrix fails every attempt.
+ * Replaces ef.cholesky_inv_upper(Hp, damp, _max_tries) -- coldpress/ef.py:46-84
+ * -- together with the gather and float32 cast of ef.py:188-189.
+ * Synchronizes ``stream`` (it reads the per-matrix failure flags). */
+int cp_chol_inv_upper(const void* H, int h_dtype, int64_t n, int batch, const int32_t* order,
+                      double damp, int max_tries, void* U, int u_dtype, double* damp_used,
+                      void* ws, size_t ws_bytes, void* stream);
+
+/* ---- EF encode (coldpress/ef.py:179-218) ---- */
+
+enum cp_ef_mode {
+  CP_EF_EXACT = 0 /* error propagation in the reference's sequential float32 order: bit-exact */
+};
+
+typedef struct cp_ef_tensor {
+  int ttype;             /* CP_Q2_K, CP_Q3_K, CP_Q4_K or CP_Q6_K                       */
+  int64_t nrow, n;       /* weight shape, n % 256 == 0                                  */
+  const float* x;        /* [nrow, n] weights                                           */
+  const float* qw;       /* [n] importance (imatrix means) or NULL                      */
+  const float* U;        /* [n, n] float32 upper factor in visiting order (cp_chol_inv_upper) */
+  const int32_t* order;  /* [n] visiting order (cp_act_order)                           */
+  uint8_t* raw;          /* out: [nrow, n/256*block_bytes] container bytes              */
+  float* recon;          /* out: [nrow, n] decoded weights, or NULL                     */
+} cp_ef_tensor;
+
+/* Workspace bytes cp_ef_encode_batch needs for these tensors. */
+size_t cp_ef_ws_bytes(const cp_ef_tensor* tensors, int count);
+
+/* GPTQ error feedback into committed k-quant grids for ``count`` independent
+ * tensors in one pass: per iteration, commit the container with the stock
+ * encoder (cp_kq_quantize) on the current targets, sweep the columns in
+ * visiting order quantizing onto the committed grid and propagating the
+ * error through U, re-pack the codes; after n_iter iterations decode into
+ * recon. Replaces ef.ef_encode(x, tt, qw, H, n_iter, damp, act_order=True)
+ * (coldpress/ef.py:179-218) once U and order are computed. */
+int cp_ef_encode_batch(const cp_ef_tensor* tensors, int count, int n_iter, int mode, void* ws,
+                       size_t ws_bytes, void* stream);
+
+/* Single-tensor form of cp_ef_encode_batch (CP_EF_EXACT). */
+int cp_ef_encode(int ttype, const float* x, int64_t nrow, int64_t n, const float* qw,
+                 const float* U, const int32_t* order, int n_iter, uint8_t* raw, float* recon,
+                 void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

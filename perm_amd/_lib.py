@@ -19,6 +19,19 @@ CP_ERR_HIP, CP_ERR_ARG, CP_ERR_ALIGN, CP_ERR_WORKSPACE = -4, -5, -6, -7
 TTYPE = {"Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q6_K": 14}
 
 _i64, _i32, _vp, _f64 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_double
+_sz = ctypes.c_size_t
+
+CP_EF_EXACT = 0
+
+
+class EfTensor(ctypes.Structure):
+    """struct cp_ef_tensor (include/coldpress_hip.h)."""
+    _fields_ = [("ttype", ctypes.c_int), ("nrow", ctypes.c_int64), ("n", ctypes.c_int64),
+                ("x", _vp), ("qw", _vp), ("U", _vp), ("order", _vp), ("raw", _vp),
+                ("recon", _vp)]
+
+
+_ef_p = ctypes.POINTER(EfTensor)
 
 # name -> (restype, argtypes); every symbol include/coldpress_hip.h declares
 SIGNATURES = {
@@ -26,7 +39,20 @@ SIGNATURES = {
     "cp_kq_block_bytes": (_i32, [_i32]),
     "cp_kq_quantize": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _vp]),
     "cp_kq_dequantize": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp]),
+    "cp_act_order": (_i32, [_vp, _i32, _i64, _i32, _vp, _vp]),
+    "cp_chol_ws_bytes": (_sz, [_i64, _i32]),
+    "cp_chol_inv_upper": (_i32, [_vp, _i32, _i64, _i32, _vp, _f64, _i32, _vp, _i32, _vp, _vp,
+                                 _sz, _vp]),
+    "cp_ef_ws_bytes": (_sz, [_ef_p, _i32]),
+    "cp_ef_encode_batch": (_i32, [_ef_p, _i32, _i32, _i32, _vp, _sz, _vp]),
+    "cp_ef_encode": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _sz,
+                            _vp]),
 }
+
+
+def workspace(nbytes, device="cuda"):
+    """A 256-byte aligned device workspace (torch's caching allocator aligns to 512)."""
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 _lib = None
 

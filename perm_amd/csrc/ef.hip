@@ -1,0 +1,423 @@
+// GPTQ-style error feedback (EF) into committed k-quant grids on gfx950
+// (coldpress/ef.py:179-218, with _grid_params :87-127 and _repack :130-176).
+//
+// Data layout in HBM, per tensor (nrow x n weights, columns visited in act order):
+//   WpT    [n][nrow] f32  original weights, visiting order, column-major (one
+//                         visiting column is one coalesced 4*nrow-byte row)
+//   E      [n][nrow] f32  scaled errors e_j of every visited column
+//   WcurT  [n][nrow] f32  error-compensated targets at quantization time
+//   LT     [n][nrow] u8   stored codes (q - lo) per visited column
+//   dlT/mlT [n/sub][nrow] f32  committed grid step / offset per storage sub-block
+//
+// Sweep: one wavefront owns a stripe of 64 rows (lane = row) and walks the
+// visiting order in 64-column blocks. Left-looking: before a block is swept,
+// each of its elements receives the updates of all earlier columns,
+//     t -= e_jj * U[jj][k]   (float32 multiply, then subtract, jj ascending),
+// which is exactly the order in which ef.py:213 applies them, so the sweep is
+// bit-identical to the reference. U's row segments are wave-uniform and are
+// fetched through the scalar path; E is re-read from L2 by the same lanes that
+// wrote it, so stripes never synchronize with each other.
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "cp_device.h"
+#include "cp_host.h"
+
+namespace cp {
+
+int kq_quantize(int ttype, const float* x, int64_t nrow, int64_t n, const float* qw, uint8_t* out,
+                hipStream_t st);
+int kq_dequantize(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, float* y, hipStream_t st);
+
+constexpr int BLK = 32;  // columns per sweep block
+
+struct SweepTask {
+  const float* WpT;
+  const float* U;
+  const float* dlT;
+  const float* mlT;  // null for the symmetric containers
+  const int* sbidx;  // storage sub-block of each visiting column
+  float* E;
+  float* WcurT;
+  uint8_t* LT;
+  int nrow, n, lo, hi;
+};
+
+// Up to kTasksPerLaunch tensors travel by value in the kernel arguments.
+constexpr int kTasksPerLaunch = 48;
+struct SweepBatch {
+  SweepTask t[kTasksPerLaunch];
+};
+static_assert(sizeof(SweepBatch) <= 4000, "kernel argument block");
+
+// The task table reaches device memory through the kernel arguments of a
+// one-block copy kernel (no host staging buffer whose lifetime would have to
+// outlast an asynchronous copy).
+__global__ void ef_tasks_store_kernel(const SweepBatch batch, int count, SweepTask* dst) {
+  if ((int)threadIdx.x < count) dst[threadIdx.x] = batch.t[threadIdx.x];
+}
+
+// Address-space views. U is read-only for the whole sweep and its row
+// segments are wave-uniform, so it is read through the constant address space
+// (scalar loads into SGPRs); per-lane traffic goes through global loads/stores.
+typedef const float __attribute__((address_space(4)))* ConstF;
+typedef const float __attribute__((address_space(1)))* GlobF;
+typedef float __attribute__((address_space(1)))* GlobFw;
+typedef uint8_t __attribute__((address_space(1)))* GlobBw;
+
+__device__ __forceinline__ float ld_uniform(const float* p, int64_t i) { return ((ConstF)p)[i]; }
+__device__ __forceinline__ float ld_lane(const float* p, int64_t i) { return ((GlobF)p)[i]; }
+
+// Grid: x = groups of 4 stripes (256 rows), y = task.
+template <int B>
+__global__ __launch_bounds__(256) void ef_sweep_exact_kernel(const SweepTask* __restrict__ tasks) {
+  const SweepTask tk = tasks[blockIdx.y];
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if ((int)(blockIdx.x * 256) >= tk.nrow) return;
+  const int nrow = tk.nrow, n = tk.n;
+  const bool valid = r < nrow;
+  const int rr = valid ? r : nrow - 1;
+  __shared__ float su[B][B];
+  for (int i1 = 0; i1 < n; i1 += B) {
+    float t[B];
+#pragma unroll
+    for (int k = 0; k < B; ++k) t[k] = ld_lane(tk.WpT, (int64_t)(i1 + k) * nrow + rr);
+    for (int jj = 0; jj < i1; ++jj) {
+      const float e = ld_lane(tk.E, (int64_t)jj * nrow + rr);
+      const int64_t ub = (int64_t)jj * n + i1;
+#pragma unroll
+      for (int k = 0; k < B; ++k) t[k] = t[k] - e * ld_uniform(tk.U, ub + k);
+    }
+    // the block's diagonal U tile, shared by the 4 stripes of the workgroup
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < B * B; idx += 256)
+      su[idx / B][idx % B] = ld_lane(tk.U, (int64_t)(i1 + idx / B) * n + i1 + idx % B);
+    __syncthreads();
+#pragma unroll
+    for (int jj = 0; jj < B; ++jj) {
+      const int c = i1 + jj;
+      const int s = tk.sbidx[c];
+      const float dl = ld_lane(tk.dlT, (int64_t)s * nrow + rr);
+      const float ml = tk.mlT ? ld_lane(tk.mlT, (int64_t)s * nrow + rr) : 0.0f;
+      const bool nz = dl != 0.0f;
+      const int q = nz ? clampi(rint_magic((t[jj] + ml) / dl), tk.lo, tk.hi) : 0;
+      const float recon = dl * (float)q - ml;
+      const float e = nz ? (t[jj] - recon) / su[jj][jj] : 0.0f;
+      if (valid) {
+        ((GlobFw)tk.E)[(int64_t)c * nrow + r] = e;
+        ((GlobFw)tk.WcurT)[(int64_t)c * nrow + r] = t[jj];
+        ((GlobBw)tk.LT)[(int64_t)c * nrow + r] = (uint8_t)(q - tk.lo);
+      }
+#pragma unroll
+      for (int k = jj + 1; k < B; ++k) t[k] = t[k] - e * su[jj][k];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- index helpers
+__global__ void ef_index_kernel(const int* order, int n, int sub, int* inv, int* sbidx) {
+  int jj = blockIdx.x * blockDim.x + threadIdx.x;
+  if (jj >= n) return;
+  int c = order[jj];
+  inv[c] = jj;
+  sbidx[jj] = c / sub;
+}
+
+// dst[inv[c]][r] = src[r][c]: row-major storage order -> column-major visiting
+// order, through a 64x64 LDS tile (coalesced on both sides).
+template <typename T>
+__global__ __launch_bounds__(256) void ef_to_visit_kernel(const T* __restrict__ src, int nrow, int n,
+                                                          const int* __restrict__ inv,
+                                                          T* __restrict__ dst) {
+  __shared__ T tile[64][65];
+  const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < 64; i += 4) {
+    int r = r0 + i, c = c0 + tx;
+    if (r < nrow && c < n) tile[i][tx] = src[(int64_t)r * n + c];
+  }
+  __syncthreads();
+  for (int j = ty; j < 64; j += 4) {
+    int c = c0 + j, r = r0 + tx;
+    if (r < nrow && c < n) dst[(int64_t)inv[c] * nrow + r] = tile[tx][j];
+  }
+}
+
+// dst[r][c] = src[inv[c]][r]: the inverse of ef_to_visit_kernel.
+template <typename T>
+__global__ __launch_bounds__(256) void ef_to_storage_kernel(const T* __restrict__ src, int nrow, int n,
+                                                            const int* __restrict__ inv,
+                                                            T* __restrict__ dst) {
+  __shared__ T tile[64][65];
+  const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int j = ty; j < 64; j += 4) {
+    int c = c0 + j, r = r0 + tx;
+    if (r < nrow && c < n) tile[tx][j] = src[(int64_t)inv[c] * nrow + r];
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    int r = r0 + i, c = c0 + tx;
+    if (r < nrow && c < n) dst[(int64_t)r * n + c] = tile[i][tx];
+  }
+}
+
+// ---------------------------------------------------------------- committed grid
+// Per (row, storage sub-block): step dl and offset ml of the committed bytes,
+// written transposed [sub][row] (ef.py:87-127).
+__global__ void ef_grid_kernel(int ttype, const uint8_t* __restrict__ raw, int nrow, int n,
+                               float* __restrict__ dlT, float* __restrict__ mlT) {
+  const int nsub16 = n / 16;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int r = (int)(t % nrow);
+  const int s16 = (int)(t / nrow);  // sub-block index in units of 16 weights
+  if (s16 >= nsub16) return;
+  const int sb = s16 >> 4, k = s16 & 15;
+  float dl, ml = 0.0f;
+  if (ttype == CP_Q2_K) {
+    const uint8_t* b = raw + ((int64_t)r * (n / 256) + sb) * 84;
+    float d = half_value(b[80] | b[81] << 8), dm = half_value(b[82] | b[83] << 8);
+    dl = d * (float)(b[k] & 0xF);
+    ml = dm * (float)(b[k] >> 4);
+  } else if (ttype == CP_Q3_K) {
+    const uint8_t* b = raw + ((int64_t)r * (n / 256) + sb) * 110;
+    float d = half_value(b[108] | b[109] << 8);
+    const uint8_t* sc = b + 96;
+    int lo = (k < 8) ? (sc[k] & 0xF) : (sc[k - 8] >> 4);
+    int hi = (sc[8 + (k & 3)] >> (2 * (k >> 2))) & 3;
+    dl = d * (float)((lo | hi << 4) - 32);
+  } else if (ttype == CP_Q4_K) {
+    if (k & 1) return;  // 32-wide sub-blocks: one thread per pair of 16s
+    const uint8_t* b = raw + ((int64_t)r * (n / 256) + sb) * 144;
+    float d = half_value(b[0] | b[1] << 8), dm = half_value(b[2] | b[3] << 8);
+    const uint8_t* sc = b + 4;
+    int j = k >> 1, s, m;
+    if (j < 4) {
+      s = sc[j] & 63;
+      m = sc[j + 4] & 63;
+    } else {
+      s = (sc[j + 4] & 0xF) | (sc[j - 4] >> 6) << 4;
+      m = (sc[j + 4] >> 4) | (sc[j] >> 6) << 4;
+    }
+    dl = d * (float)s;
+    ml = dm * (float)m;
+    const int64_t o = (int64_t)(s16 >> 1) * nrow + r;
+    dlT[o] = dl;
+    mlT[o] = ml;
+    return;
+  } else {  // Q6_K
+    const uint8_t* b = raw + ((int64_t)r * (n / 256) + sb) * 210;
+    float d = half_value(b[208] | b[209] << 8);
+    dl = d * (float)(int8_t)b[192 + k];
+  }
+  const int64_t o = (int64_t)s16 * nrow + r;
+  dlT[o] = dl;
+  if (mlT) mlT[o] = ml;
+}
+
+// ---------------------------------------------------------------- repack
+// Rewrite the code bytes of committed superblocks from stored codes Lrow
+// [nrow][n] (row-major storage order), keeping the scale bytes (ef.py:130-176).
+// One thread per code byte of a superblock.
+__global__ void ef_repack_kernel(int ttype, const uint8_t* __restrict__ Lrow, int64_t NB,
+                                 uint8_t* __restrict__ raw) {
+  int lo_b, hi_b, bp;
+  switch (ttype) {
+    case CP_Q2_K: lo_b = 16; hi_b = 80; bp = 84; break;
+    case CP_Q3_K: lo_b = 0; hi_b = 96; bp = 110; break;
+    case CP_Q4_K: lo_b = 16; hi_b = 144; bp = 144; break;
+    default: lo_b = 0; hi_b = 192; bp = 210; break;
+  }
+  const int span = hi_b - lo_b;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t sb = t / span;
+  if (sb >= NB) return;
+  const int b = lo_b + (int)(t % span);
+  const uint8_t* c = Lrow + sb * 256;
+  uint32_t v;
+  if (ttype == CP_Q2_K) {
+    int k = b - 16, base = (k >> 5) * 128 + (k & 31);
+    v = c[base] | c[base + 32] << 2 | c[base + 64] << 4 | c[base + 96] << 6;
+  } else if (ttype == CP_Q3_K) {
+    if (b < 32) {
+      v = 0;
+      for (int j = 0; j < 8; ++j) v |= ((c[32 * j + b] >> 2) & 1u) << j;
+    } else {
+      int k = b - 32, base = (k >> 5) * 128 + (k & 31);
+      v = (c[base] & 3) | (c[base + 32] & 3) << 2 | (c[base + 64] & 3) << 4 | (c[base + 96] & 3) << 6;
+    }
+  } else if (ttype == CP_Q4_K) {
+    int k = b - 16, base = (k >> 5) * 64 + (k & 31);
+    v = (c[base] & 0xF) | (c[base + 32] & 0xF) << 4;
+  } else {
+    if (b < 128) {
+      int h = b >> 6, k = b & 63;
+      int base = h * 128 + (k & 31) + (k >= 32 ? 32 : 0);
+      v = (c[base] & 0xF) | (c[base + 64] & 0xF) << 4;
+    } else {
+      int k = b - 128, base = (k >> 5) * 128 + (k & 31);
+      v = (c[base] >> 4) | (c[base + 32] >> 4) << 2 | (c[base + 64] >> 4) << 4 | (c[base + 96] >> 4) << 6;
+    }
+  }
+  raw[sb * bp + b] = (uint8_t)v;
+}
+
+// ---------------------------------------------------------------- host driver
+
+static size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct EfLayout {
+  size_t WpT, E, WcurT, Wcur, LT, Lrow, dlT, mlT, inv, sbidx, end;
+};
+
+static EfLayout ef_layout(int64_t nrow, int64_t n, size_t base) {
+  EfLayout L;
+  const size_t w = (size_t)nrow * n;
+  size_t o = base;
+  L.WpT = o; o += a256(w * 4);
+  L.E = o; o += a256(w * 4);
+  L.WcurT = o; o += a256(w * 4);
+  L.Wcur = o; o += a256(w * 4);
+  L.LT = o; o += a256(w);
+  L.Lrow = o; o += a256(w);
+  L.dlT = o; o += a256((size_t)nrow * (n / 16) * 4);
+  L.mlT = o; o += a256((size_t)nrow * (n / 16) * 4);
+  L.inv = o; o += a256((size_t)n * 4);
+  L.sbidx = o; o += a256((size_t)n * 4);
+  L.end = o;
+  return L;
+}
+
+size_t ef_ws_bytes(const cp_ef_tensor* t, int count) {
+  size_t o = a256((size_t)count * sizeof(SweepTask));
+  for (int i = 0; i < count; ++i) o = ef_layout(t[i].nrow, t[i].n, o).end;
+  return o;
+}
+
+static void grid_range(int ttype, int* lo, int* hi, int* sub) {
+  switch (ttype) {
+    case CP_Q2_K: *lo = 0; *hi = 3; *sub = 16; break;
+    case CP_Q3_K: *lo = -4; *hi = 3; *sub = 16; break;
+    case CP_Q4_K: *lo = 0; *hi = 15; *sub = 32; break;
+    default: *lo = -32; *hi = 31; *sub = 16; break;
+  }
+}
+
+int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, void* ws,
+                    size_t ws_bytes, hipStream_t st) {
+  if (!ts || count <= 0) return set_error(CP_ERR_ARG, "no tensors");
+  if (n_iter < 1) return set_error(CP_ERR_ARG, "n_iter must be >= 1");
+  if (mode != CP_EF_EXACT) return set_error(CP_ERR_ARG, "unknown EF mode %d", mode);
+  for (int i = 0; i < count; ++i) {
+    const cp_ef_tensor& t = ts[i];
+    KqGeom g;
+    if (!kq_geom(t.ttype, &g)) return set_error(CP_ERR_TTYPE, "tensor %d: unsupported type %d", i, t.ttype);
+    if (t.nrow <= 0 || t.n <= 0 || t.n % 256 || t.nrow > (1 << 30) || t.n > (1 << 20))
+      return set_error(CP_ERR_SHAPE, "tensor %d: bad shape [%lld, %lld]", i, (long long)t.nrow, (long long)t.n);
+    if (!t.x || !t.U || !t.order || !t.raw) return set_error(CP_ERR_ARG, "tensor %d: null pointer", i);
+    if (!aligned(t.x, 16) || !aligned(t.raw, 4) || (t.qw && !aligned(t.qw, 16)) ||
+        (t.recon && !aligned(t.recon, 16)))
+      return set_error(CP_ERR_ALIGN, "tensor %d: misaligned buffer", i);
+  }
+  if (!ws || ws_bytes < ef_ws_bytes(ts, count))
+    return set_error(CP_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, ef_ws_bytes(ts, count));
+  if (!aligned(ws, 256)) return set_error(CP_ERR_ALIGN, "workspace needs 256-byte alignment");
+  char* base = (char*)ws;
+  std::vector<EfLayout> lay(count);
+  std::vector<SweepTask> tasks(count);
+  SweepTask* dtasks = (SweepTask*)base;
+  size_t o = a256((size_t)count * sizeof(SweepTask));
+  for (int i = 0; i < count; ++i) {
+    const cp_ef_tensor& t = ts[i];
+    lay[i] = ef_layout(t.nrow, t.n, o);
+    o = lay[i].end;
+    int lo, hi, sub;
+    grid_range(t.ttype, &lo, &hi, &sub);
+    const EfLayout& L = lay[i];
+    const bool affine = t.ttype == CP_Q2_K || t.ttype == CP_Q4_K;
+    tasks[i] = SweepTask{(const float*)(base + L.WpT), t.U, (const float*)(base + L.dlT),
+                         affine ? (const float*)(base + L.mlT) : nullptr,
+                         (const int*)(base + L.sbidx), (float*)(base + L.E),
+                         (float*)(base + L.WcurT), (uint8_t*)(base + L.LT),
+                         (int)t.nrow, (int)t.n, lo, hi};
+    ef_index_kernel<<<(unsigned)((t.n + 255) / 256), 256, 0, st>>>(t.order, (int)t.n, sub,
+                                                                    (int*)(base + L.inv),
+                                                                    (int*)(base + L.sbidx));
+    dim3 tg((unsigned)((t.n + 63) / 64), (unsigned)((t.nrow + 63) / 64));
+    ef_to_visit_kernel<float><<<tg, 256, 0, st>>>(t.x, (int)t.nrow, (int)t.n,
+                                                  (const int*)(base + L.inv), (float*)(base + L.WpT));
+  }
+  for (int c0 = 0; c0 < count; c0 += kTasksPerLaunch) {
+    const int cn = count - c0 < kTasksPerLaunch ? count - c0 : kTasksPerLaunch;
+    SweepBatch b;
+    for (int i = 0; i < cn; ++i) b.t[i] = tasks[c0 + i];
+    ef_tasks_store_kernel<<<1, 64, 0, st>>>(b, cn, dtasks + c0);
+  }
+  CP_LAUNCHED("EF setup");
+
+  for (int it = 0; it < n_iter; ++it) {
+    for (int i = 0; i < count; ++i) {
+      const cp_ef_tensor& t = ts[i];
+      const EfLayout& L = lay[i];
+      const float* src = it == 0 ? t.x : (const float*)(base + L.Wcur);
+      if (int s = kq_quantize(t.ttype, src, t.nrow, t.n, t.qw, t.raw, st)) return s;
+      const int64_t thr = t.nrow * (t.n / 16);
+      ef_grid_kernel<<<(unsigned)((thr + 255) / 256), 256, 0, st>>>(
+          t.ttype, t.raw, (int)t.nrow, (int)t.n, (float*)(base + L.dlT), (float*)(base + L.mlT));
+    }
+    CP_LAUNCHED("EF commit");
+    int rows = 0;
+    for (int i = 0; i < count; ++i) rows = tasks[i].nrow > rows ? tasks[i].nrow : rows;
+    ef_sweep_exact_kernel<BLK><<<dim3((unsigned)((rows + 255) / 256), (unsigned)count), 256, 0, st>>>(dtasks);
+    CP_LAUNCHED("EF sweep");
+    for (int i = 0; i < count; ++i) {
+      const cp_ef_tensor& t = ts[i];
+      const EfLayout& L = lay[i];
+      dim3 tg((unsigned)((t.n + 63) / 64), (unsigned)((t.nrow + 63) / 64));
+      ef_to_storage_kernel<uint8_t><<<tg, 256, 0, st>>>((const uint8_t*)(base + L.LT), (int)t.nrow,
+                                                        (int)t.n, (const int*)(base + L.inv),
+                                                        (uint8_t*)(base + L.Lrow));
+      KqGeom g;
+      kq_geom(t.ttype, &g);
+      const int span = t.ttype == CP_Q2_K ? 64 : t.ttype == CP_Q3_K ? 96 : t.ttype == CP_Q4_K ? 128 : 192;
+      const int64_t NB = t.nrow * (t.n / 256);
+      ef_repack_kernel<<<(unsigned)((NB * span + 255) / 256), 256, 0, st>>>(
+          t.ttype, (const uint8_t*)(base + L.Lrow), NB, t.raw);
+      if (it + 1 < n_iter)
+        ef_to_storage_kernel<float><<<tg, 256, 0, st>>>((const float*)(base + L.WcurT), (int)t.nrow,
+                                                        (int)t.n, (const int*)(base + L.inv),
+                                                        (float*)(base + L.Wcur));
+    }
+    CP_LAUNCHED("EF repack");
+  }
+  for (int i = 0; i < count; ++i)
+    if (ts[i].recon)
+      if (int s = kq_dequantize(ts[i].ttype, ts[i].raw, ts[i].nrow, ts[i].n, ts[i].recon, st)) return s;
+  return CP_OK;
+}
+
+}  // namespace cp
+
+extern "C" {
+
+size_t cp_ef_ws_bytes(const cp_ef_tensor* tensors, int count) {
+  if (!tensors || count <= 0) return 0;
+  return cp::ef_ws_bytes(tensors, count);
+}
+
+int cp_ef_encode_batch(const cp_ef_tensor* tensors, int count, int n_iter, int mode, void* ws,
+                       size_t ws_bytes, void* stream) {
+  cp::clear_error();
+  return cp::ef_encode_batch(tensors, count, n_iter, mode, ws, ws_bytes, (hipStream_t)stream);
+}
+
+int cp_ef_encode(int ttype, const float* x, int64_t nrow, int64_t n, const float* qw,
+                 const float* U, const int32_t* order, int n_iter, uint8_t* raw, float* recon,
+                 void* ws, size_t ws_bytes, void* stream) {
+  cp::clear_error();
+  cp_ef_tensor t{ttype, nrow, n, x, qw, U, order, raw, recon};
+  return cp::ef_encode_batch(&t, 1, n_iter, CP_EF_EXACT, ws, ws_bytes, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,163 @@
+"""GPTQ-style error feedback into committed k-quant containers, on the GPU.
+
+Mirrors the encoder core of coldpress/ef.py (the reference's numpy backend):
+
+  cholesky_inv_upper(H, damp=0.01, _max_tries=6)      coldpress/ef.py:46-84
+  ef_encode(x, ttype, qw, H, n_iter=2, damp=0.01,
+            act_order=True)                            coldpress/ef.py:179-218
+
+plus the batched form the encode stage uses to run every tensor of a model in
+one pass (``ef_encode_many``): tensors that share an input Hessian (q/k/v,
+gate/up) share one factorization.
+
+numpy inputs give numpy outputs; torch CUDA inputs keep everything on the device.
+"""
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+from .kquant import BYTES_PER_SB, QK_K
+
+
+def _h_dtype(t):
+    if t.dtype == torch.float64:
+        return 1
+    if t.dtype == torch.float32:
+        return 0
+    raise TypeError(f"H must be float32 or float64, got {t.dtype}")
+
+
+def act_order_dev(H, enabled=True):
+    """Visiting order of the columns: descending diag(H), ties by index (ef.py:187).
+    H: [n, n] or [batch, n, n] float32/float64 CUDA tensor. Returns int32 [.., n]."""
+    lib = _lib.load()
+    batch = 1 if H.dim() == 2 else H.shape[0]
+    n = H.shape[-1]
+    if not enabled:
+        o = torch.arange(n, dtype=torch.int32, device=H.device)
+        return o if H.dim() == 2 else o.expand(batch, n).contiguous()
+    order = torch.empty(H.shape[:-1], dtype=torch.int32, device=H.device)
+    _lib.check(lib.cp_act_order(_lib.ptr(H), _h_dtype(H), n, batch, _lib.ptr(order),
+                                _lib.stream_ptr()))
+    return order
+
+
+def factor_dev(H, order=None, damp=0.01, max_tries=6, out_dtype=torch.float32):
+    """Upper U with U^T U = inv(Hp + lambda I), Hp = H[order][:, order], on the device.
+
+    H: [n, n] or [batch, n, n] CUDA tensor (float32/float64, contiguous).
+    Returns (U [.., n, n] of out_dtype, damp actually used per matrix)."""
+    lib = _lib.load()
+    squeeze = H.dim() == 2
+    Hb = H.unsqueeze(0) if squeeze else H
+    batch, n = Hb.shape[0], Hb.shape[-1]
+    if order is not None:
+        order = order.reshape(batch, n).to(torch.int32).contiguous()
+    U = torch.empty((batch, n, n), dtype=out_dtype, device=H.device)
+    ws = _lib.workspace(lib.cp_chol_ws_bytes(n, batch), H.device)
+    used = (ctypes.c_double * batch)()
+    st = lib.cp_chol_inv_upper(_lib.ptr(Hb), _h_dtype(Hb), n, batch, _lib.ptr(order), float(damp),
+                               int(max_tries), _lib.ptr(U), 1 if out_dtype == torch.float64 else 0,
+                               ctypes.cast(used, ctypes.c_void_p), _lib.ptr(ws), ws.numel(),
+                               _lib.stream_ptr())
+    _lib.check(st)
+    return (U[0] if squeeze else U), list(used)
+
+
+def cholesky_inv_upper(H, damp=0.01, _max_tries=6):
+    """U = chol(inv(H + lambda I), upper), float64 (coldpress/ef.py:46-84).
+
+    lambda = damp * mean(diag H) + 1e-8; escalates damp x10 on failure, up to
+    _max_tries attempts, then raises np.linalg.LinAlgError."""
+    Hd, host = _lib.to_device(H, torch.float64)
+    U, _ = factor_dev(Hd, None, damp, _max_tries, out_dtype=torch.float64)
+    return np.ascontiguousarray(_lib.to_host(U)) if host else U
+
+
+def _ws_for(tensors):
+    lib = _lib.load()
+    arr = (_lib.EfTensor * len(tensors))(*tensors)
+    return arr, lib.cp_ef_ws_bytes(arr, len(tensors))
+
+
+def ef_encode_dev(items, n_iter=2, mode=_lib.CP_EF_EXACT):
+    """Batched EF on device tensors.
+
+    items: list of dicts with keys ttype, x [nrow, n] f32, qw [n] f32 or None,
+    U [n, n] f32 (visiting order), order [n] int32, and optional ``recon`` flag.
+    Returns a list of (raw uint8 [nrow, row_bytes], recon f32 or None)."""
+    lib = _lib.load()
+    keep, structs, outs = [], [], []
+    for it in items:
+        tt = it["ttype"]
+        x = it["x"]
+        nrow, n = x.shape
+        raw = torch.empty((nrow, (n // QK_K) * BYTES_PER_SB[tt]), dtype=torch.uint8, device=x.device)
+        rec = (torch.empty((nrow, n), dtype=torch.float32, device=x.device)
+               if it.get("recon", True) else None)
+        qw = it.get("qw")
+        keep += [x, qw, it["U"], it["order"], raw, rec]
+        structs.append(_lib.EfTensor(_lib.TTYPE[tt], nrow, n, x.data_ptr(),
+                                     qw.data_ptr() if qw is not None else None,
+                                     it["U"].data_ptr(), it["order"].data_ptr(), raw.data_ptr(),
+                                     rec.data_ptr() if rec is not None else None))
+        outs.append((raw, rec))
+    arr, nbytes = _ws_for(structs)
+    ws = _lib.workspace(nbytes, items[0]["x"].device)
+    st = lib.cp_ef_encode_batch(arr, len(structs), int(n_iter), int(mode), _lib.ptr(ws), ws.numel(),
+                                _lib.stream_ptr())
+    _lib.check(st)
+    return outs
+
+
+def ef_encode(x, ttype, qw, H, n_iter=2, damp=0.01, act_order=True):
+    """GPTQ error feedback into committed k-quant containers (coldpress/ef.py:179-218).
+
+    x: [nrow, n] f32; qw: imatrix means [n] or None; H: [n, n] (X^T X).
+    Returns (raw bytes [nrow, row_bytes], recon [nrow, n])."""
+    if ttype not in BYTES_PER_SB:
+        raise ValueError(ttype)
+    xd, host = _lib.to_device(x, torch.float32)
+    Hd, _ = _lib.to_device(H, torch.float64 if (isinstance(H, np.ndarray) and H.dtype == np.float64)
+                           or (isinstance(H, torch.Tensor) and H.dtype == torch.float64)
+                           else torch.float32)
+    qd = _lib.to_device(qw, torch.float32)[0].reshape(-1) if qw is not None else None
+    order = act_order_dev(Hd, act_order)
+    U, _ = factor_dev(Hd, order, damp)
+    (raw, rec), = ef_encode_dev([{"ttype": ttype, "x": xd, "qw": qd, "U": U, "order": order}],
+                                n_iter)
+    if host:
+        return _lib.to_host(raw), _lib.to_host(rec)
+    return raw, rec
+
+
+def ef_encode_many(tensors, n_iter=2, damp=0.01, act_order=True, mode=_lib.CP_EF_EXACT):
+    """EF-encode many tensors in one batched pass.
+
+    tensors: list of dicts {name, ttype, x (CUDA f32), qw (CUDA f32 or None),
+    H (CUDA f32/f64 [n, n])}. Tensors whose ``H`` is the same object share one
+    act order and one factorization (done batched per matrix size).
+    Returns {name: (raw, recon)}."""
+    # distinct Hessians, grouped by size for batched factorization
+    hs = {}
+    for t in tensors:
+        hs.setdefault(id(t["H"]), t["H"])
+    by_n = {}
+    for key, H in hs.items():
+        by_n.setdefault((H.shape[-1], H.dtype), []).append(key)
+    factor = {}
+    for (n, _dt), keys in by_n.items():
+        Hb = torch.stack([hs[k] for k in keys]) if len(keys) > 1 else hs[keys[0]].unsqueeze(0)
+        order = act_order_dev(Hb.contiguous(), act_order)
+        U, _ = factor_dev(Hb.contiguous(), order, damp)
+        for i, k in enumerate(keys):
+            factor[k] = (U[i], order[i])
+    items = []
+    for t in tensors:
+        U, order = factor[id(t["H"])]
+        items.append({"ttype": t["ttype"], "x": t["x"], "qw": t.get("qw"), "U": U,
+                      "order": order, "recon": t.get("recon", True)})
+    outs = ef_encode_dev(items, n_iter, mode)
+    return {t["name"]: o for t, o in zip(tensors, outs)}

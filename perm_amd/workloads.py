@@ -1,0 +1,69 @@
+"""Seeded synthetic workloads for the encoder path (weights, activations, Hessians).
+
+Shapes follow the reference's target models; there is no network, so weights
+are random-init and activations synthetic, with the statistics each workload
+names. The draw order of every generator is fixed: changing it changes the
+workload.
+"""
+import numpy as np
+
+F32 = np.float32
+
+# Qwen3-0.6B linear layers: (name, out_features = rows, in_features = n, Hessian family)
+QWEN3_06B_LAYER = [
+    ("attn_q", 2048, 1024, "qkv_in"),
+    ("attn_k", 1024, 1024, "qkv_in"),
+    ("attn_v", 1024, 1024, "qkv_in"),
+    ("attn_output", 1024, 2048, "o_in"),
+    ("ffn_gate", 3072, 1024, "gateup_in"),
+    ("ffn_up", 3072, 1024, "gateup_in"),
+    ("ffn_down", 1024, 3072, "down_in"),
+]
+QWEN3_06B_FAMILIES = {"qkv_in": 1024, "o_in": 2048, "gateup_in": 1024, "down_in": 3072}
+QWEN3_06B_LAYERS = 28
+
+
+def single_linear(seed=0, nrow=1024, n=1024, n_act=8192, outlier_frac=0.01, outlier_gain=20.0):
+    """One synthetic Linear on the reference's CPU path.
+
+    W [nrow, n] = N(0, 0.02^2) times a per-row log-normal(sigma 0.5) scale;
+    X [n_act, n] = N(0, 1) times per-channel log-normal(sigma 1) scales, with
+    floor(outlier_frac * n) channels (rng.choice, without replacement) x outlier_gain;
+    H = X^T X / n_act in float64. Returns (W f32, X f32, H f64)."""
+    rng = np.random.default_rng(seed)
+    W = rng.normal(0.0, 0.02, size=(nrow, n)) * np.exp(rng.normal(0.0, 0.5, size=(nrow, 1)))
+    scale = np.exp(rng.normal(0.0, 1.0, size=n))
+    out = rng.choice(n, int(outlier_frac * n), replace=False)
+    scale[out] *= outlier_gain
+    X = (rng.standard_normal((n_act, n)) * scale).astype(F32)
+    Xd = X.astype(np.float64)
+    H = Xd.T @ Xd / n_act
+    return W.astype(F32), X, H
+
+
+def student_t_activations(n_rows, d, nu=4.0, seed=0, device="cuda", dtype=None):
+    """Heavy-tailed activations on the device: Student-t(nu) times per-channel
+    log-normal(sigma 1) scales, as bfloat16 by default. Generated with torch's
+    device RNG (seeded) so the 65536-row batches never cross PCIe."""
+    import torch
+    dtype = dtype or torch.bfloat16
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    z = torch.randn((n_rows, d), generator=g, device=device)
+    # chi-square(nu) / nu from nu standard normals squared (nu = 4)
+    chi = torch.zeros((n_rows, 1), device=device)
+    for _ in range(int(nu)):
+        chi += torch.randn((n_rows, 1), generator=g, device=device) ** 2
+    t = z / torch.sqrt(chi / nu)
+    scale = torch.exp(torch.randn((d,), generator=g, device=device))
+    return (t * scale).to(dtype)
+
+
+def qwen3_layer_weights(layer, seed=0, device="cuda"):
+    """Random-init fp32 weights N(0, 0.02^2) for one Qwen3-0.6B decoder layer:
+    {name: [rows, n]} on the device."""
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed(seed * 1000 + layer)
+    return {name: torch.randn((rows, n), generator=g, device=device) * 0.02
+            for name, rows, n, _fam in QWEN3_06B_LAYER}

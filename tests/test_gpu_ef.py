@@ -1,0 +1,186 @@
+"""GPU EF path parity: act order, the fp64 inverse-Hessian factor, and the EF
+sweep (bit-exact against the oracle when both use the same factor; within the
+code-agreement and H-weighted-error gates when the GPU computes its own)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import correlated_hessian, heavy_tailed
+from oracle import ef_oracle as E
+from oracle import kquant_oracle as K
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+TYPES = ["Q2_K", "Q3_K", "Q4_K", "Q6_K"]
+
+
+@pytest.fixture(scope="module")
+def ef():
+    from perm_amd import ef as gef
+    return gef
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _spectrum_matrix(n, eig, seed=0):
+    rng = np.random.default_rng(seed)
+    Q, _ = np.linalg.qr(rng.standard_normal((n, n)))
+    M = (Q * eig) @ Q.T
+    return (M + M.T) / 2
+
+
+def test_act_order_is_stable_descending(ef):
+    rng = np.random.default_rng(0)
+    d = rng.standard_normal(1000)
+    d[::7] = 0.5                                    # ties
+    H = np.diag(d)
+    got = ef.act_order_dev(torch.from_numpy(H).cuda()).cpu().numpy()
+    assert np.array_equal(got, np.argsort(-d, kind="stable"))
+
+
+@pytest.mark.parametrize("n", [96, 200, 256, 1024])
+def test_factor_matches_closed_form(ef, n):
+    _say(f"factor n={n}")
+    H = correlated_hessian(n, 4 * n, seed=n)
+    U = ef.cholesky_inv_upper(H, 0.01)
+    U_ref = E.inv_upper_factor(H, 0.01)
+    assert U.dtype == np.float64 and np.array_equal(U, np.triu(U))
+    rel = np.abs(U - U_ref).max() / np.abs(U_ref).max()
+    assert rel < 1e-11, rel
+    Hd = H + (0.01 * np.mean(np.diag(H)) + 1e-8) * np.eye(n)
+    assert np.abs(U.T @ U @ Hd - np.eye(n)).max() < 1e-9
+
+
+def test_factor_with_order_and_f32_output(ef):
+    n = 512
+    H = correlated_hessian(n, 2048, seed=3)
+    Hd = torch.from_numpy(H).cuda()
+    order = ef.act_order_dev(Hd)
+    U, used = ef.factor_dev(Hd, order, 0.01)
+    o = order.cpu().numpy()
+    U_ref = E.inv_upper_factor(H[np.ix_(o, o)], 0.01).astype(F32)
+    assert used == [0.01]
+    Ug = U.cpu().numpy()
+    assert (Ug != U_ref).mean() < 0.01                      # f32 cast: rare 1-ulp differences
+    assert np.abs(Ug - U_ref).max() <= 4 * np.spacing(np.abs(U_ref).max())
+
+
+def test_factor_batched_equals_single(ef):
+    Hs = [correlated_hessian(256, 1024, seed=s) for s in range(3)]
+    Hb = torch.from_numpy(np.stack(Hs)).cuda()
+    order = ef.act_order_dev(Hb)
+    Ub, _ = ef.factor_dev(Hb, order, 0.01)
+    for i in range(3):
+        Ui, _ = ef.factor_dev(Hb[i].contiguous(), order[i], 0.01)
+        assert torch.equal(Ub[i], Ui)
+
+
+def test_factor_escalates_like_reference(ef, capfd):
+    n = 256
+    eig = np.linspace(1.0, 100.0, n)
+    eig[0] = -2.0
+    H = _spectrum_matrix(n, eig, seed=1)
+    Hd = torch.from_numpy(H).cuda()
+    U, used = ef.factor_dev(Hd, None, 0.01, out_dtype=torch.float64)
+    U = U.cpu().numpy()
+    assert used[0] > 0.01 and np.all(np.isfinite(U)) and np.array_equal(U, np.triu(U))
+    # the oracle escalates to the same damp and lands on the same factor
+    U_ref = E.inv_upper_factor(H, 0.01, log=False)
+    assert np.abs(U - U_ref).max() / np.abs(U_ref).max() < 1e-9
+
+
+def test_factor_gives_up(ef):
+    H = -np.eye(64) * 1e6
+    H[0, 0] = 1.0
+    with pytest.raises(np.linalg.LinAlgError, match="not positive definite"):
+        ef.cholesky_inv_upper(H, 0.01, _max_tries=3)
+
+
+def _run_exact(ef, W, tt, qw, H, n_iter=2):
+    """GPU EF with the oracle's own float32 factor and order: must be bit-exact."""
+    order = E.act_order(H, stable=True)
+    U = E.inv_upper_factor(H[np.ix_(order, order)], 0.01).astype(F32)
+    want_raw, want_rec = E.ef_encode(W, tt, qw, H, n_iter=n_iter, U=U, stable_order=True)
+    item = {"ttype": tt, "x": torch.from_numpy(W).cuda(),
+            "qw": torch.from_numpy(qw).cuda() if qw is not None else None,
+            "U": torch.from_numpy(U).cuda(), "order": torch.from_numpy(order.astype(np.int32)).cuda()}
+    (raw, rec), = ef.ef_encode_dev([item], n_iter)
+    return raw.cpu().numpy(), rec.cpu().numpy(), want_raw, want_rec
+
+
+@pytest.mark.parametrize("tt", TYPES)
+@pytest.mark.parametrize("weighted", [False, True])
+def test_sweep_bit_exact_vs_oracle(ef, tt, weighted):
+    nrow, n = 70, 512                                   # 70 rows: a partial stripe
+    _say(f"exact sweep {tt} weighted={weighted}")
+    W = heavy_tailed(nrow, n, seed=17)
+    H = correlated_hessian(n, 4096, seed=5)
+    qw = (np.diag(H) / 4096).astype(F32) if weighted else None
+    raw, rec, want_raw, want_rec = _run_exact(ef, W, tt, qw, H)
+    bad = np.nonzero((raw != want_raw).any(1))[0]
+    assert bad.size == 0, f"rows {bad[:10]} differ"
+    assert np.array_equal(rec, want_rec)
+
+
+@pytest.mark.parametrize("n_iter", [1, 3])
+def test_sweep_bit_exact_iterations(ef, n_iter):
+    W = heavy_tailed(64, 768, seed=3)
+    H = correlated_hessian(768, 2048, seed=6)
+    qw = (np.diag(H) / 2048).astype(F32)
+    raw, _, want_raw, _ = _run_exact(ef, W, "Q2_K", qw, H, n_iter=n_iter)
+    assert np.array_equal(raw, want_raw)
+
+
+def _codes(tt, raw, nrow, n):
+    b = raw.reshape(-1, K.BYTES_PER_SB[tt])
+    if tt == "Q2_K":
+        return K.unpack_2bit(b[:, 16:80]).reshape(nrow, n)
+    if tt == "Q3_K":
+        return K.unpack_q3_codes(b[:, 0:32], b[:, 32:96]).reshape(nrow, n)
+    if tt == "Q4_K":
+        return K.unpack_nibbles(b[:, 16:144]).reshape(nrow, n)
+    return K.unpack_q6_codes(b[:, 0:128], b[:, 128:192]).reshape(nrow, n)
+
+
+@pytest.mark.parametrize("tt", TYPES)
+def test_full_gpu_path_within_gates(ef, tt):
+    """GPU order + fp64 factor + sweep against the reference-equivalent oracle:
+    >= 99.9 % identical codes, tr(dW H dW^T) within 1e-3 relative."""
+    from perm_amd.workloads import single_linear
+    _say(f"full path {tt}")
+    W, _X, H = single_linear(seed=0, nrow=192, n=1024, n_act=8192)
+    qw = np.diag(H).astype(F32)
+    raw, rec = ef.ef_encode(W, tt, qw, H)
+    want_raw, want_rec = E.ef_encode(W, tt, qw, H, stable_order=True)
+    agree = (_codes(tt, raw, *W.shape) == _codes(tt, want_raw, *W.shape)).mean()
+    e_gpu, e_ref = E.h_weighted_err(W, rec, H), E.h_weighted_err(W, want_rec, H)
+    _say(f"  codes agree {agree:.6f}, err rel diff {abs(e_gpu - e_ref) / e_ref:.2e}")
+    assert agree >= 0.999
+    assert abs(e_gpu - e_ref) / e_ref < 1e-3
+
+
+def test_ef_beats_rtn_on_gpu(ef):
+    """test_ef_synthetic.py:30-46 on the GPU path."""
+    n, nrow, T = 512, 24, 4096
+    rng = np.random.default_rng(101)
+    W = (rng.standard_normal((nrow, n)) ** 3).astype(F32)
+    H = correlated_hessian(n, T, seed=0)
+    qw = (np.diag(H) / T).astype(F32)
+    rtn = K.roundtrip(W, "Q2_K", qw)
+    _, rec = ef.ef_encode(W, "Q2_K", qw, H)
+    assert E.h_weighted_err(W, rec, H) < 0.97 * E.h_weighted_err(W, rtn, H)
+
+
+def test_many_shares_factor_and_matches_single(ef):
+    n = 512
+    H = torch.from_numpy(correlated_hessian(n, 2048, seed=9)).cuda()
+    qw = torch.diagonal(H).float().contiguous() / 2048
+    ws = {nm: torch.from_numpy(heavy_tailed(r, n, seed=i)).cuda()
+          for i, (nm, r) in enumerate([("a", 64), ("b", 128), ("c", 96)])}
+    tens = [{"name": nm, "ttype": "Q2_K", "x": x, "qw": qw, "H": H} for nm, x in ws.items()]
+    out = ef.ef_encode_many(tens)
+    for nm, x in ws.items():
+        raw1, rec1 = ef.ef_encode(x, "Q2_K", qw, H)
+        assert torch.equal(out[nm][0], raw1) and torch.equal(out[nm][1], rec1)
