@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""EF k-quant encode (Q2_K) + Hessian X^T X throughput on one MI355X.
+
+Workload (one step): the Qwen3-0.6B-shaped layer set, random-init, 28 decoder
+layers x 7 linear tensors -- q 2048x1024, k/v 1024x1024, o 1024x2048,
+gate/up 3072x1024, down 1024x3072: 440,401,920 weights.
+  1. Hessians: per layer the 4 distinct input Hessians (qkv_in d=1024,
+     o_in 2048, gateup_in 1024, down_in 3072), each H = X^T X over 65536
+     synthetic bf16 activation rows (Student-t nu=4, per-channel log-normal
+     scales), float32 accumulation on MFMA.
+  2. EF encode: act order + damped fp64 inverse-Hessian factor per distinct H,
+     then GPTQ error feedback (2 iterations) of all 196 tensors into Q2_K with
+     qw = diag(H)/N (imatrix-style channel means), and the final decode.
+Activations and weights are generated on the device before the timed region.
+
+value = EF Mweights/s = 440.4e6 / (EF time per step); the Hessian TFLOP/s
+(2*N*d^2 per Hessian) is reported beside it. cpu_baseline: the numpy oracle
+(a port of the reference's ef.py / kquant.py) on a row subsample of one layer,
+extrapolated to the full workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "EF k-quant encode Mweights/s (Q2_K) + Hessian X^T·X TFLOP/s, 1 GPU"
+ROWS = 65536
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_FP32_TFLOPS = 157.3
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_workload(layers, device):
+    import torch
+    from perm_amd import workloads as wl
+    X, W = [], []
+    for l in range(layers):
+        X.append({fam: wl.student_t_activations(ROWS, d, nu=4.0, seed=1000 * l + i, device=device)
+                  for i, (fam, d) in enumerate(wl.QWEN3_06B_FAMILIES.items())})
+        W.append(wl.qwen3_layer_weights(l, seed=0, device=device))
+        if (l + 1) % 7 == 0 or l + 1 == layers:
+            log(f"generated layer {l + 1}/{layers}")
+    # Hessian accumulators, batched by matrix size (qkv_in and gateup_in share d=1024)
+    H = {1024: torch.zeros((2 * layers, 1024, 1024), device=device),
+         2048: torch.zeros((layers, 2048, 2048), device=device),
+         3072: torch.zeros((layers, 3072, 3072), device=device)}
+    slot = {}
+    for l in range(layers):
+        slot[(l, "qkv_in")] = (1024, l)
+        slot[(l, "gateup_in")] = (1024, layers + l)
+        slot[(l, "o_in")] = (2048, l)
+        slot[(l, "down_in")] = (3072, l)
+    torch.cuda.synchronize()
+    return X, W, H, slot
+
+
+def hessian_phase(X, H, slot):
+    from perm_amd.hessians import xtx_accumulate
+    for Hb in H.values():
+        Hb.zero_()
+    for l, fams in enumerate(X):
+        for fam, Xf in fams.items():
+            d, i = slot[(l, fam)]
+            xtx_accumulate(Xf, H[d][i])
+
+
+def ef_phase(W, H, slot, layers, mode):
+    from perm_amd import ef as gef
+    from perm_amd import workloads as wl
+    factor = {}
+    for d, Hb in H.items():
+        order = gef.act_order_dev(Hb)
+        U, _ = gef.factor_dev(Hb, order, 0.01)
+        factor[d] = (order, U)
+    items = []
+    for l in range(layers):
+        for name, _rows, _n, fam in wl.QWEN3_06B_LAYER:
+            d, i = slot[(l, fam)]
+            order, U = factor[d]
+            qw = H[d][i].diagonal() / float(ROWS)
+            items.append({"ttype": "Q2_K", "x": W[l][name], "qw": qw.contiguous(), "U": U[i],
+                          "order": order[i], "recon": True})
+    return gef.ef_encode_dev(items, n_iter=2, mode=mode)
+
+
+def cpu_baseline(W, H, slot, layers, total_weights):
+    """Time the numpy oracle (port of coldpress/ef.py:46-218 + kquant.py) on
+    64- and 256-row subsamples of layer 0's 7 tensors, with one factorization
+    per tensor as the reference does (ef.py:189), and extrapolate:
+    T(tensor) = T_factor + a + b * nrow, times 28 identical layers."""
+    import numpy as np
+    from oracle import ef_oracle as E
+    from perm_amd import workloads as wl
+    try:
+        from threadpoolctl import threadpool_info
+        blas_threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:  # threadpoolctl missing or unreadable
+        blas_threads = 1
+    t_total = 0.0
+    t_spent = 0.0
+    per = []
+    for name, rows, n, fam in wl.QWEN3_06B_LAYER:
+        d, i = slot[(0, fam)]
+        Hn = H[d][i].double().cpu().numpy()
+        qw = (np.diag(Hn) / ROWS).astype(np.float32)
+        Wn = W[0][name].cpu().numpy()
+        t0 = time.perf_counter()
+        order = E.act_order(Hn)
+        U = E.inv_upper_factor(Hn[np.ix_(order, order)], 0.01).astype(np.float32)
+        t_fact = time.perf_counter() - t0
+        ts = {}
+        for r in (64, 256):
+            t0 = time.perf_counter()
+            E.ef_encode(Wn[:r], "Q2_K", qw, Hn, U=U)
+            ts[r] = time.perf_counter() - t0
+        b = (ts[256] - ts[64]) / 192.0
+        a = ts[64] - 64 * b
+        t_tensor = t_fact + a + b * rows
+        per.append((name, t_fact, ts[64], ts[256], t_tensor))
+        t_total += t_tensor
+        t_spent += t_fact + ts[64] + ts[256]
+        log(f"cpu {name}: factor {t_fact:.2f}s ef64 {ts[64]:.2f}s ef256 {ts[256]:.2f}s "
+            f"-> full tensor {t_tensor:.1f}s")
+    t_total *= layers
+    return {
+        "value": total_weights / t_total / 1e6,
+        "unit": "Mweights/s",
+        "cores": int(blas_threads),
+        "kind": "port",
+        "sample": (f"numpy oracle (port of ef.py/kquant.py) on layer 0's 7 tensors at 64 and 256 "
+                   f"rows + one factorization per tensor ({t_spent:.1f} s of CPU work); "
+                   f"extrapolated linearly in rows to all {layers} layers "
+                   f"(est. {t_total:.0f} s for the full encode); sweep and codec are "
+                   f"single-threaded numpy, the factorization uses {blas_threads} BLAS threads"),
+        "host_cpus": os.cpu_count(),
+        "affinity_cpus": len(os.sched_getaffinity(0)),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--layers", type=int, default=28,
+                    help="decoder layers (28 = the full workload; fewer only for quick checks)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        msg = (f"bench.py runs on one GPU only (got --gpus {args.gpus}); the encoder path "
+               f"shards by tensor / row stripe with no exchange, see DESIGN.md")
+        print(msg, file=sys.stderr)
+        print(json.dumps({"metric": METRIC, "error": msg}))
+        sys.exit(2)
+
+    import torch
+    from perm_amd import _lib
+    from perm_amd import workloads as wl
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a GPU")
+    lib = _lib.load()
+    dev = "cuda"
+    layers = args.layers
+    total_weights = layers * sum(r * n for _, r, n, _ in wl.QWEN3_06B_LAYER)
+    hess_flops = layers * sum(2.0 * ROWS * d * d for d in wl.QWEN3_06B_FAMILIES.values())
+    ef_flops = 2 * layers * sum(r * n * (n - 1) for _, r, n, _ in wl.QWEN3_06B_LAYER)
+    log(f"building workload: {layers} layers, {total_weights} weights")
+    X, W, H, slot = build_workload(layers, dev)
+
+    def step(profile):
+        hs, he, ee = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        hs.record()
+        hessian_phase(X, H, slot)
+        he.record()
+        lib.cp_ef_profile(1 if profile else 0)
+        ef_phase(W, H, slot, layers, _lib.CP_EF_EXACT)
+        ee.record()
+        lib.cp_ef_profile(0)
+        return hs, he, ee
+
+    for i in range(args.warmup):
+        step(False)
+        torch.cuda.synchronize()
+        log(f"warmup {i + 1}/{args.warmup} done")
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    marks, phases = [], []
+    import ctypes
+    for i in range(args.steps):
+        marks.append(step(True))
+        buf = (ctypes.c_float * 5)()
+        lib.cp_ef_phase_ms(ctypes.cast(buf, ctypes.c_void_p), 5)
+        phases.append(list(buf))
+        log(f"step {i + 1}/{args.steps} done")
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    hess_ms = sum(hs.elapsed_time(he) for hs, he, _ in marks) / args.steps
+    ef_ms = sum(he.elapsed_time(ee) for _, he, ee in marks) / args.steps
+    ph = [sum(p[k] for p in phases) / args.steps for k in range(5)]
+    ms_per_step = wall * 1e3 / args.steps
+    ef_mw = total_weights / (ef_ms * 1e-3) / 1e6
+    hess_tflops = hess_flops / (hess_ms * 1e-3) / 1e12
+
+    # dominant kernel: the Hessian MFMA kernel (one launch per Hessian) or the EF sweep
+    hess_launches = 4 * layers
+    sweep_launches = 2
+    if hess_ms >= ph[2]:
+        avg_ms = hess_ms / hess_launches
+        flops_per_launch = hess_flops / hess_launches
+        ach = flops_per_launch / (avg_ms * 1e-3) / 1e12
+        roof = {"kernel": "hess_bf16_kernel", "bound": "mfma", "achieved": ach,
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_BF16_TFLOPS,
+                "traffic": None, "avg_launch_ms": avg_ms, "launches_per_step": hess_launches}
+    else:
+        avg_ms = ph[2] / sweep_launches
+        flops_per_launch = ef_flops / sweep_launches
+        ach = flops_per_launch / (avg_ms * 1e-3) / 1e12
+        roof = {"kernel": "ef_sweep_exact_kernel", "bound": "mfma", "achieved": ach,
+                "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_FP32_TFLOPS,
+                "traffic": None, "avg_launch_ms": avg_ms, "launches_per_step": sweep_launches}
+
+    result = {
+        "metric": METRIC,
+        "value": ef_mw,
+        "unit": "Mweights/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (random-init weights, Student-t bf16 activations; generated on device)",
+        "config": {"workload": f"qwen3-0.6b-shaped {layers}-layer Q2_K EF + Hessians",
+                   "layers": layers, "tensors": 7 * layers, "weights": total_weights,
+                   "hessians": 4 * layers, "hessian_rows": ROWS, "activations": "bf16",
+                   "container": "Q2_K", "qw": "diag(H)/N", "n_iter": 2, "damp": 0.01,
+                   "act_order": True, "ef_mode": "exact"},
+        "ef": {"ms": ef_ms, "mweights_per_s": ef_mw, "flops_update": ef_flops,
+               "phase_ms": {"factor_and_setup": ef_ms - sum(ph), "setup": ph[0],
+                            "commit": ph[1], "sweep": ph[2], "repack": ph[3], "decode": ph[4]}},
+        "hessian": {"ms": hess_ms, "tflops": hess_tflops, "flops": hess_flops,
+                    "frac_of_bf16_peak": hess_tflops / PEAK_BF16_TFLOPS},
+        "roofline": roof,
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline (numpy oracle on a layer-0 row subsample)")
+        result["cpu_baseline"] = cpu_baseline(W, H, slot, layers, total_weights)
+        result["gpu_over_cpu"] = ef_mw / result["cpu_baseline"]["value"]
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

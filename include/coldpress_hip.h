@@ -117,6 +117,26 @@ int cp_ef_encode(int ttype, const float* x, int64_t nrow, int64_t n, const float
                  const float* U, const int32_t* order, int n_iter, uint8_t* raw, float* recon,
                  void* ws, size_t ws_bytes, void* stream);
 
+/* Per-thread switch for phase timing of EF calls (hipEvents recorded on the
+ * call's stream; no synchronization inside the call). No counterpart in the
+ * reference, which times whole tensors with time.time() (coldpress/ef.py:277, 304). */
+void cp_ef_profile(int enable);
+
+/* Milliseconds spent by the calling thread's last profiled EF call in each
+ * phase: out[0] setup (index, gather), out[1] commit (encode + grid decode),
+ * out[2] sweep, out[3] repack (+ target scatter), out[4] final decode.
+ * Waits for the call's last event. Returns the number of phases written. */
+int cp_ef_phase_ms(float* out, int nphase);
+
+/* ---- Hessian accumulation (coldpress/hessians.py:137-154) ---- */
+
+/* H [d, d] float32 += X^T X for X [N, d] row-major (x_dtype 0 = float32,
+ * 1 = bfloat16 with d % 8 == 0). Float32 accumulation on MFMA. Replaces the
+ * forward hook's ``acc += (x.float().T @ x)`` (coldpress/hessians.py:142-152),
+ * with the accumulator kept on the device. The summation order over rows is
+ * not fixed (split-K partials are added with float32 atomics). */
+int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, float* H, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -304,6 +304,36 @@ static void grid_range(int ttype, int* lo, int* hi, int* sub) {
   }
 }
 
+// Optional per-phase timing of an EF call with hipEvents on its stream
+// (cp_ef_profile / cp_ef_phase_ms): setup, commit, sweep, repack, decode.
+struct PhaseClock {
+  bool on = false;
+  std::vector<hipEvent_t> ev;
+  std::vector<int> label;  // label[i]: phase of the interval ending at ev[i]
+  int used = 0;
+  hipError_t start(hipStream_t st) {
+    used = 0;
+    label.clear();
+    return mark(-1, st);
+  }
+  hipError_t mark(int phase, hipStream_t st) {
+    if (used == (int)ev.size()) {
+      hipEvent_t e;
+      hipError_t r = hipEventCreate(&e);
+      if (r != hipSuccess) return r;
+      ev.push_back(e);
+    }
+    label.push_back(phase);
+    return hipEventRecord(ev[used++], st);
+  }
+};
+static thread_local PhaseClock g_clock;
+
+#define CP_PHASE(p)                                                   \
+  do {                                                                \
+    if (g_clock.on) CP_HIP(p < 0 ? g_clock.start(st) : g_clock.mark(p, st)); \
+  } while (0)
+
 int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, void* ws,
                     size_t ws_bytes, hipStream_t st) {
   if (!ts || count <= 0) return set_error(CP_ERR_ARG, "no tensors");
@@ -323,6 +353,7 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
   if (!ws || ws_bytes < ef_ws_bytes(ts, count))
     return set_error(CP_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, ef_ws_bytes(ts, count));
   if (!aligned(ws, 256)) return set_error(CP_ERR_ALIGN, "workspace needs 256-byte alignment");
+  CP_PHASE(-1);
   char* base = (char*)ws;
   std::vector<EfLayout> lay(count);
   std::vector<SweepTask> tasks(count);
@@ -355,6 +386,7 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     ef_tasks_store_kernel<<<1, 64, 0, st>>>(b, cn, dtasks + c0);
   }
   CP_LAUNCHED("EF setup");
+  CP_PHASE(0);
 
   for (int it = 0; it < n_iter; ++it) {
     for (int i = 0; i < count; ++i) {
@@ -367,10 +399,12 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
           t.ttype, t.raw, (int)t.nrow, (int)t.n, (float*)(base + L.dlT), (float*)(base + L.mlT));
     }
     CP_LAUNCHED("EF commit");
+    CP_PHASE(1);
     int rows = 0;
     for (int i = 0; i < count; ++i) rows = tasks[i].nrow > rows ? tasks[i].nrow : rows;
     ef_sweep_exact_kernel<BLK><<<dim3((unsigned)((rows + 255) / 256), (unsigned)count), 256, 0, st>>>(dtasks);
     CP_LAUNCHED("EF sweep");
+    CP_PHASE(2);
     for (int i = 0; i < count; ++i) {
       const cp_ef_tensor& t = ts[i];
       const EfLayout& L = lay[i];
@@ -390,16 +424,39 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
                                                         (float*)(base + L.Wcur));
     }
     CP_LAUNCHED("EF repack");
+    CP_PHASE(3);
   }
   for (int i = 0; i < count; ++i)
     if (ts[i].recon)
       if (int s = kq_dequantize(ts[i].ttype, ts[i].raw, ts[i].nrow, ts[i].n, ts[i].recon, st)) return s;
+  CP_PHASE(4);
   return CP_OK;
+}
+
+int ef_phase_ms(float* out, int nphase) {
+  for (int p = 0; p < nphase; ++p) out[p] = 0.0f;
+  if (g_clock.used < 2) return 0;
+  CP_HIP(hipEventSynchronize(g_clock.ev[g_clock.used - 1]));
+  for (int i = 1; i < g_clock.used; ++i) {
+    float ms = 0.0f;
+    CP_HIP(hipEventElapsedTime(&ms, g_clock.ev[i - 1], g_clock.ev[i]));
+    const int p = g_clock.label[i];
+    if (p >= 0 && p < nphase) out[p] += ms;
+  }
+  return nphase < 5 ? nphase : 5;
 }
 
 }  // namespace cp
 
 extern "C" {
+
+void cp_ef_profile(int enable) { cp::g_clock.on = enable != 0; }
+
+int cp_ef_phase_ms(float* out, int nphase) {
+  cp::clear_error();
+  if (!out || nphase <= 0) return cp::set_error(CP_ERR_ARG, "bad phase buffer");
+  return cp::ef_phase_ms(out, nphase);
+}
 
 size_t cp_ef_ws_bytes(const cp_ef_tensor* tensors, int count) {
   if (!tensors || count <= 0) return 0;
