@@ -153,6 +153,8 @@ def main():
     ap.add_argument("--layers", type=int, default=28,
                     help="decoder layers (28 = the full workload; fewer only for quick checks)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--ef-mode", choices=["mfma", "exact"], default="exact",
+                    help="cross-block error propagation: MFMA GEMM or the reference's exact order")
     args = ap.parse_args()
     if args.gpus != 1:
         msg = (f"bench.py runs on one GPU only (got --gpus {args.gpus}); the encoder path "
@@ -174,6 +176,8 @@ def main():
     ef_flops = 2 * layers * sum(r * n * (n - 1) for _, r, n, _ in wl.QWEN3_06B_LAYER)
     log(f"building workload: {layers} layers, {total_weights} weights")
     X, W, H, slot = build_workload(layers, dev)
+    mode = _lib.CP_EF_MFMA if args.ef_mode == "mfma" else _lib.CP_EF_EXACT
+    other = _lib.CP_EF_EXACT if mode == _lib.CP_EF_MFMA else _lib.CP_EF_MFMA
 
     def step(profile):
         hs, he, ee = (torch.cuda.Event(enable_timing=True) for _ in range(3))
@@ -181,7 +185,7 @@ def main():
         hessian_phase(X, H, slot)
         he.record()
         lib.cp_ef_profile(1 if profile else 0)
-        ef_phase(W, H, slot, layers, _lib.CP_EF_EXACT)
+        ef_phase(W, H, slot, layers, mode)
         ee.record()
         lib.cp_ef_profile(0)
         return hs, he, ee
@@ -204,6 +208,14 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
+    # one untimed-by-contract step of the other EF mode, reported for comparison
+    o0, o1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    o0.record()
+    ef_phase(W, H, slot, layers, other)
+    o1.record()
+    torch.cuda.synchronize()
+    other_ms = o0.elapsed_time(o1)
+
     hess_ms = sum(hs.elapsed_time(he) for hs, he, _ in marks) / args.steps
     ef_ms = sum(he.elapsed_time(ee) for _, he, ee in marks) / args.steps
     ph = [sum(p[k] for p in phases) / args.steps for k in range(5)]
@@ -225,7 +237,8 @@ def main():
         avg_ms = ph[2] / sweep_launches
         flops_per_launch = ef_flops / sweep_launches
         ach = flops_per_launch / (avg_ms * 1e-3) / 1e12
-        roof = {"kernel": "ef_sweep_exact_kernel", "bound": "mfma", "achieved": ach,
+        roof = {"kernel": ("ef_sweep_mfma_kernel" if mode == _lib.CP_EF_MFMA
+                           else "ef_sweep_exact_kernel"), "bound": "mfma", "achieved": ach,
                 "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_FP32_TFLOPS,
                 "traffic": None, "avg_launch_ms": avg_ms, "launches_per_step": sweep_launches}
 
@@ -246,10 +259,13 @@ def main():
                    "layers": layers, "tensors": 7 * layers, "weights": total_weights,
                    "hessians": 4 * layers, "hessian_rows": ROWS, "activations": "bf16",
                    "container": "Q2_K", "qw": "diag(H)/N", "n_iter": 2, "damp": 0.01,
-                   "act_order": True, "ef_mode": "exact"},
+                   "act_order": True, "ef_mode": args.ef_mode},
         "ef": {"ms": ef_ms, "mweights_per_s": ef_mw, "flops_update": ef_flops,
                "phase_ms": {"factor_and_setup": ef_ms - sum(ph), "setup": ph[0],
-                            "commit": ph[1], "sweep": ph[2], "repack": ph[3], "decode": ph[4]}},
+                            "commit": ph[1], "sweep": ph[2], "repack": ph[3], "decode": ph[4]},
+               "other_mode": {"mode": "exact" if mode == _lib.CP_EF_MFMA else "mfma",
+                              "ms": other_ms,
+                              "mweights_per_s": total_weights / (other_ms * 1e-3) / 1e6}},
         "hessian": {"ms": hess_ms, "tflops": hess_tflops, "flops": hess_flops,
                     "frac_of_bf16_peak": hess_tflops / PEAK_BF16_TFLOPS},
         "roofline": roof,

@@ -85,7 +85,11 @@ int cp_chol_inv_upper(const void* H, int h_dtype, int64_t n, int batch, const in
 /* ---- EF encode (coldpress/ef.py:179-218) ---- */
 
 enum cp_ef_mode {
-  CP_EF_EXACT = 0 /* error propagation in the reference's sequential float32 order: bit-exact */
+  CP_EF_EXACT = 0,      /* error propagation in the reference's sequential float32 order
+                           (products on MFMA, ordered subtraction on VALU): bit-exact          */
+  CP_EF_MFMA = 1,       /* cross-block propagation as float32-accumulated MFMA GEMMs (lazy
+                           batch of 32 columns); in-block propagation exact; not bit-exact   */
+  CP_EF_EXACT_VALU = 2  /* as CP_EF_EXACT with products and subtractions on VALU only        */
 };
 
 typedef struct cp_ef_tensor {

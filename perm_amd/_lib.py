@@ -22,6 +22,8 @@ _i64, _i32, _vp, _f64 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_
 _sz = ctypes.c_size_t
 
 CP_EF_EXACT = 0
+CP_EF_MFMA = 1
+CP_EF_EXACT_VALU = 2
 
 
 class EfTensor(ctypes.Structure):

@@ -28,11 +28,16 @@ def sources():
     return sorted(f for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
+# Per-source code-generation flags. ef.hip: MFMA results in VGPRs, so the EF
+# sweep's ordered subtraction reads the products without AGPR copies.
+EXTRA = {"ef.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src):
     obj = os.path.join(BUILD, src + ".o")
     cmd = [HIPCC, *COMMON, "-c", os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".hip"):
-        cmd[1:1] = HIP_FLAGS
+        cmd[1:1] = HIP_FLAGS + EXTRA.get(src, [])
     else:
         cmd[1:1] = ["-x", "c++", "-I/opt/rocm/include", "-D__HIP_PLATFORM_AMD__"]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -59,8 +59,9 @@ __global__ void ef_tasks_store_kernel(const SweepBatch batch, int count, SweepTa
 }
 
 // Address-space views. U is read-only for the whole sweep and its row
-// segments are wave-uniform, so it is read through the constant address space
-// (scalar loads into SGPRs); per-lane traffic goes through global loads/stores.
+// segments are wave-uniform, so the exact kernel reads it through the constant
+// address space (scalar loads into SGPRs); per-lane traffic goes through
+// global loads/stores.
 typedef const float __attribute__((address_space(4)))* ConstF;
 typedef const float __attribute__((address_space(1)))* GlobF;
 typedef float __attribute__((address_space(1)))* GlobFw;
@@ -69,16 +70,75 @@ typedef uint8_t __attribute__((address_space(1)))* GlobBw;
 __device__ __forceinline__ float ld_uniform(const float* p, int64_t i) { return ((ConstF)p)[i]; }
 __device__ __forceinline__ float ld_lane(const float* p, int64_t i) { return ((GlobF)p)[i]; }
 
-// Grid: x = groups of 4 stripes (256 rows), y = task.
+constexpr int SUBP = 16;  // sub-panel width inside a block
+
+// In-block part of the sweep for one lane (= one row), shared by both kernels.
+// On entry trow[k] (k < B, LDS, stride 1) holds the block's targets after all
+// earlier blocks' updates; su is the block's diagonal U tile (LDS, [B][B]).
+// The block is walked in sub-panels of SUBP columns, left-looking: a
+// sub-panel's columns first receive the updates of the block's earlier
+// columns (jj ascending), then are quantized and propagated among themselves.
+// Every element therefore still sees its updates one at a time in ascending
+// jj, as in ef.py:199-213. A consumed target slot trow[c] is reused for e_c.
 template <int B>
-__global__ __launch_bounds__(256) void ef_sweep_exact_kernel(const SweepTask* __restrict__ tasks) {
+__device__ __forceinline__ void sweep_block(const SweepTask& tk, int i1, int r, int rr, bool valid,
+                                            float* trow, const float (*su)[B]) {
+  const int nrow = tk.nrow;
+#pragma unroll
+  for (int s0 = 0; s0 < B; s0 += SUBP) {
+    float ts[SUBP];
+#pragma unroll
+    for (int c = 0; c < SUBP; ++c) ts[c] = trow[s0 + c];
+#pragma unroll 1
+    for (int jj = 0; jj < s0; ++jj) {
+      const float e = trow[jj];
+#pragma unroll
+      for (int c = 0; c < SUBP; ++c) ts[c] = ts[c] - e * su[jj][s0 + c];
+    }
+#pragma unroll
+    for (int j = 0; j < SUBP; ++j) {
+      const int cb = s0 + j, c = i1 + cb;
+      const int sb = tk.sbidx[c];
+      const float dl = ld_lane(tk.dlT, (int64_t)sb * nrow + rr);
+      const float ml = tk.mlT ? ld_lane(tk.mlT, (int64_t)sb * nrow + rr) : 0.0f;
+      const bool nz = dl != 0.0f;
+      const int q = nz ? clampi(rint_magic((ts[j] + ml) / dl), tk.lo, tk.hi) : 0;
+      const float recon = dl * (float)q - ml;
+      const float e = nz ? (ts[j] - recon) / su[cb][cb] : 0.0f;
+      if (valid) {
+        ((GlobFw)tk.E)[(int64_t)c * nrow + r] = e;
+        ((GlobFw)tk.WcurT)[(int64_t)c * nrow + r] = ts[j];
+        ((GlobBw)tk.LT)[(int64_t)c * nrow + r] = (uint8_t)(q - tk.lo);
+      }
+      trow[cb] = e;
+#pragma unroll
+      for (int k = j + 1; k < SUBP; ++k) ts[k] = ts[k] - e * su[cb][s0 + k];
+    }
+  }
+}
+
+template <int B>
+__device__ __forceinline__ void load_diag_tile(const SweepTask& tk, int i1, int lane, int nthreads,
+                                               float (*su)[B]) {
+  for (int idx = lane; idx < B * B; idx += nthreads)
+    su[idx / B][idx % B] = ld_lane(tk.U, (int64_t)(i1 + idx / B) * tk.n + i1 + idx % B);
+}
+
+// Exact mode on the VALU only (cross-check of the MFMA-product kernel).
+// Grid: x = groups of 4 stripes (256 rows), y = task. Cross-block
+// updates in the reference's order: t -= e_jj * U[jj][k], jj ascending, one
+// float32 multiply and one subtract each, U row segments via scalar loads.
+template <int B>
+__global__ __launch_bounds__(256, 2) void ef_sweep_exact_kernel(const SweepTask* __restrict__ tasks) {
   const SweepTask tk = tasks[blockIdx.y];
-  const int r = blockIdx.x * 256 + threadIdx.x;
   if ((int)(blockIdx.x * 256) >= tk.nrow) return;
+  const int r = blockIdx.x * 256 + threadIdx.x;
   const int nrow = tk.nrow, n = tk.n;
   const bool valid = r < nrow;
   const int rr = valid ? r : nrow - 1;
   __shared__ float su[B][B];
+  __shared__ float st[256][B + 1];
+  float* trow = st[threadIdx.x];
   for (int i1 = 0; i1 < n; i1 += B) {
     float t[B];
 #pragma unroll
@@ -89,29 +149,188 @@ __global__ __launch_bounds__(256) void ef_sweep_exact_kernel(const SweepTask* __
 #pragma unroll
       for (int k = 0; k < B; ++k) t[k] = t[k] - e * ld_uniform(tk.U, ub + k);
     }
-    // the block's diagonal U tile, shared by the 4 stripes of the workgroup
+#pragma unroll
+    for (int k = 0; k < B; ++k) trow[k] = t[k];
     __syncthreads();
-    for (int idx = threadIdx.x; idx < B * B; idx += 256)
-      su[idx / B][idx % B] = ld_lane(tk.U, (int64_t)(i1 + idx / B) * n + i1 + idx % B);
+    load_diag_tile<B>(tk, i1, threadIdx.x, 256, su);
+    __syncthreads();
+    sweep_block<B>(tk, i1, r, rr, valid, trow, su);
+  }
+}
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+
+// Row of the 32x32 MFMA result held by register v of lane l (column = l % 32).
+__device__ __forceinline__ int mfma32_row(int v, int l) { return 8 * (v >> 2) + 4 * (l >> 5) + (v & 3); }
+
+// Exact mode on the matrix cores. One wave per 64-row stripe (lane = row in
+// the panel; grid: x = stripe, y = task). For every earlier column jj one
+// v_mfma_f32_32x32x1_2b_f32 forms the 64 x 32 outer product e_jj (x) U[jj][block]
+// with a -0.0 accumulator, i.e. each product rounded once to float32 --
+// exactly the fl(e * u) that np.outer forms -- and the VALU subtracts it from
+// the targets in jj order: t = fl(t - fl(e * u)), the reference's two roundings
+// in the reference's order. The targets live in the MFMA result layout during
+// this phase and move through LDS to one row per lane for the block's panel.
+template <int B>
+__global__ __launch_bounds__(64) void ef_sweep_xmfma_kernel(const SweepTask* __restrict__ tasks) {
+  static_assert(B == 32, "one 32-wide MFMA column tile per block");
+  const SweepTask tk = tasks[blockIdx.y];
+  const int row0 = blockIdx.x * 64;
+  if (row0 >= tk.nrow) return;
+  const int l = threadIdx.x;
+  const int nrow = tk.nrow, n = tk.n;
+  const int r = row0 + l;
+  const bool valid = r < nrow;
+  const int rr = valid ? r : nrow - 1;
+  __shared__ float su[B][B];
+  __shared__ float st[64][B + 1];
+  float* trow = st[l];
+  const int cl = l & 31;
+  for (int i1 = 0; i1 < n; i1 += B) {
+    // targets into the MFMA layout: block b, register v -> row b*32 + mfma32_row(v, l), col cl
+#pragma unroll
+    for (int k = 0; k < B; ++k) trow[k] = ld_lane(tk.WpT, (int64_t)(i1 + k) * nrow + rr);
+    __syncthreads();
+    float tv[32];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      tv[v] = st[mfma32_row(v, l)][cl];
+      tv[16 + v] = st[32 + mfma32_row(v, l)][cl];
+    }
+    // products for column jj+1 are formed while column jj's are subtracted; the
+    // accumulator operand is the inline constant 0, so fl(0 + e*u) = fl(e*u)
+    // except that an exactly-zero product comes back as +0.0: only the sign of
+    // a zero target can differ, which no code, byte or non-zero value sees.
+    const f32x32 nz = {};
+    if (i1 > 0) {
+      // columns in groups of 4 (i1 is a multiple of 32); the next group's
+      // operands are loaded one group ahead, results ping-pong between P0/P1
+      float ea[4], ua[4], eb[4], ub[4];
+      auto load = [&](int g, float (&e)[4], float (&u)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t jj = (int64_t)g * 4 + q;
+          e[q] = ld_lane(tk.E, jj * nrow + rr);
+          u[q] = ld_lane(tk.U, jj * n + i1 + cl);
+        }
+      };
+      const int groups = i1 / 4;
+      load(0, ea, ua);
+      f32x32 P0 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[0], ua[0], nz, 0, 0, 0), P1;
+      for (int g = 0; g + 1 < groups; ++g) {
+        load(g + 1, eb, ub);
+        P1 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[1], ua[1], nz, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P0[v];
+        P0 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[2], ua[2], nz, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P1[v];
+        P1 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[3], ua[3], nz, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P0[v];
+        P0 = __builtin_amdgcn_mfma_f32_32x32x1f32(eb[0], ub[0], nz, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P1[v];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          ea[q] = eb[q];
+          ua[q] = ub[q];
+        }
+      }
+      // last group
+      P1 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[1], ua[1], nz, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P0[v];
+      P0 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[2], ua[2], nz, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P1[v];
+      P1 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[3], ua[3], nz, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P0[v];
+#pragma unroll
+      for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P1[v];
+    }
     __syncthreads();
 #pragma unroll
-    for (int jj = 0; jj < B; ++jj) {
-      const int c = i1 + jj;
-      const int s = tk.sbidx[c];
-      const float dl = ld_lane(tk.dlT, (int64_t)s * nrow + rr);
-      const float ml = tk.mlT ? ld_lane(tk.mlT, (int64_t)s * nrow + rr) : 0.0f;
-      const bool nz = dl != 0.0f;
-      const int q = nz ? clampi(rint_magic((t[jj] + ml) / dl), tk.lo, tk.hi) : 0;
-      const float recon = dl * (float)q - ml;
-      const float e = nz ? (t[jj] - recon) / su[jj][jj] : 0.0f;
-      if (valid) {
-        ((GlobFw)tk.E)[(int64_t)c * nrow + r] = e;
-        ((GlobFw)tk.WcurT)[(int64_t)c * nrow + r] = t[jj];
-        ((GlobBw)tk.LT)[(int64_t)c * nrow + r] = (uint8_t)(q - tk.lo);
+    for (int v = 0; v < 16; ++v) {
+      st[mfma32_row(v, l)][cl] = tv[v];
+      st[32 + mfma32_row(v, l)][cl] = tv[16 + v];
+    }
+    load_diag_tile<B>(tk, i1, l, 64, su);
+    __syncthreads();
+    sweep_block<B>(tk, i1, r, rr, valid, trow, su);
+    __syncthreads();
+  }
+}
+
+// MFMA mode. One wave per 64-row stripe (grid: x = stripe, y = task).
+// Cross-block updates of a block are one GEMM, acc[64 x B] = E[64 x i1] *
+// U[i1 x B], on v_mfma_f32_32x32x2f32 (A = E from the column-major error
+// buffer, B = U rows, both coalesced, prefetched one 8-column group ahead);
+// the targets are then x - acc (one float32 subtraction of the float32-
+// accumulated sum), and the block itself is swept exactly as in exact mode.
+template <int B>
+__global__ __launch_bounds__(64, 2) void ef_sweep_mfma_kernel(const SweepTask* __restrict__ tasks) {
+  static_assert(B == 32, "one 32-wide MFMA column tile per block");
+  const SweepTask tk = tasks[blockIdx.y];
+  const int row0 = blockIdx.x * 64;
+  if (row0 >= tk.nrow) return;
+  const int l = threadIdx.x;
+  const int nrow = tk.nrow, n = tk.n;
+  const int r = row0 + l;
+  const bool valid = r < nrow;
+  const int rr = valid ? r : nrow - 1;
+  __shared__ float su[B][B];
+  __shared__ float st[64][B + 1];
+  float* trow = st[l];
+  const int kl = l >> 5, cl = l & 31;
+  const int ra0 = min(row0 + cl, nrow - 1), ra1 = min(row0 + 32 + cl, nrow - 1);
+  for (int i1 = 0; i1 < n; i1 += B) {
+    f32x16 acc0, acc1;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      acc0[v] = 0.0f;
+      acc1[v] = 0.0f;
+    }
+    // jj in groups of 8 (4 MFMA k-steps), next group's operands loaded ahead
+    float a0[4], a1[4], b[4], na0[4], na1[4], nb[4];
+    const int groups = i1 / 8;
+    auto load = [&](int g, float (&x0)[4], float (&x1)[4], float (&y)[4]) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int64_t jj = (int64_t)g * 8 + 2 * s + kl;
+        x0[s] = ld_lane(tk.E, jj * nrow + ra0);
+        x1[s] = ld_lane(tk.E, jj * nrow + ra1);
+        y[s] = ld_lane(tk.U, jj * n + i1 + cl);
+      }
+    };
+    if (groups > 0) load(0, a0, a1, b);
+    for (int g = 0; g < groups; ++g) {
+      if (g + 1 < groups) load(g + 1, na0, na1, nb);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b[s], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b[s], acc1, 0, 0, 0);
       }
 #pragma unroll
-      for (int k = jj + 1; k < B; ++k) t[k] = t[k] - e * su[jj][k];
+      for (int s = 0; s < 4; ++s) {
+        a0[s] = na0[s];
+        a1[s] = na1[s];
+        b[s] = nb[s];
+      }
     }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      st[mfma32_row(v, l)][cl] = acc0[v];
+      st[32 + mfma32_row(v, l)][cl] = acc1[v];
+    }
+    load_diag_tile<B>(tk, i1, l, 64, su);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < B; ++k) trow[k] = ld_lane(tk.WpT, (int64_t)(i1 + k) * nrow + rr) - trow[k];
+    sweep_block<B>(tk, i1, r, rr, valid, trow, su);
+    __syncthreads();
   }
 }
 
@@ -338,7 +557,8 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
                     size_t ws_bytes, hipStream_t st) {
   if (!ts || count <= 0) return set_error(CP_ERR_ARG, "no tensors");
   if (n_iter < 1) return set_error(CP_ERR_ARG, "n_iter must be >= 1");
-  if (mode != CP_EF_EXACT) return set_error(CP_ERR_ARG, "unknown EF mode %d", mode);
+  if (mode != CP_EF_EXACT && mode != CP_EF_MFMA && mode != CP_EF_EXACT_VALU)
+    return set_error(CP_ERR_ARG, "unknown EF mode %d", mode);
   for (int i = 0; i < count; ++i) {
     const cp_ef_tensor& t = ts[i];
     KqGeom g;
@@ -402,7 +622,12 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     CP_PHASE(1);
     int rows = 0;
     for (int i = 0; i < count; ++i) rows = tasks[i].nrow > rows ? tasks[i].nrow : rows;
-    ef_sweep_exact_kernel<BLK><<<dim3((unsigned)((rows + 255) / 256), (unsigned)count), 256, 0, st>>>(dtasks);
+    if (mode == CP_EF_EXACT_VALU)
+      ef_sweep_exact_kernel<BLK><<<dim3((unsigned)((rows + 255) / 256), (unsigned)count), 256, 0, st>>>(dtasks);
+    else if (mode == CP_EF_EXACT)
+      ef_sweep_xmfma_kernel<BLK><<<dim3((unsigned)((rows + 63) / 64), (unsigned)count), 64, 0, st>>>(dtasks);
+    else
+      ef_sweep_mfma_kernel<BLK><<<dim3((unsigned)((rows + 63) / 64), (unsigned)count), 64, 0, st>>>(dtasks);
     CP_LAUNCHED("EF sweep");
     CP_PHASE(2);
     for (int i = 0; i < count; ++i) {

@@ -112,10 +112,16 @@ def ef_encode_dev(items, n_iter=2, mode=_lib.CP_EF_EXACT):
     return outs
 
 
-def ef_encode(x, ttype, qw, H, n_iter=2, damp=0.01, act_order=True):
+MODES = {"exact": _lib.CP_EF_EXACT, "mfma": _lib.CP_EF_MFMA, "exact_valu": _lib.CP_EF_EXACT_VALU}
+
+
+def ef_encode(x, ttype, qw, H, n_iter=2, damp=0.01, act_order=True, mode="exact"):
     """GPTQ error feedback into committed k-quant containers (coldpress/ef.py:179-218).
 
     x: [nrow, n] f32; qw: imatrix means [n] or None; H: [n, n] (X^T X).
+    mode "exact" propagates errors in the reference's sequential float32 order
+    (bit-identical codes); "mfma" applies the cross-block propagation as
+    float32-accumulated MFMA GEMMs.
     Returns (raw bytes [nrow, row_bytes], recon [nrow, n])."""
     if ttype not in BYTES_PER_SB:
         raise ValueError(ttype)
@@ -127,13 +133,13 @@ def ef_encode(x, ttype, qw, H, n_iter=2, damp=0.01, act_order=True):
     order = act_order_dev(Hd, act_order)
     U, _ = factor_dev(Hd, order, damp)
     (raw, rec), = ef_encode_dev([{"ttype": ttype, "x": xd, "qw": qd, "U": U, "order": order}],
-                                n_iter)
+                                n_iter, MODES[mode])
     if host:
         return _lib.to_host(raw), _lib.to_host(rec)
     return raw, rec
 
 
-def ef_encode_many(tensors, n_iter=2, damp=0.01, act_order=True, mode=_lib.CP_EF_EXACT):
+def ef_encode_many(tensors, n_iter=2, damp=0.01, act_order=True, mode="exact"):
     """EF-encode many tensors in one batched pass.
 
     tensors: list of dicts {name, ttype, x (CUDA f32), qw (CUDA f32 or None),
@@ -159,5 +165,5 @@ def ef_encode_many(tensors, n_iter=2, damp=0.01, act_order=True, mode=_lib.CP_EF
         U, order = factor[id(t["H"])]
         items.append({"ttype": t["ttype"], "x": t["x"], "qw": t.get("qw"), "U": U,
                       "order": order, "recon": t.get("recon", True)})
-    outs = ef_encode_dev(items, n_iter, mode)
+    outs = ef_encode_dev(items, n_iter, MODES[mode])
     return {t["name"]: o for t, o in zip(tensors, outs)}
