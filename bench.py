@@ -93,7 +93,7 @@ def ef_phase(W, H, slot, layers, mode):
 
 def cpu_baseline(W, H, slot, layers, total_weights):
     """Time the numpy oracle (port of coldpress/ef.py:46-218 + kquant.py) on
-    64- and 256-row subsamples of layer 0's 7 tensors, with one factorization
+    128- and 512-row subsamples of layer 0's 7 tensors, with one factorization
     per tensor as the reference does (ef.py:189), and extrapolate:
     T(tensor) = T_factor + a + b * nrow, times 28 identical layers."""
     import numpy as np
@@ -117,17 +117,17 @@ def cpu_baseline(W, H, slot, layers, total_weights):
         U = E.inv_upper_factor(Hn[np.ix_(order, order)], 0.01).astype(np.float32)
         t_fact = time.perf_counter() - t0
         ts = {}
-        for r in (64, 256):
+        for r in (128, 512):
             t0 = time.perf_counter()
             E.ef_encode(Wn[:r], "Q2_K", qw, Hn, U=U)
             ts[r] = time.perf_counter() - t0
-        b = (ts[256] - ts[64]) / 192.0
-        a = ts[64] - 64 * b
+        b = (ts[512] - ts[128]) / 384.0
+        a = ts[128] - 128 * b
         t_tensor = t_fact + a + b * rows
-        per.append((name, t_fact, ts[64], ts[256], t_tensor))
+        per.append((name, t_fact, ts[128], ts[512], t_tensor))
         t_total += t_tensor
-        t_spent += t_fact + ts[64] + ts[256]
-        log(f"cpu {name}: factor {t_fact:.2f}s ef64 {ts[64]:.2f}s ef256 {ts[256]:.2f}s "
+        t_spent += t_fact + ts[128] + ts[512]
+        log(f"cpu {name}: factor {t_fact:.2f}s ef128 {ts[128]:.2f}s ef512 {ts[512]:.2f}s "
             f"-> full tensor {t_tensor:.1f}s")
     t_total *= layers
     return {
@@ -135,7 +135,7 @@ def cpu_baseline(W, H, slot, layers, total_weights):
         "unit": "Mweights/s",
         "cores": int(blas_threads),
         "kind": "port",
-        "sample": (f"numpy oracle (port of ef.py/kquant.py) on layer 0's 7 tensors at 64 and 256 "
+        "sample": (f"numpy oracle (port of ef.py/kquant.py) on layer 0's 7 tensors at 128 and 512 "
                    f"rows + one factorization per tensor ({t_spent:.1f} s of CPU work); "
                    f"extrapolated linearly in rows to all {layers} layers "
                    f"(est. {t_total:.0f} s for the full encode); sweep and codec are "
