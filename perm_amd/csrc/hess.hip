@@ -38,19 +38,18 @@ constexpr int KP = KT + 8;
 
 __device__ __forceinline__ void load_block_bf16(const uint16_t* __restrict__ X, int64_t N, int d,
                                                 int64_t t0, int c0, uint4 (&v)[4]) {
-  // rows t0..t0+3, channels c0..c0+7
+  // rows t0..t0+3, channels c0..c0+7; d % 8 == 0 and c0 % 8 == 0, so the 8
+  // channels are either all inside the matrix or all outside. Out-of-range
+  // blocks load a clamped in-range address and are zeroed without branching.
+  const bool cin = c0 < d;
+  const int cc = cin ? c0 : 0;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    int64_t t = t0 + q;
-    if (t < N && c0 + 7 < d) {
-      v[q] = *reinterpret_cast<const uint4*>(X + t * d + c0);
-    } else {
-      uint32_t w[4] = {0, 0, 0, 0};
-      if (t < N)
-        for (int c = 0; c < 8; ++c)
-          if (c0 + c < d) w[c >> 1] |= (uint32_t)X[t * d + c0 + c] << (16 * (c & 1));
-      v[q] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+    const int64_t t = t0 + q;
+    const bool ok = cin && t < N;
+    const int64_t tc = t < N ? t : N - 1;
+    uint4 x = *reinterpret_cast<const uint4*>(X + tc * d + cc);
+    v[q] = ok ? x : make_uint4(0, 0, 0, 0);
   }
 }
 
@@ -135,6 +134,127 @@ __global__ __launch_bounds__(256) void hess_bf16_kernel(const uint16_t* __restri
       }
 }
 
+// ---------------------------------------------------------------- bf16, large tiles
+// Lower-triangle tiles of 256 x 256 (H is symmetric; hess_mirror_kernel copies
+// the lower triangle into the upper one afterwards). Each of the 8 waves owns
+// a 128 x 64 block as 4 x 2 MFMA 32x32 tiles (128 float32 accumulators), so a
+// 16-byte LDS fragment feeds 2 to 4 MFMAs; two waves share each SIMD. Work items
+// (row split, tile) are ordered split-major and handed out XCD-contiguously:
+// the hardware places workgroup w on XCD w % 8, so item = (w % 8) * per + w / 8
+// keeps the workgroups of one XCD on the same rows of X (shared in its L2).
+constexpr int BT = 256;
+
+__global__ __launch_bounds__(512) void hess_bf16_tri_kernel(const uint16_t* __restrict__ X, int64_t N,
+                                                            int d, int ntiles, int splits,
+                                                            int64_t rows_per_split,
+                                                            float* __restrict__ H) {
+  __shared__ uint16_t sA[2][BT * KP];
+  __shared__ uint16_t sB[2][BT * KP];
+  const int total = ntiles * splits;
+  const int per = (total + 7) / 8;
+  const int item = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (item >= total) return;
+  const int split = item / ntiles, tile = item - split * ntiles;
+  int ti = (int)((sqrtf(8.0f * (float)tile + 1.0f) - 1.0f) * 0.5f);
+  while (ti * (ti + 1) / 2 > tile) --ti;
+  while ((ti + 1) * (ti + 2) / 2 <= tile) ++ti;
+  const int tj = tile - ti * (ti + 1) / 2;
+  const int i0 = ti * BT, j0 = tj * BT;
+  const int64_t r0 = (int64_t)split * rows_per_split;
+  const int64_t r1 = min(N, r0 + rows_per_split);
+  if (r0 >= r1) return;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int wm = (w >> 2) * 128, wn = (w & 3) * 64;  // 8 waves: 2 x 4 quadrants of 128 x 64
+  // loader: threads 0..255 stage the i-panel, 256..511 the j-panel, a 4(t) x 8 block each
+  // Lanes 8k..8k+7 take rows 0, 4, .., 28 of one 8-channel block, so each
+  // transposed 8-byte LDS store of a 16-lane phase covers two 64-byte row runs
+  // on disjoint banks; a wave's 16-byte global loads read 8 rows x 128 bytes.
+  const bool loadsA = tid < 256;
+  const int lt = (tid & 7) * 4;            // 0..28
+  const int lc = ((tid & 255) >> 3) * 8;   // 0..248
+  const int cbase = (loadsA ? i0 : j0) + lc;
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+
+  uint4 blk[4];
+  load_block_bf16(X, r1, d, r0 + lt, cbase, blk);
+  store_block_bf16(loadsA ? sA[0] : sB[0], lc, lt, blk);
+  __syncthreads();
+  int buf = 0;
+  for (int64_t t0 = r0; t0 < r1; t0 += KT) {
+    // the next step's rows (clamped loads past the end are discarded)
+    load_block_bf16(X, r1, d, t0 + KT + lt, cbase, blk);
+#pragma unroll
+    for (int kk = 0; kk < KT / 16; ++kk) {
+      const int koff = kk * 16 + 8 * (l >> 5);
+      bf16x8 a[4], b[2];
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+        a[x] = *reinterpret_cast<const bf16x8*>(&sA[buf][(wm + x * 32 + (l & 31)) * KP + koff]);
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+        b[y] = *reinterpret_cast<const bf16x8*>(&sB[buf][(wn + y * 32 + (l & 31)) * KP + koff]);
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y)
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[x], b[y], acc[x][y], 0, 0, 0);
+    }
+    store_block_bf16(loadsA ? sA[buf ^ 1] : sB[buf ^ 1], lc, lt, blk);
+    __syncthreads();
+    buf ^= 1;
+  }
+  // lane l holds, for register v of tile (x, y), row wm + 32x + mfma32_row(v, l)
+  // and column wn + 32y + l % 32 of the workgroup tile
+  float* Hb = H + (int64_t)(i0 + wm + 4 * (l >> 5)) * d + (j0 + wn + (l & 31));
+  if (ti != tj && i0 + BT <= d) {
+    // interior tile strictly below the diagonal: every element is stored
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          atomicAdd(Hb + (int64_t)(x * 32 + 8 * (v >> 2) + (v & 3)) * d + y * 32, acc[x][y][v]);
+  } else {
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int i = i0 + wm + x * 32 + mfma32_row(v, l);
+          const int j = j0 + wn + y * 32 + (l & 31);
+          if (i < d && j <= i)
+            atomicAdd(Hb + (int64_t)(x * 32 + 8 * (v >> 2) + (v & 3)) * d + y * 32, acc[x][y][v]);
+        }
+  }
+}
+
+// H[i][j] = H[j][i] for i < j, through 64 x 64 LDS tiles.
+__global__ __launch_bounds__(256) void hess_mirror_kernel(float* __restrict__ H, int d) {
+  __shared__ float tl[64][65];
+  const int bi = blockIdx.y, bj = blockIdx.x;  // target tile (upper): rows bi, cols bj
+  if (bj < bi) return;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  // source: lower tile rows bj, cols bi
+  for (int r = ty; r < 64; r += 4) {
+    int i = bj * 64 + r, j = bi * 64 + tx;
+    if (i < d && j < d) tl[r][tx] = H[(int64_t)i * d + j];
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    int i = bi * 64 + r, j = bj * 64 + tx;
+    if (i < d && j < d && j > i) H[(int64_t)i * d + j] = tl[tx][r];
+  }
+}
+
 // ---------------------------------------------------------------- f32 input
 __global__ __launch_bounds__(256) void hess_f32_kernel(const float* __restrict__ X, int64_t N, int d,
                                                        int64_t rows_per_split, float* __restrict__ H) {
@@ -189,6 +309,24 @@ __global__ __launch_bounds__(256) void hess_f32_kernel(const float* __restrict__
       }
 }
 
+// Row splits for the triangle kernel: as many workgroups as fill whole rounds
+// of the 256 CUs (one 80 KB-LDS workgroup per CU), each split >= 1024 rows.
+static int pick_splits(int ntiles, int64_t N) {
+  int best_s = 1;
+  double best_eff = -1.0;
+  for (int s = 1; s <= 256; ++s) {
+    if (s > 1 && N / s < 1024) break;
+    const int64_t wg = (int64_t)ntiles * s;
+    const int64_t rounds = (wg + 255) / 256;
+    const double eff = (double)wg / (double)(rounds * 256);
+    if (eff > best_eff + 1e-9) {
+      best_eff = eff;
+      best_s = s;
+    }
+  }
+  return best_s;
+}
+
 }  // namespace cp
 
 extern "C" int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, float* H, void* stream) {
@@ -199,6 +337,22 @@ extern "C" int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, f
   if (!cp::aligned(X, 16) || !cp::aligned(H, 4)) return cp::set_error(CP_ERR_ALIGN, "X needs 16-byte alignment");
   if (x_dtype == 1 && d % 8) return cp::set_error(CP_ERR_SHAPE, "bf16 X needs d %% 8 == 0 (got %lld)", (long long)d);
   hipStream_t st = (hipStream_t)stream;
+  if (x_dtype == 1) {
+    const int T = (int)((d + cp::BT - 1) / cp::BT);
+    const int ntiles = T * (T + 1) / 2;
+    const int splits = cp::pick_splits(ntiles, N);
+    int64_t rps = (N + splits - 1) / splits;
+    rps = (rps + cp::KT - 1) / cp::KT * cp::KT;
+    const int total = ntiles * splits;
+    const int per = (total + 7) / 8;
+    cp::hess_bf16_tri_kernel<<<dim3(8 * per), 512, 0, st>>>((const uint16_t*)X, N, (int)d, ntiles,
+                                                            splits, rps, H);
+    CP_LAUNCHED("hessian launch");
+    const int tb = (int)((d + 63) / 64);
+    cp::hess_mirror_kernel<<<dim3(tb, tb), 256, 0, st>>>(H, (int)d);
+    CP_LAUNCHED("hessian mirror");
+    return CP_OK;
+  }
   const int tiles = (int)((d + cp::HT - 1) / cp::HT);
   // enough row splits for ~4 workgroups per CU, each at least 512 rows
   int64_t want = (1024 + (int64_t)tiles * tiles - 1) / ((int64_t)tiles * tiles);
@@ -208,10 +362,7 @@ extern "C" int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, f
   rps = (rps + cp::KT - 1) / cp::KT * cp::KT;
   splits = (N + rps - 1) / rps;
   dim3 grid(tiles, tiles, (unsigned)splits);
-  if (x_dtype == 1)
-    cp::hess_bf16_kernel<<<grid, 256, 0, st>>>((const uint16_t*)X, N, (int)d, rps, H);
-  else
-    cp::hess_f32_kernel<<<grid, 256, 0, st>>>((const float*)X, N, (int)d, rps, H);
+  cp::hess_f32_kernel<<<grid, 256, 0, st>>>((const float*)X, N, (int)d, rps, H);
   CP_LAUNCHED("hessian launch");
   return CP_OK;
 }
