@@ -141,6 +141,18 @@ int cp_ef_phase_ms(float* out, int nphase);
  * not fixed (split-K partials are added with float32 atomics). */
 int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, float* H, void* stream);
 
+/* ---- PERM channel permutations (coldpress/perm/spacemaps/qwen3.py, ef.py:289-290) ---- */
+
+/* dst[r][c] = src[row_perm[r]][col_perm[c]] for a row-major [rows, cols] matrix of
+ * elem_bytes-byte elements (1, 2, 4 or 8); a NULL permutation is the identity.
+ * Every index must lie in range (the permutations are validated by the caller).
+ * Replaces the index_select / fancy-index moves of qwen3.apply_perms
+ * (coldpress/perm/spacemaps/qwen3.py:141-188) and H[np.ix_(p, p)] (ef.py:289-290).
+ * Not in place. */
+int cp_permute_gather(const void* src, void* dst, const int32_t* row_perm,
+                      const int32_t* col_perm, int64_t rows, int64_t cols, int elem_bytes,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

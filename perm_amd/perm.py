@@ -1,0 +1,141 @@
+"""PERM channel permutations on the GPU, Qwen3 dense space map (the index moves of
+coldpress/perm/spacemaps/qwen3.py).
+
+Three permutation spaces (qwen3.py module docstring):
+  res [d_model]            embedding cols, q/k/v/gate/up input cols, o/down output rows
+  ffn [d_ffn] per layer    gate/up output rows, down input cols
+  vo  [head_dim] per (layer, kv-head)   v output rows of the kv head, o input cols of
+                           its GQA q heads
+Every move is a pure index gather (bit-exact); Hessians and importance vectors of
+an input space move with the same index (ef.py:274-276, 289-290).
+
+perms: {"res": int [d_model], "ffn": [int [d_ffn]] * n_layers,
+        "vo": [[int [head_dim]] * n_kv] * n_layers}  (the reference's container).
+dims:  {"d_model", "d_ffn", "n_layers", "n_heads", "n_kv", "head_dim"}.
+"""
+import numpy as np
+import torch
+
+from . import _lib
+
+RES_INPUT_KINDS = ("attn_q", "attn_k", "attn_v", "ffn_gate", "ffn_up")
+
+
+def identity_perms(dims):
+    return {"res": np.arange(dims["d_model"]),
+            "ffn": [np.arange(dims["d_ffn"]) for _ in range(dims["n_layers"])],
+            "vo": [[np.arange(dims["head_dim"]) for _ in range(dims["n_kv"])]
+                   for _ in range(dims["n_layers"])]}
+
+
+def _check(p, n):
+    p = np.asarray(p)
+    if p.shape != (n,) or not np.array_equal(np.sort(p), np.arange(n)):
+        raise ValueError(f"not a permutation of {n}")
+    return p
+
+
+def v_output_index(perms, layer, dims):
+    """Row index of attn_v's output (n_kv * head_dim): kv head h uses vo[layer][h]
+    (qwen3.py:163-167)."""
+    hd, nkv = dims["head_dim"], dims["n_kv"]
+    idx = np.arange(nkv * hd)
+    for h in range(nkv):
+        idx[h * hd:(h + 1) * hd] = h * hd + _check(perms["vo"][layer][h], hd)
+    return idx
+
+
+def o_input_index(perms, layer, dims):
+    """Column index of attn_output's input (n_heads * head_dim): q head q uses
+    vo[layer][q // group] (qwen3.py:94-103)."""
+    hd, nh = dims["head_dim"], dims["n_heads"]
+    group = nh // dims["n_kv"]
+    idx = np.arange(nh * hd)
+    for q in range(nh):
+        idx[q * hd:(q + 1) * hd] = q * hd + _check(perms["vo"][layer][q // group], hd)
+    return idx
+
+
+def input_perm(gguf_name, perms, dims):
+    """Permutation of a tensor's input axis (GGUF ne[0]) or None (qwen3.py:106-123)."""
+    if gguf_name in ("token_embd.weight", "output.weight"):
+        return np.asarray(perms["res"])
+    if not gguf_name.startswith("blk."):
+        return None
+    parts = gguf_name.split(".")
+    layer, kind = int(parts[1]), parts[2]
+    if kind in RES_INPUT_KINDS:
+        return np.asarray(perms["res"])
+    if kind == "ffn_down":
+        return np.asarray(perms["ffn"][layer])
+    if kind == "attn_output":
+        return o_input_index(perms, layer, dims)
+    return None
+
+
+def inverse(p):
+    p = np.asarray(p)
+    inv = np.empty_like(p)
+    inv[p] = np.arange(p.size)
+    return inv
+
+
+def _dev_index(p, device):
+    if p is None:
+        return None
+    if isinstance(p, torch.Tensor):
+        return p.to(device=device, dtype=torch.int32).contiguous()
+    return torch.from_numpy(np.ascontiguousarray(np.asarray(p), dtype=np.int32)).to(device)
+
+
+def gather(t, rows=None, cols=None):
+    """t[rows][:, cols] on the device (None = all). t: 2-D CUDA tensor of 1/2/4/8-byte
+    elements. The permutations must be in range."""
+    lib = _lib.load()
+    if t.dim() != 2:
+        raise ValueError("gather needs a 2-D tensor")
+    t = t.contiguous()
+    R, C = t.shape
+    rp, cp = _dev_index(rows, t.device), _dev_index(cols, t.device)
+    if rp is not None and rp.numel() != R or cp is not None and cp.numel() != C:
+        raise ValueError("permutation length does not match the tensor")
+    out = torch.empty_like(t)
+    st = lib.cp_permute_gather(_lib.ptr(t), _lib.ptr(out), _lib.ptr(rp), _lib.ptr(cp), R, C,
+                               t.element_size(), _lib.stream_ptr())
+    _lib.check(st)
+    return out
+
+
+def permute_hessian(H, p):
+    """H[np.ix_(p, p)] (ef.py:289-290)."""
+    return gather(H, p, p)
+
+
+def permute_layer(W, perms, layer, dims):
+    """Permuted copies of one decoder layer's linear weights, keyed by GGUF kind
+    (attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up, ffn_down), each
+    [out_features, in_features] as in the HF state dict (qwen3.py:141-188)."""
+    P = _check(perms["res"], dims["d_model"])
+    Pf = _check(perms["ffn"][layer], dims["d_ffn"])
+    out = {}
+    out["attn_q"] = gather(W["attn_q"], None, P)
+    out["attn_k"] = gather(W["attn_k"], None, P)
+    out["attn_v"] = gather(W["attn_v"], v_output_index(perms, layer, dims), P)
+    out["attn_output"] = gather(W["attn_output"], P, o_input_index(perms, layer, dims))
+    out["ffn_gate"] = gather(W["ffn_gate"], Pf, P)
+    out["ffn_up"] = gather(W["ffn_up"], Pf, P)
+    out["ffn_down"] = gather(W["ffn_down"], P, Pf)
+    return out
+
+
+def unpermute_layer(Wp, perms, layer, dims):
+    """Inverse of permute_layer (bit-exact)."""
+    P = inverse(perms["res"])
+    Pf = inverse(perms["ffn"][layer])
+    v_idx = inverse(v_output_index(perms, layer, dims))
+    o_idx = inverse(o_input_index(perms, layer, dims))
+    return {"attn_q": gather(Wp["attn_q"], None, P), "attn_k": gather(Wp["attn_k"], None, P),
+            "attn_v": gather(Wp["attn_v"], v_idx, P),
+            "attn_output": gather(Wp["attn_output"], P, o_idx),
+            "ffn_gate": gather(Wp["ffn_gate"], Pf, P), "ffn_up": gather(Wp["ffn_up"], Pf, P),
+            "ffn_down": gather(Wp["ffn_down"], P, Pf)}
