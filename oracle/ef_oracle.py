@@ -159,13 +159,15 @@ def sweep(xp, U, dl, ml, lo, hi, sub, order):
 
 
 def ef_encode(x, ttype, qw, H, n_iter=2, damp=0.01, act_order_on=True, U=None,
-              stable_order=False):
+              stable_order=False, order=None):
     """GPTQ error feedback into committed k-quant containers (ef.py:179-218).
 
     Returns (raw bytes [nrow, row_bytes], recon [nrow, n] f32). ``U`` lets a test
-    supply the float32 factor directly (in visiting order)."""
+    supply the float32 factor directly (in visiting order), ``order`` the
+    visiting order (then H is not read)."""
     nrow, n = x.shape
-    order = act_order(H, act_order_on, stable_order)
+    if order is None:
+        order = act_order(H, act_order_on, stable_order)
     if U is None:
         U = inv_upper_factor(H[np.ix_(order, order)], damp).astype(F32)
     w_cur = x.astype(F32).copy()
