@@ -10,12 +10,14 @@
 //
 //  * the act_order gather, the reversal and the damping shift fuse into one
 //    pass over H (fact_prepare);
-//  * Cholesky is right-looking with 64-wide panels: the diagonal block is
-//    factored and inverted in LDS, the panel below it is a GEMM with that
-//    inverse, and the trailing update is a lower-triangle fp64 MFMA GEMM;
+//  * Cholesky is left-looking with 64-wide block columns: a block column first
+//    receives the updates of everything to its left in one large-K fp64 MFMA
+//    GEMM, then its diagonal block is factored and inverted in LDS and the
+//    panel below it is a GEMM with that inverse;
 //  * L^{-1} is assembled by recursive doubling: diagonal 64-blocks come from
 //    the panel step, then at block size s, X21 = -X22 (L21 X11) for every pair
-//    of neighbouring s-blocks -- two batched fp64 MFMA GEMMs per level;
+//    of neighbouring s-blocks -- two batched fp64 MFMA GEMMs per level that
+//    skip the all-zero K blocks of their triangular operand;
 //  * a non-positive (or NaN) pivot raises a per-matrix flag; the host reads
 //    the flags and re-runs failed matrices with damp x 10, up to max_tries
 //    attempts, as the reference does.
@@ -40,6 +42,9 @@ constexpr int NB = 64;  // panel width
 // as z = z1 * nz2 + z2 with separate strides per level. LOWER skips tiles
 // strictly above the diagonal of C and writes only C[i][j] with i >= j.
 // Tile 64x64x16, 4 waves of 32x32 each built from v_mfma_f64_16x16x4f64.
+// tri: bit 0 -- A is lower triangular (A[r][k] = 0 for k > r), so output row
+// tile bm only needs k < bm + 64; bit 1 -- B ([K,N], not transposed) is lower
+// triangular (B[k][c] = 0 for k < c), so output column tile bn needs k >= bn.
 struct GemmArgs {
   const double* A;
   const double* B;
@@ -48,6 +53,7 @@ struct GemmArgs {
   double alpha, beta;
   int64_t sA1, sB1, sC1, sA2, sB2, sC2;
   int nz2;
+  int tri;
 };
 
 template <bool BT, bool LOWER>
@@ -68,7 +74,9 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = dbl4{0.0, 0.0, 0.0, 0.0};
 
-  for (int k0 = 0; k0 < g.K; k0 += 16) {
+  const int kbeg = (g.tri & 2) ? (bn & ~15) : 0;
+  const int kend = (g.tri & 1) ? min(g.K, bm + 64) : g.K;
+  for (int k0 = kbeg; k0 < kend; k0 += 16) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       int idx = t + 256 * q;
@@ -342,20 +350,25 @@ static int fact_run(const T* H, int64_t sH, int n, int batch, const int* order, 
     fact_prepare_kernel<T><<<dim3((n + 63) / 64, (n + 3) / 4, batch), 256, 0, st>>>(
         H, n, sH, order, sO, shift, A, sA, active);
     CP_LAUNCHED("factor prepare");
+    // left-looking: block column k first receives all earlier columns' updates
+    // in one large-K GEMM, then its diagonal block is factored and the panel
+    // below it solved
     for (int k = 0; k < n; k += NB) {
+      const int w = n - k < NB ? n - k : NB;
+      if (k > 0) {
+        // A[k:, k:k+w] -= L[k:, 0:k] * L[k:k+w, 0:k]^T
+        GemmArgs ga{A + (int64_t)k * n, A + (int64_t)k * n, A + (int64_t)k * n + k, n - k, w, k,
+                    n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 0};
+        if (int s = dgemm(ga, batch, true, false, st)) return s;
+      }
       fact_diag_kernel<<<batch, 256, 0, st>>>(A, sA, X, sA, n, k, fail, active);
       CP_LAUNCHED("factor diagonal block");
       const int m = n - k - NB;
       if (m <= 0) break;
       // panel: A[k+NB:, k:k+NB] <- A[k+NB:, k:k+NB] * inv(L_kk)^T  (in place, row tiles)
       GemmArgs pa{A + (int64_t)(k + NB) * n + k, X + (int64_t)k * n + k, A + (int64_t)(k + NB) * n + k,
-                  m, NB, NB, n, n, n, 1.0, 0.0, sA, sA, sA, 0, 0, 0, 1};
+                  m, NB, NB, n, n, n, 1.0, 0.0, sA, sA, sA, 0, 0, 0, 1, 0};
       if (int s = dgemm(pa, batch, true, false, st)) return s;
-      // trailing: A[k+NB:, k+NB:] -= P P^T  (lower triangle)
-      GemmArgs ta{A + (int64_t)(k + NB) * n + k, A + (int64_t)(k + NB) * n + k,
-                  A + (int64_t)(k + NB) * n + k + NB, m, m, NB, n, n, n, -1.0, 1.0,
-                  sA, sA, sA, 0, 0, 0, 1};
-      if (int s = dgemm(ta, batch, true, true, st)) return s;
     }
     // L^{-1} by recursive doubling over neighbouring s-blocks
     for (int s = NB; s < n; s *= 2) {
@@ -369,11 +382,11 @@ static int fact_run(const T* H, int64_t sH, int n, int batch, const int* order, 
         const int64_t step = (int64_t)2 * s * (n + 1);
         // T_p = L21 X11
         GemmArgs g1{A + (int64_t)(b0 + s) * n + b0, X + (int64_t)b0 * n + b0, Tm, s2, s, s, n, n, s,
-                    1.0, 0.0, sA, sA, (int64_t)nn, step, step, (int64_t)s * s, pairs};
+                    1.0, 0.0, sA, sA, (int64_t)nn, step, step, (int64_t)s * s, pairs, 2};
         if (int e = dgemm(g1, batch, false, false, st)) return e;
         // X21 = -X22 T_p
         GemmArgs g2{X + (int64_t)(b0 + s) * n + b0 + s, Tm, X + (int64_t)(b0 + s) * n + b0, s2, s, s2,
-                    n, s, n, -1.0, 0.0, sA, (int64_t)nn, sA, step, (int64_t)s * s, step, pairs};
+                    n, s, n, -1.0, 0.0, sA, (int64_t)nn, sA, step, (int64_t)s * s, step, pairs, 1};
         if (int e = dgemm(g2, batch, false, false, st)) return e;
       }
     }
