@@ -10,10 +10,12 @@
 //
 //  * the act_order gather, the reversal and the damping shift fuse into one
 //    pass over H (fact_prepare);
-//  * Cholesky is left-looking with 64-wide block columns: a block column first
+//  * Cholesky is left-looking in two levels: a 256-wide block column first
 //    receives the updates of everything to its left in one large-K fp64 MFMA
-//    GEMM, then its diagonal block is factored and inverted in LDS and the
-//    panel below it is a GEMM with that inverse;
+//    GEMM (wide enough in N to fill the GPU); inside it each 64-wide column
+//    takes its left neighbours' updates, then its diagonal block is factored
+//    and inverted by four waves in registers and the panel below it is a GEMM
+//    with that inverse;
 //  * L^{-1} is assembled by recursive doubling: diagonal 64-blocks come from
 //    the panel step, then at block size s, X21 = -X22 (L21 X11) for every pair
 //    of neighbouring s-blocks -- two batched fp64 MFMA GEMMs per level that
@@ -34,17 +36,29 @@ namespace cp {
 
 typedef double dbl4 __attribute__((ext_vector_type(4)));
 
-constexpr int NB = 64;  // panel width
+constexpr int NB = 64;   // diagonal block and panel width
+constexpr int NW = 256;  // outer block-column width of the left-looking sweep
 
 // ---------------------------------------------------------------- fp64 MFMA GEMM
 // C[M,N] = alpha * A[M,K] * op(B) + beta * C, row-major with leading dims.
 // op(B) = B [K,N] or, with BT, B^T for B stored [N,K]. Batched over blockIdx.z
-// as z = z1 * nz2 + z2 with separate strides per level. LOWER skips tiles
-// strictly above the diagonal of C and writes only C[i][j] with i >= j.
-// Tile 64x64x16, 4 waves of 32x32 each built from v_mfma_f64_16x16x4f64.
-// tri: bit 0 -- A is lower triangular (A[r][k] = 0 for k > r), so output row
-// tile bm only needs k < bm + 64; bit 1 -- B ([K,N], not transposed) is lower
-// triangular (B[k][c] = 0 for k < c), so output column tile bn needs k >= bn.
+// as z = z1 * nz2 + z2 with separate strides per level.
+//
+// Block tile BM x 64 (BM = 64 or 128), K tile 16; the 4 waves are stacked
+// along M, each BM/4 x 64 built from v_mfma_f64_16x16x4f64. The next K tile is
+// fetched into registers while the current one is multiplied, then stored into
+// the other half of a double-buffered LDS, so one barrier separates K tiles.
+// Within a K tile, lane group g = lane/16 supplies k = 4g + s to MFMA step s
+// (the MFMA sums over g, and any fixed assignment of the 16 k values to (g, s)
+// gives the same sum of products), which lets a lane fetch the four A values of
+// a fragment with two 16-byte LDS reads.
+//
+// tri: bit 0 -- A is lower triangular (A[r][k] = 0 for k > r), so row tile bm
+// only needs k < bm + BM; bit 1 -- B ([K,N], not transposed) is lower
+// triangular (B[k][c] = 0 for k < c), so column tile bn needs k >= bn; bit 2 --
+// C above the diagonal is not wanted, so tiles entirely above it are skipped.
+// The skipped K ranges are multiplied in at K-tile granularity, so the zeros of
+// a triangular operand must be stored.
 struct GemmArgs {
   const double* A;
   const double* B;
@@ -56,83 +70,180 @@ struct GemmArgs {
   int tri;
 };
 
-template <bool BT, bool LOWER>
+constexpr int GBK = 16;       // K tile
+constexpr int GLD = GBK + 2;  // LDS row of a [rows][K] tile: 144 B, fragment reads conflict-free
+constexpr int GNLD = 64 + 4;  // LDS row of a [K][64] tile: 544 B, lane groups 4 rows apart land
+                              // in opposite halves of the banks
+
+// p[0], p[1] at column indices c, c + 1, zero where the row is out of range
+// (!ok) or the column reaches lim. VEC: p is 16-byte aligned.
+template <bool VEC>
+__device__ inline double2 ld_pair(const double* p, bool ok, int c, int lim) {
+  double2 v;
+  if (VEC && ok && c + 1 < lim) {
+    v = *reinterpret_cast<const double2*>(p);
+  } else {
+    v.x = (ok && c < lim) ? p[0] : 0.0;
+    v.y = (ok && c + 1 < lim) ? p[1] : 0.0;
+  }
+  return v;
+}
+
+template <bool BT, int BM, bool VEC>
 __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
-  __shared__ double As[16][64 + 1];
-  __shared__ double Bs[16][64 + 1];
+  constexpr int TI = BM / 64;  // 16-row MFMA tiles per wave
+  constexpr int AQ = BM / 32;  // A-tile pairs fetched per thread
+  constexpr int BROWS = BT ? 64 : GBK;
+  constexpr int BLD = BT ? GLD : GNLD;
+  __shared__ __align__(16) double As[2][BM][GLD];
+  __shared__ __align__(16) double Bs[2][BROWS][BLD];
   const int z1 = blockIdx.z / g.nz2, z2 = blockIdx.z % g.nz2;
   const double* A = g.A + z1 * g.sA1 + z2 * g.sA2;
   const double* B = g.B + z1 * g.sB1 + z2 * g.sB2;
   double* C = g.C + z1 * g.sC1 + z2 * g.sC2;
-  const int bm = blockIdx.y * 64, bn = blockIdx.x * 64;
-  if (LOWER && bn > bm + 63) return;
-  const int t = threadIdx.x, w = t >> 6, l = t & 63;
-  const int wm = (w >> 1) * 32, wn = (w & 1) * 32;
-  dbl4 acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = dbl4{0.0, 0.0, 0.0, 0.0};
+  const int bm = blockIdx.y * BM, bn = blockIdx.x * 64;
+  if ((g.tri & 4) && bn >= bm + BM) return;
+  const int t = threadIdx.x, l = t & 63, wm = (t >> 6) * (BM / 4);
+  const int lr = l & 15, lg = l >> 4;
+  // loader coordinates: [rows][K] tiles as (row t/8 + 32q, k pair t%8),
+  // [K][64] tiles as (k t/32 + 8q, column pair t%32)
+  const int tr = t >> 3, tk = (t & 7) * 2;
+  const int nr = t >> 5, nc = (t & 31) * 2;
 
-  const int kbeg = (g.tri & 2) ? (bn & ~15) : 0;
-  const int kend = (g.tri & 1) ? min(g.K, bm + 64) : g.K;
-  for (int k0 = kbeg; k0 < kend; k0 += 16) {
+  dbl4 acc[TI][4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      int idx = t + 256 * q;
-      int r = idx >> 4, c = idx & 15;
-      int gr = bm + r, gc = k0 + c;
-      As[c][r] = (gr < g.M && gc < g.K) ? A[(int64_t)gr * g.lda + gc] : 0.0;
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = dbl4{0.0, 0.0, 0.0, 0.0};
+
+  const int kbeg = (g.tri & 2) ? (bn & ~(GBK - 1)) : 0;
+  const int kend = (g.tri & 1) ? min(g.K, bm + BM) : g.K;
+  const int nt = kend > kbeg ? (kend - kbeg + GBK - 1) / GBK : 0;
+
+  double2 ra[AQ], rb[2];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < AQ; ++q) {
+      const int r = bm + tr + 32 * q;
+      ra[q] = ld_pair<VEC>(A + (int64_t)r * g.lda + k0 + tk, r < g.M, k0 + tk, g.K);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
       if (BT) {
-        int gn = bn + r;
-        Bs[c][r] = (gn < g.N && gc < g.K) ? B[(int64_t)gn * g.ldb + gc] : 0.0;
+        const int r = bn + tr + 32 * q;
+        rb[q] = ld_pair<VEC>(B + (int64_t)r * g.ldb + k0 + tk, r < g.N, k0 + tk, g.K);
       } else {
-        int c2 = idx >> 6, r2 = idx & 63;
-        int gk = k0 + c2, gn = bn + r2;
-        Bs[c2][r2] = (gk < g.K && gn < g.N) ? B[(int64_t)gk * g.ldb + gn] : 0.0;
+        const int k = k0 + nr + 8 * q;
+        rb[q] = ld_pair<VEC>(B + (int64_t)k * g.ldb + bn + nc, k < g.K, bn + nc, g.N);
       }
     }
-    __syncthreads();
+  };
+  auto stash = [&](int b) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int kr = kk * 4 + (l >> 4);
-      double a0 = As[kr][wm + (l & 15)], a1 = As[kr][wm + 16 + (l & 15)];
-      double b0 = Bs[kr][wn + (l & 15)], b1 = Bs[kr][wn + 16 + (l & 15)];
-      acc[0][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
+    for (int q = 0; q < AQ; ++q) *reinterpret_cast<double2*>(&As[b][tr + 32 * q][tk]) = ra[q];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      if (BT)
+        *reinterpret_cast<double2*>(&Bs[b][tr + 32 * q][tk]) = rb[q];
+      else
+        *reinterpret_cast<double2*>(&Bs[b][nr + 8 * q][nc]) = rb[q];
     }
+  };
+
+  if (nt > 0) {
+    fetch(kbeg);
+    stash(0);
+  }
+  __syncthreads();
+  for (int it = 0; it < nt; ++it) {
+    const int b = it & 1;
+    if (it + 1 < nt) fetch(kbeg + (it + 1) * GBK);
+    double af[TI][4], bf[4][4];
+#pragma unroll
+    for (int ti = 0; ti < TI; ++ti) {
+      const double2* p = reinterpret_cast<const double2*>(&As[b][wm + 16 * ti + lr][4 * lg]);
+      const double2 u = p[0], v = p[1];
+      af[ti][0] = u.x;
+      af[ti][1] = u.y;
+      af[ti][2] = v.x;
+      af[ti][3] = v.y;
+    }
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj) {
+      if (BT) {
+        const double2* p = reinterpret_cast<const double2*>(&Bs[b][16 * tj + lr][4 * lg]);
+        const double2 u = p[0], v = p[1];
+        bf[tj][0] = u.x;
+        bf[tj][1] = u.y;
+        bf[tj][2] = v.x;
+        bf[tj][3] = v.y;
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) bf[tj][s] = Bs[b][4 * lg + s][16 * tj + lr];
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj)
+          acc[ti][tj] = __builtin_amdgcn_mfma_f64_16x16x4f64(af[ti][s], bf[tj][s], acc[ti][tj], 0, 0, 0);
+    if (it + 1 < nt) stash(b ^ 1);
     __syncthreads();
   }
 #pragma unroll
-  for (int ti = 0; ti < 2; ++ti)
+  for (int ti = 0; ti < TI; ++ti)
 #pragma unroll
-    for (int tj = 0; tj < 2; ++tj)
+    for (int tj = 0; tj < 4; ++tj)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         // v_mfma_f64_16x16x4f64 result: register r of lane l holds row 4r + l/16, column l%16
-        int i = bm + wm + ti * 16 + 4 * r + (l >> 4);
-        int j = bn + wn + tj * 16 + (l & 15);
-        if (i < g.M && j < g.N && (!LOWER || i >= j)) {
+        const int i = bm + wm + 16 * ti + 4 * r + lg;
+        const int j = bn + 16 * tj + lr;
+        if (i < g.M && j < g.N) {
           double* p = C + (int64_t)i * g.ldc + j;
-          double v = g.alpha * acc[ti][tj][r];
+          const double v = g.alpha * acc[ti][tj][r];
           *p = g.beta == 0.0 ? v : v + g.beta * *p;
         }
       }
 }
 
-static int dgemm(const GemmArgs& a, int nz1, bool bt, bool lower, hipStream_t st) {
-  if (a.M <= 0 || a.N <= 0) return CP_OK;
-  dim3 grid((a.N + 63) / 64, (a.M + 63) / 64, nz1 * a.nz2);
-  if (bt) {
-    if (lower) dgemm_kernel<true, true><<<grid, 256, 0, st>>>(a);
-    else dgemm_kernel<true, false><<<grid, 256, 0, st>>>(a);
-  } else {
-    if (lower) dgemm_kernel<false, true><<<grid, 256, 0, st>>>(a);
-    else dgemm_kernel<false, false><<<grid, 256, 0, st>>>(a);
+template <bool BT, int BM>
+static void launch_gemm(const GemmArgs& a, dim3 grid, bool vec, hipStream_t st) {
+  if (vec)
+    dgemm_kernel<BT, BM, true><<<grid, 256, 0, st>>>(a);
+  else
+    dgemm_kernel<BT, BM, false><<<grid, 256, 0, st>>>(a);
+}
+
+// every (z1, z2) base of the operand is 16-byte aligned and so are its rows
+static bool pairs_aligned(const double* p, int ld, int64_t s1, int64_t s2) {
+  return aligned(p, 16) && !(ld & 1) && !(s1 & 1) && !(s2 & 1);
+}
+
+static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
+  if (a0.M <= 0 || a0.N <= 0 || nz1 <= 0) return CP_OK;
+  const bool vec = pairs_aligned(a0.A, a0.lda, a0.sA1, a0.sA2) &&
+                   pairs_aligned(a0.B, a0.ldb, a0.sB1, a0.sB2);
+  const int nt = (a0.N + 63) / 64;
+  // 128-row tiles when they still give two blocks per CU, 64-row ones otherwise
+  const bool big = (int64_t)nt * ((a0.M + 127) / 128) * nz1 * a0.nz2 >= 512;
+  const int bm = big ? 128 : 64;
+  const int chunk = 65535 / a0.nz2;  // grid.z limit
+  for (int z0 = 0; z0 < nz1; z0 += chunk) {
+    GemmArgs a = a0;
+    a.A += z0 * a0.sA1;
+    a.B += z0 * a0.sB1;
+    a.C += z0 * a0.sC1;
+    const int nz = (nz1 - z0 < chunk ? nz1 - z0 : chunk) * a0.nz2;
+    const dim3 grid(nt, (a.M + bm - 1) / bm, nz);
+    if (bt)
+      big ? launch_gemm<true, 128>(a, grid, vec, st) : launch_gemm<true, 64>(a, grid, vec, st);
+    else
+      big ? launch_gemm<false, 128>(a, grid, vec, st) : launch_gemm<false, 64>(a, grid, vec, st);
+    CP_LAUNCHED("fp64 GEMM launch");
   }
-  CP_LAUNCHED("fp64 GEMM launch");
   return CP_OK;
 }
 
@@ -209,62 +320,107 @@ __global__ void fact_prepare_kernel(const T* H, int n, int64_t sH, const int* or
 }
 
 // ---------------------------------------------------------------- diagonal block
-// Factor the nb x nb diagonal block at (k, k) in LDS, write L_kk back to A and
-// inv(L_kk) into the matching diagonal block of X; flag a bad pivot.
+// Factor the nb x nb diagonal block at (k, k) (nb = min(64, n - k)), write L_kk
+// back to A and inv(L_kk) into the matching diagonal block of X; flag a bad
+// pivot. A partial last block is padded with identity rows.
+//
+// Four waves per matrix; lane i of wave w keeps entries (i, 4m + w), m < 16, in
+// registers. Cholesky is right-looking by columns: the wave owning column j
+// takes the pivot from lane j, scales the column and publishes it through LDS;
+// after one barrier every wave subtracts L[i][j] L[c][j] from its columns
+// c > j, reading L[c][j] from lane c by readlane. Entries above the diagonal
+// collect finite garbage on the way and are never stored. The inverse is
+// column-oriented forward substitution with the same layout turned round: lane
+// i solves for column i of inv(L_kk), wave w owns its rows 4m + w, and the
+// owner of row r publishes x_r before the others eliminate it.
+__device__ inline double readlane_f64(double v, int lane) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, lane);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), lane);
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
 __global__ __launch_bounds__(256) void fact_diag_kernel(double* A, int64_t sA, double* X,
                                                         int64_t sX, int n, int k, int* fail,
                                                         const int* active) {
-  __shared__ double a[NB][NB + 1];
-  __shared__ double x[NB][NB + 1];
+  __shared__ double L[NB][NB + 1];
+  __shared__ double pub[2][NB];
   const int z = blockIdx.x;
   if (active && !active[z]) return;
   const int nb = min(NB, n - k);
   double* Ak = A + z * sA + (int64_t)k * n + k;
   double* Xk = X + z * sX + (int64_t)k * n + k;
-  const int t = threadIdx.x;
-  for (int idx = t; idx < NB * NB; idx += 256) {
-    int i = idx / NB, j = idx % NB;
-    a[i][j] = (i < nb && j <= i) ? Ak[(int64_t)i * n + j] : 0.0;
+  const int t = threadIdx.x, i = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  {
+    double v[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int r = 4 * q + w;
+      v[q] = r == i ? 1.0 : 0.0;
+      if (r < nb && i < nb && i <= r) v[q] = Ak[(int64_t)r * n + i];
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) L[4 * q + w][i] = v[q];
   }
   __syncthreads();
-  __shared__ int bad;
-  if (t == 0) bad = 0;
+  double a[16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) a[m] = L[i][4 * m + w];
+
+  int bad = 0;
+#pragma unroll
+  for (int J = 0; J < 16; ++J) {
+#pragma unroll
+    for (int jw = 0; jw < 4; ++jw) {
+      const int j = 4 * J + jw;
+      if (w == jw) {
+        const double piv = readlane_f64(a[J], j);
+        bad |= !(piv > 0.0);
+        const double d = sqrt(piv > 0.0 ? piv : 1.0);
+        const double v = i > j ? a[J] * (1.0 / d) : (i == j ? d : 0.0);
+        a[J] = v;
+        pub[j & 1][i] = v;
+      }
+      __syncthreads();
+      const double vi = pub[j & 1][i];
+      if (w > jw) a[J] = __builtin_fma(-vi, readlane_f64(vi, 4 * J + w), a[J]);
+#pragma unroll
+      for (int m = J + 1; m < 16; ++m) a[m] = __builtin_fma(-vi, readlane_f64(vi, 4 * m + w), a[m]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 16; ++m) L[i][4 * m + w] = a[m];
   __syncthreads();
-  for (int j = 0; j < nb; ++j) {
-    if (t == 0) {
-      double v = a[j][j];
-      if (!(v > 0.0)) bad = 1;
-      a[j][j] = sqrt(v > 0.0 ? v : 1.0);
-    }
-    __syncthreads();
-    const double piv = a[j][j];
-    for (int i = j + 1 + t; i < nb; i += 256) a[i][j] = a[i][j] / piv;
-    __syncthreads();
-    const int m = nb - j - 1;
-    for (int idx = t; idx < m * m; idx += 256) {
-      int i = j + 1 + idx / m, c = j + 1 + idx % m;
-      if (c <= i) a[i][c] = a[i][c] - a[i][j] * a[c][j];
-    }
-    __syncthreads();
-  }
-  // inverse of the lower-triangular block, one column per thread
-  if (t < nb) {
-    const int c = t;
-    for (int i = 0; i < c; ++i) x[i][c] = 0.0;
-    x[c][c] = 1.0 / a[c][c];
-    for (int i = c + 1; i < nb; ++i) {
-      double s = 0.0;
-      for (int kk = c; kk < i; ++kk) s = s + a[i][kk] * x[kk][c];
-      x[i][c] = -s / a[i][i];
+
+  // a[m] now accumulates row 4m + w of column i of inv(L_kk)
+#pragma unroll
+  for (int m = 0; m < 16; ++m) a[m] = 4 * m + w == i ? 1.0 : 0.0;
+#pragma unroll
+  for (int J = 0; J < 16; ++J) {
+#pragma unroll
+    for (int jw = 0; jw < 4; ++jw) {
+      const int r = 4 * J + jw;
+      if (w == jw) {
+        a[J] = a[J] / L[r][r];
+        pub[r & 1][i] = a[J];
+      }
+      __syncthreads();
+      const double xr = pub[r & 1][i];
+      if (w > jw) a[J] = __builtin_fma(-L[4 * J + w][r], xr, a[J]);
+#pragma unroll
+      for (int m = J + 1; m < 16; ++m) a[m] = __builtin_fma(-L[4 * m + w][r], xr, a[m]);
     }
   }
-  __syncthreads();
-  for (int idx = t; idx < nb * nb; idx += 256) {
-    int i = idx / nb, j = idx % nb;
-    Ak[(int64_t)i * n + j] = j <= i ? a[i][j] : 0.0;
-    Xk[(int64_t)i * n + j] = x[i][j];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int r = 4 * m + w;
+    if (r < nb && i < nb) {
+      Xk[(int64_t)r * n + i] = a[m];
+      Ak[(int64_t)r * n + i] = i <= r ? L[r][i] : 0.0;
+    }
   }
-  if (t == 0 && bad) fail[z] = 1;
+  if (i == 0 && bad) fail[z] = 1;
 }
 
 // U[i][j] = X[n-1-i][n-1-j] for i <= j, 0 below the diagonal (OutT = float:
@@ -350,25 +506,36 @@ static int fact_run(const T* H, int64_t sH, int n, int batch, const int* order, 
     fact_prepare_kernel<T><<<dim3((n + 63) / 64, (n + 3) / 4, batch), 256, 0, st>>>(
         H, n, sH, order, sO, shift, A, sA, active);
     CP_LAUNCHED("factor prepare");
-    // left-looking: block column k first receives all earlier columns' updates
-    // in one large-K GEMM, then its diagonal block is factored and the panel
-    // below it solved
-    for (int k = 0; k < n; k += NB) {
-      const int w = n - k < NB ? n - k : NB;
-      if (k > 0) {
-        // A[k:, k:k+w] -= L[k:, 0:k] * L[k:k+w, 0:k]^T
-        GemmArgs ga{A + (int64_t)k * n, A + (int64_t)k * n, A + (int64_t)k * n + k, n - k, w, k,
-                    n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 0};
-        if (int s = dgemm(ga, batch, true, false, st)) return s;
+    // left-looking in two levels: an NW-wide block column first receives all
+    // earlier columns' updates in one large-K GEMM; inside it, each NB-wide
+    // column receives its left neighbours' updates, then its diagonal block is
+    // factored and the panel below it solved
+    for (int k0 = 0; k0 < n; k0 += NW) {
+      const int w0 = n - k0 < NW ? n - k0 : NW;
+      if (k0 > 0) {
+        // A[k0:, k0:k0+w0] -= L[k0:, 0:k0] * L[k0:k0+w0, 0:k0]^T, lower part
+        GemmArgs ga{A + (int64_t)k0 * n, A + (int64_t)k0 * n, A + (int64_t)k0 * n + k0, n - k0, w0,
+                    k0, n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 4};
+        if (int s = dgemm(ga, batch, true, st)) return s;
       }
-      fact_diag_kernel<<<batch, 256, 0, st>>>(A, sA, X, sA, n, k, fail, active);
-      CP_LAUNCHED("factor diagonal block");
-      const int m = n - k - NB;
-      if (m <= 0) break;
-      // panel: A[k+NB:, k:k+NB] <- A[k+NB:, k:k+NB] * inv(L_kk)^T  (in place, row tiles)
-      GemmArgs pa{A + (int64_t)(k + NB) * n + k, X + (int64_t)k * n + k, A + (int64_t)(k + NB) * n + k,
-                  m, NB, NB, n, n, n, 1.0, 0.0, sA, sA, sA, 0, 0, 0, 1, 0};
-      if (int s = dgemm(pa, batch, true, false, st)) return s;
+      for (int k = k0; k < k0 + w0; k += NB) {
+        const int w = n - k < NB ? n - k : NB;
+        if (k > k0) {
+          // A[k:, k:k+w] -= L[k:, k0:k] * L[k:k+w, k0:k]^T
+          GemmArgs gb{A + (int64_t)k * n + k0, A + (int64_t)k * n + k0, A + (int64_t)k * n + k,
+                      n - k, w, k - k0, n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 0};
+          if (int s = dgemm(gb, batch, true, st)) return s;
+        }
+        fact_diag_kernel<<<batch, 256, 0, st>>>(A, sA, X, sA, n, k, fail, active);
+        CP_LAUNCHED("factor diagonal block");
+        const int m = n - k - NB;
+        if (m <= 0) break;
+        // panel: A[k+NB:, k:k+NB] <- A[k+NB:, k:k+NB] * inv(L_kk)^T  (in place, row tiles)
+        GemmArgs pa{A + (int64_t)(k + NB) * n + k, X + (int64_t)k * n + k,
+                    A + (int64_t)(k + NB) * n + k, m, NB, NB, n, n, n, 1.0, 0.0, sA, sA, sA,
+                    0, 0, 0, 1, 0};
+        if (int s = dgemm(pa, batch, true, st)) return s;
+      }
     }
     // L^{-1} by recursive doubling over neighbouring s-blocks
     for (int s = NB; s < n; s *= 2) {
@@ -383,11 +550,11 @@ static int fact_run(const T* H, int64_t sH, int n, int batch, const int* order, 
         // T_p = L21 X11
         GemmArgs g1{A + (int64_t)(b0 + s) * n + b0, X + (int64_t)b0 * n + b0, Tm, s2, s, s, n, n, s,
                     1.0, 0.0, sA, sA, (int64_t)nn, step, step, (int64_t)s * s, pairs, 2};
-        if (int e = dgemm(g1, batch, false, false, st)) return e;
+        if (int e = dgemm(g1, batch, false, st)) return e;
         // X21 = -X22 T_p
         GemmArgs g2{X + (int64_t)(b0 + s) * n + b0 + s, Tm, X + (int64_t)(b0 + s) * n + b0, s2, s, s2,
                     n, s, n, -1.0, 0.0, sA, (int64_t)nn, sA, step, (int64_t)s * s, step, pairs, 1};
-        if (int e = dgemm(g2, batch, false, false, st)) return e;
+        if (int e = dgemm(g2, batch, false, st)) return e;
       }
     }
     const dim3 og((n + 63) / 64, (n + 3) / 4, batch);

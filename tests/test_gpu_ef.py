@@ -40,7 +40,7 @@ def test_act_order_is_stable_descending(ef):
     assert np.array_equal(got, np.argsort(-d, kind="stable"))
 
 
-@pytest.mark.parametrize("n", [96, 200, 256, 1024])
+@pytest.mark.parametrize("n", [96, 200, 256, 777, 1024, 1500])
 def test_factor_matches_closed_form(ef, n):
     _say(f"factor n={n}")
     H = correlated_hessian(n, 4 * n, seed=n)
