@@ -9,16 +9,17 @@
 //   LT     [n][nrow] u8   stored codes (q - lo) per visited column
 //   dlT/mlT [n/sub][nrow] f32  committed grid step / offset per storage sub-block
 //
-// Sweep: one wavefront owns a stripe of 64 rows (lane = row) and walks the
+// Sweep (exact mode): one wavefront owns a stripe of 32 rows and walks the
 // visiting order in 64-column blocks. Left-looking: before a block is swept,
 // each of its elements receives the updates of all earlier columns,
 //     t -= e_jj * U[jj][k]   (float32 multiply, then subtract, jj ascending),
 // which is exactly the order in which ef.py:213 applies them, so the sweep is
-// bit-identical to the reference. U's row segments are wave-uniform and are
-// fetched through the scalar path; E is re-read from L2 by the same lanes that
-// wrote it, so stripes never synchronize with each other.
+// bit-identical to the reference. The products come from the matrix cores
+// (one rounding each), the subtractions from the VALU. E is re-read from L2 /
+// HBM by the wave that wrote it, so stripes never synchronize with each other.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "cp_device.h"
@@ -72,17 +73,24 @@ __device__ __forceinline__ float ld_lane(const float* p, int64_t i) { return ((G
 
 constexpr int SUBP = 16;  // sub-panel width inside a block
 
-// In-block part of the sweep for one lane (= one row), shared by both kernels.
+// The block's diagonal U tile, U[i1 + a][i1 + b], staged in LDS.
+template <int B>
+struct LdsTile {
+  const float (*su)[B];
+  __device__ __forceinline__ float operator()(int a, int b) const { return su[a][b]; }
+};
+
+// In-block part of the sweep for one lane (= one row), shared by the kernels.
 // On entry trow[k] (k < B, LDS, stride 1) holds the block's targets after all
-// earlier blocks' updates; su is the block's diagonal U tile (LDS, [B][B]).
+// earlier blocks' updates; su(a, b) reads the block's diagonal U tile.
 // The block is walked in sub-panels of SUBP columns, left-looking: a
 // sub-panel's columns first receive the updates of the block's earlier
 // columns (jj ascending), then are quantized and propagated among themselves.
 // Every element therefore still sees its updates one at a time in ascending
 // jj, as in ef.py:199-213. A consumed target slot trow[c] is reused for e_c.
-template <int B>
+template <int B, typename Tile>
 __device__ __forceinline__ void sweep_block(const SweepTask& tk, int i1, int r, int rr, bool valid,
-                                            float* trow, const float (*su)[B]) {
+                                            float* trow, const Tile su) {
   const int nrow = tk.nrow;
 #pragma unroll
   for (int s0 = 0; s0 < B; s0 += SUBP) {
@@ -93,7 +101,7 @@ __device__ __forceinline__ void sweep_block(const SweepTask& tk, int i1, int r, 
     for (int jj = 0; jj < s0; ++jj) {
       const float e = trow[jj];
 #pragma unroll
-      for (int c = 0; c < SUBP; ++c) ts[c] = ts[c] - e * su[jj][s0 + c];
+      for (int c = 0; c < SUBP; ++c) ts[c] = ts[c] - e * su(jj, s0 + c);
     }
 #pragma unroll
     for (int j = 0; j < SUBP; ++j) {
@@ -104,7 +112,7 @@ __device__ __forceinline__ void sweep_block(const SweepTask& tk, int i1, int r, 
       const bool nz = dl != 0.0f;
       const int q = nz ? clampi(rint_magic((ts[j] + ml) / dl), tk.lo, tk.hi) : 0;
       const float recon = dl * (float)q - ml;
-      const float e = nz ? (ts[j] - recon) / su[cb][cb] : 0.0f;
+      const float e = nz ? (ts[j] - recon) / su(cb, cb) : 0.0f;
       if (valid) {
         ((GlobFw)tk.E)[(int64_t)c * nrow + r] = e;
         ((GlobFw)tk.WcurT)[(int64_t)c * nrow + r] = ts[j];
@@ -112,9 +120,84 @@ __device__ __forceinline__ void sweep_block(const SweepTask& tk, int i1, int r, 
       }
       trow[cb] = e;
 #pragma unroll
-      for (int k = j + 1; k < SUBP; ++k) ts[k] = ts[k] - e * su[cb][s0 + k];
+      for (int k = j + 1; k < SUBP; ++k) ts[k] = ts[k] - e * su(cb, s0 + k);
     }
   }
+}
+
+// In-block sweep with the lane's row of the block in registers (lane = row),
+// right-looking: ts[k] holds the target of column cb + k, so the column being
+// quantized is always ts[0], and subtracting e_cb * U[cb][cb + k] from ts[k]
+// moves it to ts[k - 1] in the same step. Each element still receives its
+// updates one at a time in ascending column order (ef.py:199-213). sud is the
+// block's diagonal U tile aligned at the diagonal, sud[a][k] = U[i1 + a][i1 + a
+// + k] (zero past the tile). The grid step and offset of column cb + EF_Q are
+// fetched into the ring slot that column cb frees (slot = cb % EF_Q, static
+// inside the unrolled group, so no slot is copied while its load is in flight).
+constexpr int EF_Q = 2;
+
+// Columns cb0 .. cb0 + 15 of the block; only queue positions below KMAX still
+// hold columns of the block (KMAX = B - cb0).
+template <int KMAX, int B>
+__device__ __forceinline__ void sweep_cols(const SweepTask& tk, int i1, int r, int rr, bool valid,
+                                           float (&ts)[B], const float (*sud)[B], const int* sbo,
+                                           int cb0, float (&dq)[EF_Q], float (&mq)[EF_Q]) {
+  const int nrow = tk.nrow;
+#pragma unroll 1
+  for (int h = 0; h < 16; h += EF_Q) {
+#pragma unroll
+    for (int j = 0; j < EF_Q; ++j) {
+      const int cb = cb0 + h + j, c = i1 + cb;
+      const float dl = dq[j], ml = mq[j];
+      if (cb + EF_Q < B) {
+        const int64_t o = (int64_t)sbo[cb + EF_Q] + rr;
+        dq[j] = ld_lane(tk.dlT, o);
+        mq[j] = tk.mlT ? ld_lane(tk.mlT, o) : 0.0f;
+      }
+      const float4* urow = reinterpret_cast<const float4*>(sud[cb]);
+      const float4 u0 = urow[0];
+      const bool nz = dl != 0.0f;
+      const int q = nz ? clampi(rint_magic((ts[0] + ml) / dl), tk.lo, tk.hi) : 0;
+      const float recon = dl * (float)q - ml;
+      const float e = nz ? (ts[0] - recon) / u0.x : 0.0f;
+      if (valid) {
+        ((GlobFw)tk.E)[(int64_t)c * nrow + r] = e;
+        ((GlobFw)tk.WcurT)[(int64_t)c * nrow + r] = ts[0];
+        ((GlobBw)tk.LT)[(int64_t)c * nrow + r] = (uint8_t)(q - tk.lo);
+      }
+      ts[0] = ts[1] - e * u0.y;
+      ts[1] = ts[2] - e * u0.z;
+      ts[2] = ts[3] - e * u0.w;
+#pragma unroll
+      for (int k4 = 1; k4 < KMAX / 4; ++k4) {
+        const float4 u = urow[k4];
+        ts[4 * k4 - 1] = ts[4 * k4] - e * u.x;
+        ts[4 * k4] = ts[4 * k4 + 1] - e * u.y;
+        ts[4 * k4 + 1] = ts[4 * k4 + 2] - e * u.z;
+        ts[4 * k4 + 2] = ts[4 * k4 + 3] - e * u.w;
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one column's tile row in registers at a time
+    }
+  }
+}
+
+// sbo[k] = (storage sub-block of column i1 + k) * nrow, staged in LDS so that
+// the grid fetches wait on nothing but LDS.
+template <int B>
+__device__ __forceinline__ void sweep_block_rl(const SweepTask& tk, int i1, int r, int rr, bool valid,
+                                               float (&ts)[B], const float (*sud)[B], const int* sbo) {
+  static_assert(B == 64, "four 16-column pieces");
+  float dq[EF_Q], mq[EF_Q];
+#pragma unroll
+  for (int j = 0; j < EF_Q; ++j) {
+    const int64_t o = (int64_t)sbo[j] + rr;
+    dq[j] = ld_lane(tk.dlT, o);
+    mq[j] = tk.mlT ? ld_lane(tk.mlT, o) : 0.0f;
+  }
+  sweep_cols<64, B>(tk, i1, r, rr, valid, ts, sud, sbo, 0, dq, mq);
+  sweep_cols<48, B>(tk, i1, r, rr, valid, ts, sud, sbo, 16, dq, mq);
+  sweep_cols<32, B>(tk, i1, r, rr, valid, ts, sud, sbo, 32, dq, mq);
+  sweep_cols<16, B>(tk, i1, r, rr, valid, ts, sud, sbo, 48, dq, mq);
 }
 
 template <int B>
@@ -154,7 +237,7 @@ __global__ __launch_bounds__(256, 2) void ef_sweep_exact_kernel(const SweepTask*
     __syncthreads();
     load_diag_tile<B>(tk, i1, threadIdx.x, 256, su);
     __syncthreads();
-    sweep_block<B>(tk, i1, r, rr, valid, trow, su);
+    sweep_block<B>(tk, i1, r, rr, valid, trow, LdsTile<B>{su});
   }
 }
 
@@ -164,102 +247,113 @@ typedef float f32x32 __attribute__((ext_vector_type(32)));
 // Row of the 32x32 MFMA result held by register v of lane l (column = l % 32).
 __device__ __forceinline__ int mfma32_row(int v, int l) { return 8 * (v >> 2) + 4 * (l >> 5) + (v & 3); }
 
-// Exact mode on the matrix cores. One wave per 64-row stripe (lane = row in
-// the panel; grid: x = stripe, y = task). For every earlier column jj one
-// v_mfma_f32_32x32x1_2b_f32 forms the 64 x 32 outer product e_jj (x) U[jj][block]
-// with a -0.0 accumulator, i.e. each product rounded once to float32 --
-// exactly the fl(e * u) that np.outer forms -- and the VALU subtracts it from
-// the targets in jj order: t = fl(t - fl(e * u)), the reference's two roundings
-// in the reference's order. The targets live in the MFMA result layout during
-// this phase and move through LDS to one row per lane for the block's panel.
-template <int B>
-__global__ __launch_bounds__(64) void ef_sweep_xmfma_kernel(const SweepTask* __restrict__ tasks) {
-  static_assert(B == 32, "one 32-wide MFMA column tile per block");
+// Exact mode on the matrix cores with 32-row stripes and 64-column blocks.
+// One wave per 32-row stripe: a stripe's cross-block work is a sequential
+// chain (every column of a row depends on all earlier ones), and a 32-row
+// stripe halves that chain's length per wave against a 64-row one. For every
+// earlier column jj one v_mfma_f32_32x32x1_2b_f32 forms the 32 x 64 products
+// e_jj (x) U[jj][block] -- block 0 of the instruction takes columns 0-31, block 1
+// columns 32-63, both for the stripe's 32 rows -- with the inline-zero
+// accumulator (each product rounded once to float32), and the VALU subtracts
+// them in jj order; the products for jj + 1 are formed while those for jj are
+// subtracted. E and U for the next 8 columns are loaded while the current 8 are
+// applied. The in-block sweep runs on lanes 0-31 (lane = row), reading the
+// diagonal U tile through the scalar path.
+__global__ __launch_bounds__(64, 2) void ef_sweep_r32_kernel(const SweepTask* __restrict__ tasks) {
+  constexpr int B = 64, G = 8;
   const SweepTask tk = tasks[blockIdx.y];
-  const int row0 = blockIdx.x * 64;
+  const int row0 = blockIdx.x * 32;
   if (row0 >= tk.nrow) return;
-  const int l = threadIdx.x;
+  const int l = threadIdx.x, cl = l & 31, half = l >> 5;
   const int nrow = tk.nrow, n = tk.n;
-  const int r = row0 + l;
+  const int r = row0 + cl;
   const bool valid = r < nrow;
   const int rr = valid ? r : nrow - 1;
-  __shared__ float su[B][B];
-  __shared__ float st[64][B + 1];
-  float* trow = st[l];
-  const int cl = l & 31;
+  // one LDS buffer: the 32 x 64 target transpose, then the diagonal U tile
+  // aligned at its diagonal
+  __shared__ __align__(16) float lds[B * B];
+  __shared__ int sbo[B];
+  float (*st)[B + 1] = reinterpret_cast<float (*)[B + 1]>(lds);
+  float (*su)[B] = reinterpret_cast<float (*)[B]>(lds);
+  float* trow = st[cl];
   for (int i1 = 0; i1 < n; i1 += B) {
-    // targets into the MFMA layout: block b, register v -> row b*32 + mfma32_row(v, l), col cl
+    // targets: lane l stages row cl, columns 32*half .. +31; then into the MFMA
+    // layout: register v -> row mfma32_row(v % 16, l), column 32 * (v / 16) + cl
 #pragma unroll
-    for (int k = 0; k < B; ++k) trow[k] = ld_lane(tk.WpT, (int64_t)(i1 + k) * nrow + rr);
+    for (int k = 0; k < 32; ++k)
+      trow[32 * half + k] = ld_lane(tk.WpT, (int64_t)(i1 + 32 * half + k) * nrow + rr);
     __syncthreads();
-    float tv[32];
+    f32x32 t;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      tv[v] = st[mfma32_row(v, l)][cl];
-      tv[16 + v] = st[32 + mfma32_row(v, l)][cl];
+      t[v] = st[mfma32_row(v, l)][cl];
+      t[16 + v] = st[mfma32_row(v, l)][32 + cl];
     }
-    // products for column jj+1 are formed while column jj's are subtracted; the
-    // accumulator operand is the inline constant 0, so fl(0 + e*u) = fl(e*u)
-    // except that an exactly-zero product comes back as +0.0: only the sign of
-    // a zero target can differ, which no code, byte or non-zero value sees.
     const f32x32 nz = {};
     if (i1 > 0) {
-      // columns in groups of 4 (i1 is a multiple of 32); the next group's
-      // operands are loaded one group ahead, results ping-pong between P0/P1
-      float ea[4], ua[4], eb[4], ub[4];
-      auto load = [&](int g, float (&e)[4], float (&u)[4]) {
+      float ea[G], ua[G], eb[G], ub[G];
+      auto load = [&](int g, float (&e)[G], float (&u)[G]) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int64_t jj = (int64_t)g * 4 + q;
+        for (int q = 0; q < G; ++q) {
+          const int64_t jj = (int64_t)g * G + q;
           e[q] = ld_lane(tk.E, jj * nrow + rr);
-          u[q] = ld_lane(tk.U, jj * n + i1 + cl);
+          u[q] = ld_lane(tk.U, jj * n + i1 + l);
         }
       };
-      const int groups = i1 / 4;
+      const int groups = i1 / G;
       load(0, ea, ua);
+#pragma unroll
+      for (int q = 0; q < G; ++q) eb[q] = ub[q] = 0.0f;
       f32x32 P0 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[0], ua[0], nz, 0, 0, 0), P1;
-      for (int g = 0; g + 1 < groups; ++g) {
-        load(g + 1, eb, ub);
-        P1 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[1], ua[1], nz, 0, 0, 0);
+      for (int g = 0; g < groups; ++g) {
+        if (g + 1 < groups) load(g + 1, eb, ub);
 #pragma unroll
-        for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P0[v];
-        P0 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[2], ua[2], nz, 0, 0, 0);
+        for (int q = 0; q < G; q += 2) {
+          // P0 holds column g*G + q, P1 column g*G + q + 1; the last group's
+          // final products are unused
+          P1 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[q + 1], ua[q + 1], nz, 0, 0, 0);
 #pragma unroll
-        for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P1[v];
-        P1 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[3], ua[3], nz, 0, 0, 0);
+          for (int v = 0; v < 32; ++v) t[v] = t[v] - P0[v];
+          P0 = __builtin_amdgcn_mfma_f32_32x32x1f32(q + 2 < G ? ea[q + 2] : eb[0],
+                                                    q + 2 < G ? ua[q + 2] : ub[0], nz, 0, 0, 0);
 #pragma unroll
-        for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P0[v];
-        P0 = __builtin_amdgcn_mfma_f32_32x32x1f32(eb[0], ub[0], nz, 0, 0, 0);
+          for (int v = 0; v < 32; ++v) t[v] = t[v] - P1[v];
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);
+        }
 #pragma unroll
-        for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P1[v];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < G; ++q) {
           ea[q] = eb[q];
           ua[q] = ub[q];
         }
       }
-      // last group
-      P1 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[1], ua[1], nz, 0, 0, 0);
-#pragma unroll
-      for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P0[v];
-      P0 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[2], ua[2], nz, 0, 0, 0);
-#pragma unroll
-      for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P1[v];
-      P1 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[3], ua[3], nz, 0, 0, 0);
-#pragma unroll
-      for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P0[v];
-#pragma unroll
-      for (int v = 0; v < 32; ++v) tv[v] = tv[v] - P1[v];
     }
     __syncthreads();
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      st[mfma32_row(v, l)][cl] = tv[v];
-      st[32 + mfma32_row(v, l)][cl] = tv[16 + v];
+      st[mfma32_row(v, l)][cl] = t[v];
+      st[mfma32_row(v, l)][32 + cl] = t[16 + v];
     }
-    load_diag_tile<B>(tk, i1, l, 64, su);
     __syncthreads();
-    sweep_block<B>(tk, i1, r, rr, valid, trow, su);
+    float ts[B];
+#pragma unroll
+    for (int k = 0; k < B; ++k) ts[k] = trow[k];
+    __syncthreads();
+    // diagonal tile: lane l fills column l of the aligned rows, 16 loads in flight
+#pragma unroll
+    for (int a0 = 0; a0 < B; a0 += 16) {
+      float u[16];
+#pragma unroll
+      for (int a = 0; a < 16; ++a)
+        u[a] = a0 + a + l < B ? ld_lane(tk.U, (int64_t)(i1 + a0 + a) * n + i1 + a0 + a + l) : 0.0f;
+#pragma unroll
+      for (int a = 0; a < 16; ++a) su[a0 + a][l] = u[a];
+    }
+    sbo[l] = tk.sbidx[i1 + l] * nrow;
+    __syncthreads();
+    if (half == 0) sweep_block_rl<B>(tk, i1, r, rr, valid, ts, su, sbo);
     __syncthreads();
   }
 }
@@ -329,7 +423,7 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_mfma_kernel(const SweepTask* _
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < B; ++k) trow[k] = ld_lane(tk.WpT, (int64_t)(i1 + k) * nrow + rr) - trow[k];
-    sweep_block<B>(tk, i1, r, rr, valid, trow, su);
+    sweep_block<B>(tk, i1, r, rr, valid, trow, LdsTile<B>{su});
     __syncthreads();
   }
 }
@@ -563,7 +657,8 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     const cp_ef_tensor& t = ts[i];
     KqGeom g;
     if (!kq_geom(t.ttype, &g)) return set_error(CP_ERR_TTYPE, "tensor %d: unsupported type %d", i, t.ttype);
-    if (t.nrow <= 0 || t.n <= 0 || t.n % 256 || t.nrow > (1 << 30) || t.n > (1 << 20))
+    if (t.nrow <= 0 || t.n <= 0 || t.n % 256 || t.nrow > (1 << 30) || t.n > (1 << 20) ||
+        (t.n / 16) * t.nrow >= ((int64_t)1 << 31))
       return set_error(CP_ERR_SHAPE, "tensor %d: bad shape [%lld, %lld]", i, (long long)t.nrow, (long long)t.n);
     if (!t.x || !t.U || !t.order || !t.raw) return set_error(CP_ERR_ARG, "tensor %d: null pointer", i);
     if (!aligned(t.x, 16) || !aligned(t.raw, 4) || (t.qw && !aligned(t.qw, 16)) ||
@@ -599,10 +694,16 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     ef_to_visit_kernel<float><<<tg, 256, 0, st>>>(t.x, (int)t.nrow, (int)t.n,
                                                   (const int*)(base + L.inv), (float*)(base + L.WpT));
   }
+  // the sweep grid walks the task table in order: longest stripes (largest n)
+  // first, so they do not start last and set the tail
+  std::vector<int> by_len(count);
+  for (int i = 0; i < count; ++i) by_len[i] = i;
+  std::stable_sort(by_len.begin(), by_len.end(),
+                   [&](int a, int b) { return tasks[a].n > tasks[b].n; });
   for (int c0 = 0; c0 < count; c0 += kTasksPerLaunch) {
     const int cn = count - c0 < kTasksPerLaunch ? count - c0 : kTasksPerLaunch;
     SweepBatch b;
-    for (int i = 0; i < cn; ++i) b.t[i] = tasks[c0 + i];
+    for (int i = 0; i < cn; ++i) b.t[i] = tasks[by_len[c0 + i]];
     ef_tasks_store_kernel<<<1, 64, 0, st>>>(b, cn, dtasks + c0);
   }
   CP_LAUNCHED("EF setup");
@@ -625,7 +726,7 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     if (mode == CP_EF_EXACT_VALU)
       ef_sweep_exact_kernel<BLK><<<dim3((unsigned)((rows + 255) / 256), (unsigned)count), 256, 0, st>>>(dtasks);
     else if (mode == CP_EF_EXACT)
-      ef_sweep_xmfma_kernel<BLK><<<dim3((unsigned)((rows + 63) / 64), (unsigned)count), 64, 0, st>>>(dtasks);
+      ef_sweep_r32_kernel<<<dim3((unsigned)((rows + 31) / 32), (unsigned)count), 64, 0, st>>>(dtasks);
     else
       ef_sweep_mfma_kernel<BLK><<<dim3((unsigned)((rows + 63) / 64), (unsigned)count), 64, 0, st>>>(dtasks);
     CP_LAUNCHED("EF sweep");
