@@ -72,23 +72,32 @@ def hessian_phase(X, H, slot):
             xtx_accumulate(Xf, H[d][i])
 
 
-def ef_phase(W, H, slot, layers, mode):
+def ef_phase(W, H, slot, layers, mode, concurrent=True):
+    """Act order + factor per Hessian size class, then EF of that class's tensors.
+    With ``concurrent`` each size class runs on its own stream, so one class's
+    factorization overlaps another's sweep."""
     from perm_amd import ef as gef
     from perm_amd import workloads as wl
-    factor = {}
-    for d, Hb in H.items():
-        order = gef.act_order_dev(Hb)
-        U, _ = gef.factor_dev(Hb, order, 0.01)
-        factor[d] = (order, U)
-    items = []
-    for l in range(layers):
-        for name, _rows, _n, fam in wl.QWEN3_06B_LAYER:
-            d, i = slot[(l, fam)]
-            order, U = factor[d]
-            qw = H[d][i].diagonal() / float(ROWS)
-            items.append({"ttype": "Q2_K", "x": W[l][name], "qw": qw.contiguous(), "U": U[i],
-                          "order": order[i], "recon": True})
-    return gef.ef_encode_dev(items, n_iter=2, mode=mode)
+
+    def job(d):
+        def run():
+            Hb = H[d]
+            order = gef.act_order_dev(Hb)
+            U, _ = gef.factor_dev(Hb, order, 0.01)
+            items = []
+            for l in range(layers):
+                for name, _rows, _n, fam in wl.QWEN3_06B_LAYER:
+                    dd, i = slot[(l, fam)]
+                    if dd != d:
+                        continue
+                    qw = H[d][i].diagonal() / float(ROWS)
+                    items.append({"ttype": "Q2_K", "x": W[l][name], "qw": qw.contiguous(),
+                                  "U": U[i], "order": order[i], "recon": True})
+            return gef.ef_encode_dev(items, n_iter=2, mode=mode)
+        return run
+
+    jobs = [job(d) for d in sorted(H, reverse=True)]
+    return gef.run_concurrent(jobs) if concurrent else [j() for j in jobs]
 
 
 def cpu_baseline(W, H, slot, layers, total_weights):
@@ -180,34 +189,44 @@ def main():
     mode = _lib.CP_EF_MFMA if args.ef_mode == "mfma" else _lib.CP_EF_EXACT
     other = _lib.CP_EF_EXACT if mode == _lib.CP_EF_MFMA else _lib.CP_EF_MFMA
 
-    def step(profile):
+    def step():
         hs, he, ee = (torch.cuda.Event(enable_timing=True) for _ in range(3))
         hs.record()
         hessian_phase(X, H, slot)
         he.record()
-        lib.cp_ef_profile(1 if profile else 0)
         ef_phase(W, H, slot, layers, mode)
         ee.record()
-        lib.cp_ef_profile(0)
         return hs, he, ee
 
     for i in range(args.warmup):
-        step(False)
+        step()
         torch.cuda.synchronize()
         log(f"warmup {i + 1}/{args.warmup} done")
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    marks, phases = [], []
-    import ctypes
+    marks = []
     for i in range(args.steps):
-        marks.append(step(True))
-        buf = (ctypes.c_float * 5)()
-        lib.cp_ef_phase_ms(ctypes.cast(buf, ctypes.c_void_p), 5)
-        phases.append(list(buf))
+        marks.append(step())
         log(f"step {i + 1}/{args.steps} done")
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+
+    # after the timed region: one sequential EF pass with per-phase timing
+    import ctypes
+    p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    lib.cp_ef_profile(1)
+    p0.record()
+    phases = []
+    for d in sorted(H, reverse=True):
+        ef_phase(W, {d: H[d]}, slot, layers, mode, concurrent=False)
+        buf = (ctypes.c_float * 5)()
+        lib.cp_ef_phase_ms(ctypes.cast(buf, ctypes.c_void_p), 5)
+        phases.append(list(buf))
+    p1.record()
+    lib.cp_ef_profile(0)
+    torch.cuda.synchronize()
+    seq_ms = p0.elapsed_time(p1)
 
     # one untimed-by-contract step of the other EF mode, reported for comparison
     o0, o1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -219,14 +238,14 @@ def main():
 
     hess_ms = sum(hs.elapsed_time(he) for hs, he, _ in marks) / args.steps
     ef_ms = sum(he.elapsed_time(ee) for _, he, ee in marks) / args.steps
-    ph = [sum(p[k] for p in phases) / args.steps for k in range(5)]
+    ph = [sum(p[k] for p in phases) for k in range(5)]
     ms_per_step = wall * 1e3 / args.steps
     ef_mw = total_weights / (ef_ms * 1e-3) / 1e6
     hess_tflops = hess_flops / (hess_ms * 1e-3) / 1e12
 
     # dominant kernel: the Hessian MFMA kernel (one launch per Hessian) or the EF sweep
     hess_launches = 4 * layers
-    sweep_launches = 2
+    sweep_launches = 2 * len(H)  # sequential pass: two iterations per size class
     if hess_ms >= ph[2]:
         avg_ms = hess_ms / hess_launches
         flops_per_launch = hess_flops / hess_launches
@@ -262,8 +281,9 @@ def main():
                    "container": "Q2_K", "qw": "diag(H)/N", "n_iter": 2, "damp": 0.01,
                    "act_order": True, "ef_mode": args.ef_mode},
         "ef": {"ms": ef_ms, "mweights_per_s": ef_mw, "flops_update": ef_flops,
-               "phase_ms": {"factor_and_setup": ef_ms - sum(ph), "setup": ph[0],
-                            "commit": ph[1], "sweep": ph[2], "repack": ph[3], "decode": ph[4]},
+               "sequential_pass": {"ms": seq_ms, "phase_ms": {
+                   "factor_and_setup": seq_ms - sum(ph), "setup": ph[0], "commit": ph[1],
+                   "sweep": ph[2], "repack": ph[3], "decode": ph[4]}},
                "other_mode": {"mode": "exact" if mode == _lib.CP_EF_MFMA else "mfma",
                               "ms": other_ms,
                               "mweights_per_s": total_weights / (other_ms * 1e-3) / 1e6}},

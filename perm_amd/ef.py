@@ -139,31 +139,86 @@ def ef_encode(x, ttype, qw, H, n_iter=2, damp=0.01, act_order=True, mode="exact"
     return raw, rec
 
 
-def ef_encode_many(tensors, n_iter=2, damp=0.01, act_order=True, mode="exact"):
+_STREAMS = {}
+
+
+def run_concurrent(jobs):
+    """Run each callable on its own HIP stream and host thread.
+
+    The streams first wait for the work already queued on the caller's current
+    stream, and the current stream then waits for all of them, so the call
+    behaves like one ordered step. A job that blocks on its stream (the
+    factorization reads its failure flags) does not hold up the others: ctypes
+    releases the interpreter lock during library calls. Streams keep the
+    default priority and are reused across calls (the caching allocator keeps
+    their workspaces). Returns the jobs' results in order; re-raises the first
+    error."""
+    import threading
+    cur = torch.cuda.current_stream()
+    dev = torch.cuda.current_device()
+    streams = []
+    for k in range(len(jobs)):
+        s = _STREAMS.get((dev, k))
+        if s is None:
+            s = _STREAMS[(dev, k)] = torch.cuda.Stream()
+        s.wait_stream(cur)
+        streams.append(s)
+    results, errors = [None] * len(jobs), []
+
+    def work(k):
+        try:
+            torch.cuda.set_device(dev)
+            with torch.cuda.stream(streams[k]):
+                results[k] = jobs[k]()
+        except BaseException as e:  # re-raised in the caller's thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=work, args=(k,)) for k in range(len(jobs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    for s in streams:
+        cur.wait_stream(s)
+    if errors:
+        raise errors[0]
+    return results
+
+
+def ef_encode_many(tensors, n_iter=2, damp=0.01, act_order=True, mode="exact", concurrent=True):
     """EF-encode many tensors in one batched pass.
 
     tensors: list of dicts {name, ttype, x (CUDA f32), qw (CUDA f32 or None),
     H (CUDA f32/f64 [n, n])}. Tensors whose ``H`` is the same object share one
-    act order and one factorization (done batched per matrix size).
+    act order and one factorization (done batched per matrix size). Each size
+    class (its factorization, then the EF of its tensors) runs on its own
+    stream, so one class's factorization overlaps another's sweep.
     Returns {name: (raw, recon)}."""
-    # distinct Hessians, grouped by size for batched factorization
     hs = {}
     for t in tensors:
         hs.setdefault(id(t["H"]), t["H"])
     by_n = {}
     for key, H in hs.items():
         by_n.setdefault((H.shape[-1], H.dtype), []).append(key)
-    factor = {}
-    for (n, _dt), keys in by_n.items():
-        Hb = torch.stack([hs[k] for k in keys]) if len(keys) > 1 else hs[keys[0]].unsqueeze(0)
-        order = act_order_dev(Hb.contiguous(), act_order)
-        U, _ = factor_dev(Hb.contiguous(), order, damp)
-        for i, k in enumerate(keys):
-            factor[k] = (U[i], order[i])
-    items = []
-    for t in tensors:
-        U, order = factor[id(t["H"])]
-        items.append({"ttype": t["ttype"], "x": t["x"], "qw": t.get("qw"), "U": U,
-                      "order": order, "recon": t.get("recon", True)})
-    outs = ef_encode_dev(items, n_iter, MODES[mode])
-    return {t["name"]: o for t, o in zip(tensors, outs)}
+
+    def job(keys):
+        def run():
+            Hb = torch.stack([hs[k] for k in keys]) if len(keys) > 1 else hs[keys[0]].unsqueeze(0)
+            order = act_order_dev(Hb.contiguous(), act_order)
+            U, _ = factor_dev(Hb.contiguous(), order, damp)
+            slot = {k: i for i, k in enumerate(keys)}
+            mine = [t for t in tensors if id(t["H"]) in slot]
+            items = [{"ttype": t["ttype"], "x": t["x"], "qw": t.get("qw"),
+                      "U": U[slot[id(t["H"])]], "order": order[slot[id(t["H"])]],
+                      "recon": t.get("recon", True)} for t in mine]
+            outs = ef_encode_dev(items, n_iter, MODES[mode])
+            return {t["name"]: o for t, o in zip(mine, outs)}
+        return run
+
+    # largest matrices first: their factorization is the longest chain
+    jobs = [job(keys) for _, keys in sorted(by_n.items(), key=lambda kv: -kv[0][0])]
+    res = run_concurrent(jobs) if concurrent else [j() for j in jobs]
+    out = {}
+    for r in res:
+        out.update(r)
+    return {t["name"]: out[t["name"]] for t in tensors}
