@@ -1,22 +1,16 @@
 // Input-Hessian accumulation H += X^T X on gfx950 MFMA (coldpress/hessians.py:137-154).
 //
 // X is [N, d] row-major activations (bf16 or f32), H is [d, d] float32 and is
-// accumulated in place (beta = 1), so hook batches can stream in.
+// accumulated in place (beta = 1), so hook batches can stream in. Split-K over
+// rows of X: N is 65536-131072 while d is 1024-14336, so the row dimension is
+// what fills 256 CUs. Each workgroup adds its finished tile into H with
+// float32 atomics (one per element per workgroup): the sum over row splits is
+// exact up to float32 rounding order.
 //
-// Tiling: a workgroup (4 waves) owns a 128x128 tile of H and a contiguous range
-// of rows of X (split-K over rows: N is 65536-131072 while d is 1024-14336, so
-// the row dimension is what fills 256 CUs). Each wave computes a 64x64 quadrant
-// with 2x2 MFMA 32x32 tiles. Per 32-row step the workgroup stages the two
-// 32x128 X panels (rows t, columns i-tile and j-tile) in LDS, double buffered.
-//
-//  bf16: v_mfma_f32_32x32x16_bf16 needs 8 consecutive rows t per lane for both
-//        operands, while X is channel-contiguous; each thread loads a 4(t) x
-//        8(i) block with 16-byte loads, transposes it in registers
-//        (v_perm_b32) and writes t-contiguous 8-byte runs into [i][t] LDS.
-//  f32:  v_mfma_f32_32x32x2f32 takes one t per lane, so the [t][i] panel is
-//        used as loaded.
-// The finished tile is added into H with float32 atomics (one per element per
-// workgroup): the sum over row splits is exact up to float32 rounding order.
+//  bf16: lower-triangle 256 x 256 tiles on v_mfma_f32_32x32x16_bf16, operands
+//        read transposed from LDS (hess_bf16_tri_kernel), then a mirror pass;
+//  f32:  128 x 128 tiles on v_mfma_f32_32x32x2f32, which takes one row t per
+//        lane, so the [t][i] panel is used as loaded.
 #include <hip/hip_runtime.h>
 
 #include "cp_host.h"
@@ -26,130 +20,149 @@ namespace cp {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int HT = 128;  // H tile edge
-constexpr int KT = 32;   // rows of X per step
+constexpr int HT = 128;  // f32 kernel: H tile edge
+constexpr int KT = 32;   // f32 kernel: rows of X per step
 
 // Row of the 32x32 MFMA result held by register v of lane l (column = l % 32).
 __device__ __forceinline__ int mfma32_row(int v, int l) { return 8 * (v >> 2) + 4 * (l >> 5) + (v & 3); }
 
 // ---------------------------------------------------------------- bf16 input
-// LDS panel for bf16: [HT][KT + 8] (padding breaks the 64-byte row stride)
-constexpr int KP = KT + 8;
-
-__device__ __forceinline__ void load_block_bf16(const uint16_t* __restrict__ X, int64_t N, int d,
-                                                int64_t t0, int c0, uint4 (&v)[4]) {
-  // rows t0..t0+3, channels c0..c0+7; d % 8 == 0 and c0 % 8 == 0, so the 8
-  // channels are either all inside the matrix or all outside. Out-of-range
-  // blocks load a clamped in-range address and are zeroed without branching.
-  const bool cin = c0 < d;
-  const int cc = cin ? c0 : 0;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int64_t t = t0 + q;
-    const bool ok = cin && t < N;
-    const int64_t tc = t < N ? t : N - 1;
-    uint4 x = *reinterpret_cast<const uint4*>(X + tc * d + cc);
-    v[q] = ok ? x : make_uint4(0, 0, 0, 0);
-  }
-}
-
-__device__ __forceinline__ void store_block_bf16(uint16_t* panel, int i0, int tl, const uint4 (&v)[4]) {
-  // transpose 4(t) x 8(i) -> for each i, 4 consecutive t (8 bytes)
-  const uint32_t w[4][4] = {{v[0].x, v[0].y, v[0].z, v[0].w},
-                            {v[1].x, v[1].y, v[1].z, v[1].w},
-                            {v[2].x, v[2].y, v[2].z, v[2].w},
-                            {v[3].x, v[3].y, v[3].z, v[3].w}};
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-    uint32_t lo = __builtin_amdgcn_perm(w[1][c >> 1], w[0][c >> 1], sel);
-    uint32_t hi = __builtin_amdgcn_perm(w[3][c >> 1], w[2][c >> 1], sel);
-    *reinterpret_cast<uint2*>(panel + (i0 + c) * KP + tl) = make_uint2(lo, hi);
-  }
-}
-
-__global__ __launch_bounds__(256) void hess_bf16_kernel(const uint16_t* __restrict__ X, int64_t N,
-                                                        int d, int64_t rows_per_split,
-                                                        float* __restrict__ H) {
-  __shared__ uint16_t sA[2][HT * KP];
-  __shared__ uint16_t sB[2][HT * KP];
-  const int ti = blockIdx.y, tj = blockIdx.x;
-  const int i0 = ti * HT, j0 = tj * HT;
-  const int64_t r0 = (int64_t)blockIdx.z * rows_per_split;
-  const int64_t r1 = min(N, r0 + rows_per_split);
-  if (r0 >= r1) return;
-  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-  const int wm = (w >> 1) * 64, wn = (w & 1) * 64;
-  // loader role: 128 threads per panel, each a 4(t) x 8(i) block
-  const bool loadsA = tid < 128;
-  const int lb = tid & 127;
-  const int lt = (lb >> 4) * 4;    // 0..28
-  const int lc = (lb & 15) * 8;    // 0..120
-  const int cbase = loadsA ? i0 : j0;
-
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
-
-  uint4 blk[4];
-  load_block_bf16(X, r1, d, r0 + lt, cbase + lc, blk);
-  store_block_bf16(loadsA ? sA[0] : sB[0], lc, lt, blk);
-  __syncthreads();
-  int buf = 0;
-  for (int64_t t0 = r0; t0 < r1; t0 += KT) {
-    const bool more = t0 + KT < r1;
-    if (more) load_block_bf16(X, r1, d, t0 + KT + lt, cbase + lc, blk);
-#pragma unroll
-    for (int kk = 0; kk < KT / 16; ++kk) {
-      const int koff = kk * 16 + 8 * (l >> 5);
-      bf16x8 a[2], b[2];
-#pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        a[x] = *reinterpret_cast<const bf16x8*>(&sA[buf][(wm + x * 32 + (l & 31)) * KP + koff]);
-        b[x] = *reinterpret_cast<const bf16x8*>(&sB[buf][(wn + x * 32 + (l & 31)) * KP + koff]);
-      }
-#pragma unroll
-      for (int x = 0; x < 2; ++x)
-#pragma unroll
-        for (int y = 0; y < 2; ++y)
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[x], b[y], acc[x][y], 0, 0, 0);
-    }
-    if (more) store_block_bf16(loadsA ? sA[buf ^ 1] : sB[buf ^ 1], lc, lt, blk);
-    __syncthreads();
-    buf ^= 1;
-  }
-#pragma unroll
-  for (int x = 0; x < 2; ++x)
-#pragma unroll
-    for (int y = 0; y < 2; ++y)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        int i = i0 + wm + x * 32 + mfma32_row(v, l);
-        int j = j0 + wn + y * 32 + (l & 31);
-        if (i < d && j < d) atomicAdd(H + (int64_t)i * d + j, acc[x][y][v]);
-      }
-}
-
-// ---------------------------------------------------------------- bf16, large tiles
 // Lower-triangle tiles of 256 x 256 (H is symmetric; hess_mirror_kernel copies
-// the lower triangle into the upper one afterwards). Each of the 8 waves owns
-// a 128 x 64 block as 4 x 2 MFMA 32x32 tiles (128 float32 accumulators), so a
-// 16-byte LDS fragment feeds 2 to 4 MFMAs; two waves share each SIMD. Work items
-// (row split, tile) are ordered split-major and handed out XCD-contiguously:
-// the hardware places workgroup w on XCD w % 8, so item = (w % 8) * per + w / 8
-// keeps the workgroups of one XCD on the same rows of X (shared in its L2).
-constexpr int BT = 256;
+// the lower triangle into the upper one afterwards), split-K over rows of X.
+// A workgroup is 4 waves, each owning a 128 x 128 block as 4 x 4 MFMA 32x32
+// tiles (256 float32 accumulators): the largest block a wave can hold, because
+// the LDS reads per MFMA, not the MFMAs, bound this kernel.
+//
+// Rows of X are staged 32 at a time: both 32 x 256 panels (columns of the i-
+// and j-tile; one panel on a diagonal tile) are fetched into registers two
+// stages ahead of use, stored into a 3-slot LDS ring in X's own [t][c] layout,
+// and read as MFMA operands with ds_read_b64_tr_b16, which returns 4
+// consecutive rows t of one column per lane: v_mfma_f32_32x32x16_bf16 takes 8
+// consecutive t per lane for both operands. Panel rows are 512 bytes, so the
+// four rows of one transposed read would share banks; 64-byte chunks are
+// XOR-swizzled by t & 3 to spread them over all banks.
+//
+// Work items (row split, tile) are ordered split-major and handed out
+// XCD-contiguously: the hardware places workgroup w on XCD w % 8, so
+// item = (w % 8) * per + w / 8 keeps the workgroups of one XCD on the same
+// rows of X (shared in its L2).
+constexpr int BT = 256;             // H tile edge
+constexpr int KS = 32;              // rows of X per stage
+constexpr int PROW = BT * 2;        // bytes per panel row
+constexpr int PANEL = KS * PROW;    // 16 KB
+constexpr int HNT = 256;            // threads per workgroup
+constexpr int NSLOT = 3;            // LDS ring
+constexpr int CPT = 2048 / HNT;     // 16-byte chunks per thread per stage (two panels)
 
-__global__ __launch_bounds__(512) void hess_bf16_tri_kernel(const uint16_t* __restrict__ X, int64_t N,
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef short v8i16 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) v4i16* lds_v4p;
+
+__device__ __forceinline__ int pofs(int t, int c) {  // byte offset of (row t, bf16 column c)
+  const int b = 2 * c;
+  return t * PROW + ((((b >> 6) ^ (t & 3)) << 6) | (b & 63));
+}
+
+// chunk ch of a stage: panel ch / 1024, row (ch % 1024) / 32, 16-byte column chunk ch % 32
+template <bool DIAG>
+__device__ __forceinline__ void stage_load(const uint16_t* X, int64_t N, int d, int64_t t0, int i0,
+                                           int j0, int tid, uint4 (&g)[CPT]) {
+#pragma unroll
+  for (int q = 0; q < (DIAG ? CPT / 2 : CPT); ++q) {
+    const int ch = tid + HNT * q, panel = ch >> 10, row = (ch & 1023) >> 5, c16 = ch & 31;
+    const int64_t t = t0 + row;
+    const int c = (panel ? j0 : i0) + 8 * c16;  // d % 8 == 0: 8 columns all in or all out
+    uint4 z = make_uint4(0, 0, 0, 0);
+    if (t < N && c < d) z = *reinterpret_cast<const uint4*>(X + t * d + c);
+    g[q] = z;
+  }
+}
+
+template <bool DIAG>
+__device__ __forceinline__ void stage_store(char* slot, int tid, const uint4 (&g)[CPT]) {
+#pragma unroll
+  for (int q = 0; q < (DIAG ? CPT / 2 : CPT); ++q) {
+    const int ch = tid + HNT * q, panel = ch >> 10, row = (ch & 1023) >> 5, c16 = ch & 31;
+    *reinterpret_cast<uint4*>(slot + panel * PANEL + pofs(row, 8 * c16)) = g[q];
+  }
+}
+
+// MFMA operand for columns col..col+31 and rows krow..krow+15 of a panel:
+// lane l gets column col + l % 32, rows krow + 8 * (l / 32) + 0..7
+__device__ __forceinline__ bf16x8 operand(const char* panel, int krow, int col, int l) {
+  const int g = l >> 4, c = l & 15;
+  const int row = krow + 8 * (g >> 1) + (c >> 2);
+  const int cc = col + 16 * (g & 1) + 4 * (c & 3);
+  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4p)(panel + pofs(row, cc)));
+  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4p)(panel + pofs(row + 4, cc)));
+  const v8i16 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+struct Operands {
+  bf16x8 a[4], b[4];
+};
+
+__device__ __forceinline__ void read_operands(const char* pa, const char* pb, int half, int wm,
+                                              int wn, int l, Operands& f) {
+#pragma unroll
+  for (int x = 0; x < 4; ++x) f.a[x] = operand(pa, 16 * half, wm + 32 * x, l);
+#pragma unroll
+  for (int y = 0; y < 4; ++y) f.b[y] = operand(pb, 16 * half, wn + 32 * y, l);
+}
+
+__device__ __forceinline__ void multiply(const Operands& f, f32x16 (&acc)[4][4]) {
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 4; ++y)
+      acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[x], f.b[y], acc[x][y], 0, 0, 0);
+}
+
+template <bool DIAG>
+__device__ __forceinline__ void tile_rows(const uint16_t* X, int64_t r0, int64_t r1, int d, int i0,
+                                          int j0, char* lds, f32x16 (&acc)[4][4]) {
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int wm = (w >> 1) * 128, wn = (w & 1) * 128;
+  const int ns = (int)((r1 - r0 + KS - 1) / KS);
+  constexpr int SLOT = DIAG ? PANEL : 2 * PANEL;
+  auto pa = [&](int s) -> const char* { return lds + (s % NSLOT) * SLOT; };
+  auto pb = [&](int s) -> const char* { return DIAG ? pa(s) : pa(s) + PANEL; };
+  // rows past r1 load as zeros, so a short split needs no special case
+  uint4 g0[CPT], g1[CPT];
+  stage_load<DIAG>(X, r1, d, r0, i0, j0, tid, g0);
+  stage_load<DIAG>(X, r1, d, r0 + KS, i0, j0, tid, g1);
+  stage_store<DIAG>(lds, tid, g0);
+  stage_store<DIAG>(lds + SLOT, tid, g1);
+  stage_load<DIAG>(X, r1, d, r0 + 2 * KS, i0, j0, tid, g0);
+  stage_load<DIAG>(X, r1, d, r0 + 3 * KS, i0, j0, tid, g1);
+  __syncthreads();
+  Operands f0, f1;
+  read_operands(pa(0), pb(0), 0, wm, wn, l, f0);
+  // stage s: store stage s + 2 (fetched two stages ago) into the slot stage
+  // s - 1 used, fetch stage s + 4 into the same registers, and multiply stage
+  // s while reading the next operands (its second half, then the first half of
+  // stage s + 1)
+  auto step = [&](int s, uint4 (&g)[CPT]) {
+    __syncthreads();
+    if (s + 2 < ns) stage_store<DIAG>(lds + ((s + 2) % NSLOT) * SLOT, tid, g);
+    if (s + 4 < ns) stage_load<DIAG>(X, r1, d, r0 + (int64_t)(s + 4) * KS, i0, j0, tid, g);
+    read_operands(pa(s), pb(s), 1, wm, wn, l, f1);
+    multiply(f0, acc);
+    if (s + 1 < ns) read_operands(pa(s + 1), pb(s + 1), 0, wm, wn, l, f0);
+    multiply(f1, acc);
+  };
+  for (int s = 0; s < ns; s += 2) {
+    step(s, g0);
+    if (s + 1 < ns) step(s + 1, g1);
+  }
+}
+
+__global__ __launch_bounds__(HNT) void hess_bf16_tri_kernel(const uint16_t* __restrict__ X, int64_t N,
                                                             int d, int ntiles, int splits,
                                                             int64_t rows_per_split,
                                                             float* __restrict__ H) {
-  __shared__ uint16_t sA[2][BT * KP];
-  __shared__ uint16_t sB[2][BT * KP];
+  __shared__ __align__(16) char lds[NSLOT * 2 * PANEL];
   const int total = ntiles * splits;
   const int per = (total + 7) / 8;
   const int item = (blockIdx.x % 8) * per + blockIdx.x / 8;
@@ -164,77 +177,33 @@ __global__ __launch_bounds__(512) void hess_bf16_tri_kernel(const uint16_t* __re
   const int64_t r1 = min(N, r0 + rows_per_split);
   if (r0 >= r1) return;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
-  const int wm = (w >> 2) * 128, wn = (w & 3) * 64;  // 8 waves: 2 x 4 quadrants of 128 x 64
-  // loader: threads 0..255 stage the i-panel, 256..511 the j-panel, a 4(t) x 8 block each
-  // Lanes 8k..8k+7 take rows 0, 4, .., 28 of one 8-channel block, so each
-  // transposed 8-byte LDS store of a 16-lane phase covers two 64-byte row runs
-  // on disjoint banks; a wave's 16-byte global loads read 8 rows x 128 bytes.
-  const bool loadsA = tid < 256;
-  const int lt = (tid & 7) * 4;            // 0..28
-  const int lc = ((tid & 255) >> 3) * 8;   // 0..248
-  const int cbase = (loadsA ? i0 : j0) + lc;
-
-  f32x16 acc[4][2];
+  const int wm = (w >> 1) * 128, wn = (w & 1) * 128;
+  f32x16 acc[4][4];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
-
-  uint4 blk[4];
-  load_block_bf16(X, r1, d, r0 + lt, cbase, blk);
-  store_block_bf16(loadsA ? sA[0] : sB[0], lc, lt, blk);
-  __syncthreads();
-  int buf = 0;
-  for (int64_t t0 = r0; t0 < r1; t0 += KT) {
-    // the next step's rows (clamped loads past the end are discarded)
-    load_block_bf16(X, r1, d, t0 + KT + lt, cbase, blk);
-#pragma unroll
-    for (int kk = 0; kk < KT / 16; ++kk) {
-      const int koff = kk * 16 + 8 * (l >> 5);
-      bf16x8 a[4], b[2];
-#pragma unroll
-      for (int x = 0; x < 4; ++x)
-        a[x] = *reinterpret_cast<const bf16x8*>(&sA[buf][(wm + x * 32 + (l & 31)) * KP + koff]);
-#pragma unroll
-      for (int y = 0; y < 2; ++y)
-        b[y] = *reinterpret_cast<const bf16x8*>(&sB[buf][(wn + y * 32 + (l & 31)) * KP + koff]);
-#pragma unroll
-      for (int x = 0; x < 4; ++x)
-#pragma unroll
-        for (int y = 0; y < 2; ++y)
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[x], b[y], acc[x][y], 0, 0, 0);
-    }
-    store_block_bf16(loadsA ? sA[buf ^ 1] : sB[buf ^ 1], lc, lt, blk);
-    __syncthreads();
-    buf ^= 1;
-  }
+  if (ti == tj)
+    tile_rows<true>(X, r0, r1, d, i0, j0, lds, acc);
+  else
+    tile_rows<false>(X, r0, r1, d, i0, j0, lds, acc);
   // lane l holds, for register v of tile (x, y), row wm + 32x + mfma32_row(v, l)
   // and column wn + 32y + l % 32 of the workgroup tile
   float* Hb = H + (int64_t)(i0 + wm + 4 * (l >> 5)) * d + (j0 + wn + (l & 31));
-  if (ti != tj && i0 + BT <= d) {
-    // interior tile strictly below the diagonal: every element is stored
+  const bool full = ti != tj && i0 + BT <= d;  // interior tile strictly below the diagonal
 #pragma unroll
-    for (int x = 0; x < 4; ++x)
+  for (int x = 0; x < 4; ++x)
 #pragma unroll
-      for (int y = 0; y < 2; ++y)
+    for (int y = 0; y < 4; ++y)
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
+      for (int v = 0; v < 16; ++v) {
+        const int i = i0 + wm + x * 32 + mfma32_row(v, l);
+        const int j = j0 + wn + y * 32 + (l & 31);
+        if (full || (i < d && j <= i))
           atomicAdd(Hb + (int64_t)(x * 32 + 8 * (v >> 2) + (v & 3)) * d + y * 32, acc[x][y][v]);
-  } else {
-#pragma unroll
-    for (int x = 0; x < 4; ++x)
-#pragma unroll
-      for (int y = 0; y < 2; ++y)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int i = i0 + wm + x * 32 + mfma32_row(v, l);
-          const int j = j0 + wn + y * 32 + (l & 31);
-          if (i < d && j <= i)
-            atomicAdd(Hb + (int64_t)(x * 32 + 8 * (v >> 2) + (v & 3)) * d + y * 32, acc[x][y][v]);
-        }
-  }
+      }
 }
 
 // H[i][j] = H[j][i] for i < j, through 64 x 64 LDS tiles.
@@ -309,18 +278,20 @@ __global__ __launch_bounds__(256) void hess_f32_kernel(const float* __restrict__
       }
 }
 
-// Row splits for the triangle kernel: as many workgroups as fill whole rounds
-// of the 256 CUs (one 80 KB-LDS workgroup per CU), each split >= 1024 rows.
+// Row splits for the triangle kernel: one 96 KB-LDS workgroup per CU, so the
+// time is about rounds x (stages per split + epilogue); the epilogue's
+// atomics cost about 16 stages.
 static int pick_splits(int ntiles, int64_t N) {
   int best_s = 1;
-  double best_eff = -1.0;
-  for (int s = 1; s <= 256; ++s) {
-    if (s > 1 && N / s < 1024) break;
-    const int64_t wg = (int64_t)ntiles * s;
-    const int64_t rounds = (wg + 255) / 256;
-    const double eff = (double)wg / (double)(rounds * 256);
-    if (eff > best_eff + 1e-9) {
-      best_eff = eff;
+  double best = 1e30;
+  for (int s = 1; s <= 512; ++s) {
+    const int64_t rows = (N + s - 1) / s;
+    if (s > 1 && rows < 256) break;
+    const double stages = (double)((rows + KS - 1) / KS);
+    const double rounds = (double)(((int64_t)ntiles * s + 255) / 256);
+    const double cost = rounds * (stages + 16.0);
+    if (cost < best - 1e-9) {
+      best = cost;
       best_s = s;
     }
   }
@@ -342,11 +313,11 @@ extern "C" int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, f
     const int ntiles = T * (T + 1) / 2;
     const int splits = cp::pick_splits(ntiles, N);
     int64_t rps = (N + splits - 1) / splits;
-    rps = (rps + cp::KT - 1) / cp::KT * cp::KT;
+    rps = (rps + cp::KS - 1) / cp::KS * cp::KS;
     const int total = ntiles * splits;
     const int per = (total + 7) / 8;
-    cp::hess_bf16_tri_kernel<<<dim3(8 * per), 512, 0, st>>>((const uint16_t*)X, N, (int)d, ntiles,
-                                                            splits, rps, H);
+    cp::hess_bf16_tri_kernel<<<dim3(8 * per), cp::HNT, 0, st>>>((const uint16_t*)X, N, (int)d,
+                                                                ntiles, splits, rps, H);
     CP_LAUNCHED("hessian launch");
     const int tb = (int)((d + 63) / 64);
     cp::hess_mirror_kernel<<<dim3(tb, tb), 256, 0, st>>>(H, (int)d);
