@@ -75,15 +75,12 @@ def hessian_phase(X, H, slot):
 def ef_phase(W, H, slot, layers, mode, concurrent=True):
     """Act order + factor per Hessian size class, then EF of that class's tensors.
     With ``concurrent`` each size class runs on its own stream, so one class's
-    factorization overlaps another's sweep."""
+    factorization overlaps another's sweep (perm_amd.ef.encode_size_classes)."""
     from perm_amd import ef as gef
     from perm_amd import workloads as wl
 
-    def job(d):
-        def run():
-            Hb = H[d]
-            order = gef.act_order_dev(Hb)
-            U, _ = gef.factor_dev(Hb, order, 0.01)
+    def builder(d):
+        def build(U, order):
             items = []
             for l in range(layers):
                 for name, _rows, _n, fam in wl.QWEN3_06B_LAYER:
@@ -93,11 +90,18 @@ def ef_phase(W, H, slot, layers, mode, concurrent=True):
                     qw = H[d][i].diagonal() / float(ROWS)
                     items.append({"ttype": "Q2_K", "x": W[l][name], "qw": qw.contiguous(),
                                   "U": U[i], "order": order[i], "recon": True})
-            return gef.ef_encode_dev(items, n_iter=2, mode=mode)
-        return run
+            return items
+        return build
 
-    jobs = [job(d) for d in sorted(H, reverse=True)]
-    return gef.run_concurrent(jobs) if concurrent else [j() for j in jobs]
+    classes = [(H[d], builder(d)) for d in sorted(H, reverse=True)]
+    if concurrent:
+        return gef.encode_size_classes(classes, n_iter=2, mode=mode, damp=0.01)
+    outs = []
+    for Hb, build in classes:
+        order = gef.act_order_dev(Hb)
+        U, _ = gef.factor_dev(Hb, order, 0.01)
+        outs.append(gef.ef_encode_dev(build(U, order), n_iter=2, mode=mode))
+    return outs
 
 
 def cpu_baseline(W, H, slot, layers, total_weights):

@@ -82,6 +82,16 @@ int cp_chol_inv_upper(const void* H, int h_dtype, int64_t n, int batch, const in
                       double damp, int max_tries, void* U, int u_dtype, double* damp_used,
                       void* ws, size_t ws_bytes, void* stream);
 
+/* One attempt of cp_chol_inv_upper at ``damp`` for every matrix, without waiting
+ * on the stream: flags[z] (device int32 array of ``batch``) is set to 1 where
+ * matrix z met a non-positive pivot, and that U_z is then meaningless. Work
+ * that consumes U can be queued behind it; a caller that later finds a set flag
+ * re-runs cp_chol_inv_upper, whose escalation reproduces the reference's
+ * (coldpress/ef.py:60-84). Same workspace as cp_chol_inv_upper. */
+int cp_chol_inv_upper_async(const void* H, int h_dtype, int64_t n, int batch,
+                            const int32_t* order, double damp, void* U, int u_dtype,
+                            int32_t* flags, void* ws, size_t ws_bytes, void* stream);
+
 /* ---- EF encode (coldpress/ef.py:179-218) ---- */
 
 enum cp_ef_mode {

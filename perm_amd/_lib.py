@@ -45,6 +45,8 @@ SIGNATURES = {
     "cp_chol_ws_bytes": (_sz, [_i64, _i32]),
     "cp_chol_inv_upper": (_i32, [_vp, _i32, _i64, _i32, _vp, _f64, _i32, _vp, _i32, _vp, _vp,
                                  _sz, _vp]),
+    "cp_chol_inv_upper_async": (_i32, [_vp, _i32, _i64, _i32, _vp, _f64, _vp, _i32, _vp, _vp,
+                                       _sz, _vp]),
     "cp_ef_ws_bytes": (_sz, [_ef_p, _i32]),
     "cp_ef_encode_batch": (_i32, [_ef_p, _i32, _i32, _i32, _vp, _sz, _vp]),
     "cp_ef_encode": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _sz,

@@ -28,6 +28,9 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <map>
+#include <mutex>
+#include <utility>
 #include <vector>
 
 #include "cp_host.h"
@@ -475,100 +478,186 @@ size_t fact_ws_bytes(int64_t n, int batch) {
          4 * align_up((size_t)batch * 8);
 }
 
+// Pinned host staging for the per-matrix damping, activity and failure flags.
+// Copies from pageable memory go through the runtime's staging path, and a
+// device-to-host one waits there for the whole factorization, holding up
+// other host threads' launches; pinned buffers are plain DMA. Buffers are
+// pooled process-wide (hipHostMalloc is slow) and handed to one call at a time.
+struct PinnedPool {
+  std::mutex mu;
+  std::vector<std::pair<void*, size_t>> free_list;
+  void* take(size_t bytes) {
+    {
+      std::lock_guard<std::mutex> g(mu);
+      for (size_t i = 0; i < free_list.size(); ++i)
+        if (free_list[i].second >= bytes) {
+          void* p = free_list[i].first;
+          free_list.erase(free_list.begin() + i);
+          return p;
+        }
+    }
+    void* p = nullptr;
+    const size_t cap = bytes < 4096 ? 4096 : bytes;
+    if (hipHostMalloc(&p, cap, hipHostMallocDefault) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> g(mu);
+    sizes[p] = cap;
+    return p;
+  }
+  void give(void* p) {
+    std::lock_guard<std::mutex> g(mu);
+    free_list.emplace_back(p, sizes[p]);
+  }
+  std::map<void*, size_t> sizes;
+};
+static PinnedPool g_pinned;
+
+struct PinnedLease {
+  void* p;
+  explicit PinnedLease(size_t bytes) : p(g_pinned.take(bytes)) {}
+  ~PinnedLease() {
+    if (p) g_pinned.give(p);
+  }
+};
+
+// Workspace views shared by the attempt and the driver.
+struct FactWs {
+  double *A, *X, *Tm, *diag_tmp, *shift, *damp_d;
+  int *fail, *active;
+};
+
+static FactWs fact_ws(char* ws, int n, int batch) {
+  const size_t nn = (size_t)n * n;
+  FactWs w;
+  w.A = reinterpret_cast<double*>(ws);
+  w.X = reinterpret_cast<double*>(ws + align_up(nn * batch * 8));
+  w.Tm = reinterpret_cast<double*>(ws + 2 * align_up(nn * batch * 8));
+  char* p = ws + 3 * align_up(nn * batch * 8);
+  w.diag_tmp = reinterpret_cast<double*>(p);
+  p += align_up((size_t)n * batch * 8);
+  w.shift = reinterpret_cast<double*>(p);
+  p += align_up((size_t)batch * 8);
+  w.damp_d = reinterpret_cast<double*>(p);
+  p += align_up((size_t)batch * 8);
+  w.fail = reinterpret_cast<int*>(p);
+  p += align_up((size_t)batch * 8);
+  w.active = reinterpret_cast<int*>(p);
+  return w;
+}
+
+// One factorization attempt of every active matrix at its damp (w.damp_d),
+// raising w.fail[z] on a bad pivot. Stream-ordered, nothing read back.
+template <typename T>
+static int fact_attempt(const T* H, int64_t sH, int n, int batch, const int* order, int64_t sO,
+                        void* U, int u_dtype, int64_t sU, const FactWs& w, hipStream_t st) {
+  const size_t nn = (size_t)n * n;
+  const int64_t sA = (int64_t)nn;
+  double *A = w.A, *X = w.X, *Tm = w.Tm;
+  fill_i32_kernel<<<(batch + 255) / 256, 256, 0, st>>>(w.fail, batch, 0);
+  fill_kernel<<<1024, 256, 0, st>>>(X, (int64_t)nn * batch, 0.0);
+  fact_shift_kernel<T><<<batch, 256, 0, st>>>(H, n, sH, order, sO, w.damp_d, w.diag_tmp, w.shift,
+                                                w.active);
+  fact_prepare_kernel<T><<<dim3((n + 63) / 64, (n + 3) / 4, batch), 256, 0, st>>>(
+      H, n, sH, order, sO, w.shift, A, sA, w.active);
+  CP_LAUNCHED("factor prepare");
+  // left-looking in two levels: an NW-wide block column first receives all
+  // earlier columns' updates in one large-K GEMM; inside it, each NB-wide
+  // column receives its left neighbours' updates, then its diagonal block is
+  // factored and the panel below it solved
+  for (int k0 = 0; k0 < n; k0 += NW) {
+    const int w0 = n - k0 < NW ? n - k0 : NW;
+    if (k0 > 0) {
+      // A[k0:, k0:k0+w0] -= L[k0:, 0:k0] * L[k0:k0+w0, 0:k0]^T, lower part
+      GemmArgs ga{A + (int64_t)k0 * n, A + (int64_t)k0 * n, A + (int64_t)k0 * n + k0, n - k0, w0,
+                  k0, n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 4};
+      if (int s = dgemm(ga, batch, true, st)) return s;
+    }
+    for (int k = k0; k < k0 + w0; k += NB) {
+      const int wk = n - k < NB ? n - k : NB;
+      if (k > k0) {
+        // A[k:, k:k+wk] -= L[k:, k0:k] * L[k:k+wk, k0:k]^T
+        GemmArgs gb{A + (int64_t)k * n + k0, A + (int64_t)k * n + k0, A + (int64_t)k * n + k,
+                    n - k, wk, k - k0, n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 0};
+        if (int s = dgemm(gb, batch, true, st)) return s;
+      }
+      fact_diag_kernel<<<batch, 256, 0, st>>>(A, sA, X, sA, n, k, w.fail, w.active);
+      CP_LAUNCHED("factor diagonal block");
+      const int m = n - k - NB;
+      if (m <= 0) break;
+      // panel: A[k+NB:, k:k+NB] <- A[k+NB:, k:k+NB] * inv(L_kk)^T  (in place, row tiles)
+      GemmArgs pa{A + (int64_t)(k + NB) * n + k, X + (int64_t)k * n + k,
+                  A + (int64_t)(k + NB) * n + k, m, NB, NB, n, n, n, 1.0, 0.0, sA, sA, sA,
+                  0, 0, 0, 1, 0};
+      if (int s = dgemm(pa, batch, true, st)) return s;
+    }
+  }
+  // L^{-1} by recursive doubling over neighbouring s-blocks
+  for (int s = NB; s < n; s *= 2) {
+    const int full = n / (2 * s);          // pairs with a full second block
+    const int rem = n - full * 2 * s - s;  // size of a trailing partial second block
+    for (int part = 0; part < 2; ++part) {
+      const int pairs = part == 0 ? full : (rem > 0 ? 1 : 0);
+      if (pairs == 0) continue;
+      const int s2 = part == 0 ? s : rem;
+      const int b0 = part == 0 ? 0 : full * 2 * s;
+      const int64_t step = (int64_t)2 * s * (n + 1);
+      // T_p = L21 X11
+      GemmArgs g1{A + (int64_t)(b0 + s) * n + b0, X + (int64_t)b0 * n + b0, Tm, s2, s, s, n, n, s,
+                  1.0, 0.0, sA, sA, (int64_t)nn, step, step, (int64_t)s * s, pairs, 2};
+      if (int e = dgemm(g1, batch, false, st)) return e;
+      // X21 = -X22 T_p
+      GemmArgs g2{X + (int64_t)(b0 + s) * n + b0 + s, Tm, X + (int64_t)(b0 + s) * n + b0, s2, s, s2,
+                  n, s, n, -1.0, 0.0, sA, (int64_t)nn, sA, step, (int64_t)s * s, step, pairs, 1};
+      if (int e = dgemm(g2, batch, false, st)) return e;
+    }
+  }
+  const dim3 og((n + 63) / 64, (n + 3) / 4, batch);
+  if (u_dtype == 1)
+    fact_output_kernel<double><<<og, 256, 0, st>>>(X, sA, n, (double*)U, sU, w.active);
+  else
+    fact_output_kernel<float><<<og, 256, 0, st>>>(X, sA, n, (float*)U, sU, w.active);
+  CP_LAUNCHED("factor output");
+  return CP_OK;
+}
+
+// flags_out == nullptr: the reference's escalation loop, reading the failure
+// flags back after each attempt. Otherwise one attempt at damp0 whose flags are
+// copied to flags_out (device) and nothing is read back.
 template <typename T>
 static int fact_run(const T* H, int64_t sH, int n, int batch, const int* order, int64_t sO,
                     double damp0, int max_tries, void* U, int u_dtype, int64_t sU,
-                    double* damp_used, char* ws, hipStream_t st) {
-  const size_t nn = (size_t)n * n;
-  double* A = reinterpret_cast<double*>(ws);
-  double* X = reinterpret_cast<double*>(ws + align_up(nn * batch * 8));
-  double* Tm = reinterpret_cast<double*>(ws + 2 * align_up(nn * batch * 8));
-  char* p = ws + 3 * align_up(nn * batch * 8);
-  double* diag_tmp = reinterpret_cast<double*>(p);
-  p += align_up((size_t)n * batch * 8);
-  double* shift = reinterpret_cast<double*>(p);
-  p += align_up((size_t)batch * 8);
-  double* damp_d = reinterpret_cast<double*>(p);
-  p += align_up((size_t)batch * 8);
-  int* fail = reinterpret_cast<int*>(p);
-  p += align_up((size_t)batch * 8);
-  int* active = reinterpret_cast<int*>(p);
-
+                    double* damp_used, char* ws, hipStream_t st, int32_t* flags_out = nullptr) {
+  const FactWs w = fact_ws(ws, n, batch);
+  if (flags_out) {
+    fill_kernel<<<(batch + 255) / 256, 256, 0, st>>>(w.damp_d, batch, damp0);
+    fill_i32_kernel<<<(batch + 255) / 256, 256, 0, st>>>(w.active, batch, 1);
+    if (int e = fact_attempt<T>(H, sH, n, batch, order, sO, U, u_dtype, sU, w, st)) return e;
+    CP_HIP(hipMemcpyAsync(flags_out, w.fail, batch * sizeof(int), hipMemcpyDeviceToDevice, st));
+    return CP_OK;
+  }
   std::vector<double> damp(batch, damp0);
-  std::vector<int> act(batch, 1), failed(batch, 0), done(batch, 0);
-  const int64_t sA = (int64_t)nn;
+  std::vector<int> act(batch, 1), done(batch, 0);
+  // pinned: [damp f64 x batch][active i32 x batch][fail i32 x batch]
+  PinnedLease lease((size_t)batch * 16);
+  if (!lease.p) return set_error(CP_ERR_HIP, "hipHostMalloc of %zu bytes failed", (size_t)batch * 16);
+  double* damp_h = static_cast<double*>(lease.p);
+  int* act_h = reinterpret_cast<int*>(damp_h + batch);
+  int* fail_h = act_h + batch;
   for (int attempt = 0; attempt < max_tries; ++attempt) {
-    CP_HIP(hipMemcpyAsync(damp_d, damp.data(), batch * sizeof(double), hipMemcpyHostToDevice, st));
-    CP_HIP(hipMemcpyAsync(active, act.data(), batch * sizeof(int), hipMemcpyHostToDevice, st));
-    fill_i32_kernel<<<(batch + 255) / 256, 256, 0, st>>>(fail, batch, 0);
-    fill_kernel<<<1024, 256, 0, st>>>(X, (int64_t)nn * batch, 0.0);
-    fact_shift_kernel<T><<<batch, 256, 0, st>>>(H, n, sH, order, sO, damp_d, diag_tmp, shift, active);
-    fact_prepare_kernel<T><<<dim3((n + 63) / 64, (n + 3) / 4, batch), 256, 0, st>>>(
-        H, n, sH, order, sO, shift, A, sA, active);
-    CP_LAUNCHED("factor prepare");
-    // left-looking in two levels: an NW-wide block column first receives all
-    // earlier columns' updates in one large-K GEMM; inside it, each NB-wide
-    // column receives its left neighbours' updates, then its diagonal block is
-    // factored and the panel below it solved
-    for (int k0 = 0; k0 < n; k0 += NW) {
-      const int w0 = n - k0 < NW ? n - k0 : NW;
-      if (k0 > 0) {
-        // A[k0:, k0:k0+w0] -= L[k0:, 0:k0] * L[k0:k0+w0, 0:k0]^T, lower part
-        GemmArgs ga{A + (int64_t)k0 * n, A + (int64_t)k0 * n, A + (int64_t)k0 * n + k0, n - k0, w0,
-                    k0, n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 4};
-        if (int s = dgemm(ga, batch, true, st)) return s;
-      }
-      for (int k = k0; k < k0 + w0; k += NB) {
-        const int w = n - k < NB ? n - k : NB;
-        if (k > k0) {
-          // A[k:, k:k+w] -= L[k:, k0:k] * L[k:k+w, k0:k]^T
-          GemmArgs gb{A + (int64_t)k * n + k0, A + (int64_t)k * n + k0, A + (int64_t)k * n + k,
-                      n - k, w, k - k0, n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 0};
-          if (int s = dgemm(gb, batch, true, st)) return s;
-        }
-        fact_diag_kernel<<<batch, 256, 0, st>>>(A, sA, X, sA, n, k, fail, active);
-        CP_LAUNCHED("factor diagonal block");
-        const int m = n - k - NB;
-        if (m <= 0) break;
-        // panel: A[k+NB:, k:k+NB] <- A[k+NB:, k:k+NB] * inv(L_kk)^T  (in place, row tiles)
-        GemmArgs pa{A + (int64_t)(k + NB) * n + k, X + (int64_t)k * n + k,
-                    A + (int64_t)(k + NB) * n + k, m, NB, NB, n, n, n, 1.0, 0.0, sA, sA, sA,
-                    0, 0, 0, 1, 0};
-        if (int s = dgemm(pa, batch, true, st)) return s;
-      }
+    // the previous attempt ended with a stream synchronize, so the pinned
+    // buffers are free to rewrite
+    for (int z = 0; z < batch; ++z) {
+      damp_h[z] = damp[z];
+      act_h[z] = act[z];
     }
-    // L^{-1} by recursive doubling over neighbouring s-blocks
-    for (int s = NB; s < n; s *= 2) {
-      const int full = n / (2 * s);          // pairs with a full second block
-      const int rem = n - full * 2 * s - s;  // size of a trailing partial second block
-      for (int part = 0; part < 2; ++part) {
-        const int pairs = part == 0 ? full : (rem > 0 ? 1 : 0);
-        if (pairs == 0) continue;
-        const int s2 = part == 0 ? s : rem;
-        const int b0 = part == 0 ? 0 : full * 2 * s;
-        const int64_t step = (int64_t)2 * s * (n + 1);
-        // T_p = L21 X11
-        GemmArgs g1{A + (int64_t)(b0 + s) * n + b0, X + (int64_t)b0 * n + b0, Tm, s2, s, s, n, n, s,
-                    1.0, 0.0, sA, sA, (int64_t)nn, step, step, (int64_t)s * s, pairs, 2};
-        if (int e = dgemm(g1, batch, false, st)) return e;
-        // X21 = -X22 T_p
-        GemmArgs g2{X + (int64_t)(b0 + s) * n + b0 + s, Tm, X + (int64_t)(b0 + s) * n + b0, s2, s, s2,
-                    n, s, n, -1.0, 0.0, sA, (int64_t)nn, sA, step, (int64_t)s * s, step, pairs, 1};
-        if (int e = dgemm(g2, batch, false, st)) return e;
-      }
-    }
-    const dim3 og((n + 63) / 64, (n + 3) / 4, batch);
-    if (u_dtype == 1)
-      fact_output_kernel<double><<<og, 256, 0, st>>>(X, sA, n, (double*)U, sU, active);
-    else
-      fact_output_kernel<float><<<og, 256, 0, st>>>(X, sA, n, (float*)U, sU, active);
-    CP_LAUNCHED("factor output");
-    CP_HIP(hipMemcpyAsync(failed.data(), fail, batch * sizeof(int), hipMemcpyDeviceToHost, st));
+    CP_HIP(hipMemcpyAsync(w.damp_d, damp_h, batch * sizeof(double), hipMemcpyHostToDevice, st));
+    CP_HIP(hipMemcpyAsync(w.active, act_h, batch * sizeof(int), hipMemcpyHostToDevice, st));
+    if (int e = fact_attempt<T>(H, sH, n, batch, order, sO, U, u_dtype, sU, w, st)) return e;
+    CP_HIP(hipMemcpyAsync(fail_h, w.fail, batch * sizeof(int), hipMemcpyDeviceToHost, st));
     CP_HIP(hipStreamSynchronize(st));
     int pending = 0;
     for (int z = 0; z < batch; ++z) {
       if (!act[z]) continue;
-      if (failed[z]) {
+      if (fail_h[z]) {
         damp[z] *= 10.0;
         ++pending;
       } else {
@@ -608,6 +697,27 @@ int cp_act_order(const void* H, int h_dtype, int64_t n, int batch, int32_t* orde
     cp::act_order_kernel<float><<<grid, 256, 0, st>>>((const float*)H, (int)n, n * n, order, n);
   CP_LAUNCHED("act_order launch");
   return CP_OK;
+}
+
+int cp_chol_inv_upper_async(const void* H, int h_dtype, int64_t n, int batch,
+                            const int32_t* order, double damp, void* U, int u_dtype,
+                            int32_t* flags, void* ws, size_t ws_bytes, void* stream) {
+  cp::clear_error();
+  if (!H || !U || !ws || !flags) return cp::set_error(CP_ERR_ARG, "null H/U/flags/ws");
+  if (u_dtype != 0 && u_dtype != 1) return cp::set_error(CP_ERR_ARG, "u_dtype must be 0 (f32) or 1 (f64)");
+  if (n <= 0 || batch <= 0 || n > 65536) return cp::set_error(CP_ERR_SHAPE, "bad n=%lld / batch=%d", (long long)n, batch);
+  if (ws_bytes < cp::fact_ws_bytes(n, batch))
+    return cp::set_error(CP_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, cp::fact_ws_bytes(n, batch));
+  if (!cp::aligned(ws, 256)) return cp::set_error(CP_ERR_ALIGN, "workspace needs 256-byte alignment");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t nn = n * n;
+  if (h_dtype == 1)
+    return cp::fact_run<double>((const double*)H, nn, (int)n, batch, order, n, damp, 1, U, u_dtype,
+                                nn, nullptr, (char*)ws, st, flags);
+  if (h_dtype == 0)
+    return cp::fact_run<float>((const float*)H, nn, (int)n, batch, order, n, damp, 1, U, u_dtype,
+                               nn, nullptr, (char*)ws, st, flags);
+  return cp::set_error(CP_ERR_ARG, "h_dtype must be 0 (f32) or 1 (f64)");
 }
 
 int cp_chol_inv_upper(const void* H, int h_dtype, int64_t n, int batch, const int32_t* order,

@@ -66,6 +66,28 @@ def factor_dev(H, order=None, damp=0.01, max_tries=6, out_dtype=torch.float32):
     return (U[0] if squeeze else U), list(used)
 
 
+def factor_dev_async(H, order=None, damp=0.01, out_dtype=torch.float32):
+    """One attempt of ``factor_dev`` at ``damp``, queued on the current stream
+    without waiting on it. Returns (U, flags): flags is an int32 device tensor
+    [batch] whose set entries mark matrices that met a non-positive pivot (their
+    U is meaningless and ``factor_dev`` must redo them, with escalation)."""
+    lib = _lib.load()
+    squeeze = H.dim() == 2
+    Hb = H.unsqueeze(0) if squeeze else H
+    batch, n = Hb.shape[0], Hb.shape[-1]
+    if order is not None:
+        order = order.reshape(batch, n).to(torch.int32).contiguous()
+    U = torch.empty((batch, n, n), dtype=out_dtype, device=H.device)
+    flags = torch.empty(batch, dtype=torch.int32, device=H.device)
+    ws = _lib.workspace(lib.cp_chol_ws_bytes(n, batch), H.device)
+    st = lib.cp_chol_inv_upper_async(_lib.ptr(Hb), _h_dtype(Hb), n, batch, _lib.ptr(order),
+                                     float(damp), _lib.ptr(U),
+                                     1 if out_dtype == torch.float64 else 0, _lib.ptr(flags),
+                                     _lib.ptr(ws), ws.numel(), _lib.stream_ptr())
+    _lib.check(st)
+    return (U[0] if squeeze else U), flags
+
+
 def cholesky_inv_upper(H, damp=0.01, _max_tries=6):
     """U = chol(inv(H + lambda I), upper), float64 (coldpress/ef.py:46-84).
 
@@ -142,57 +164,65 @@ def ef_encode(x, ttype, qw, H, n_iter=2, damp=0.01, act_order=True, mode="exact"
 _STREAMS = {}
 
 
-def run_concurrent(jobs):
-    """Run each callable on its own HIP stream and host thread.
-
-    The streams first wait for the work already queued on the caller's current
-    stream, and the current stream then waits for all of them, so the call
-    behaves like one ordered step. A job that blocks on its stream (the
-    factorization reads its failure flags) does not hold up the others: ctypes
-    releases the interpreter lock during library calls. Streams keep the
-    default priority and are reused across calls (the caching allocator keeps
-    their workspaces). Returns the jobs' results in order; re-raises the first
-    error."""
-    import threading
-    cur = torch.cuda.current_stream()
+def _class_stream(k):
     dev = torch.cuda.current_device()
-    streams = []
-    for k in range(len(jobs)):
-        s = _STREAMS.get((dev, k))
-        if s is None:
-            s = _STREAMS[(dev, k)] = torch.cuda.Stream()
+    s = _STREAMS.get((dev, k))
+    if s is None:
+        s = _STREAMS[(dev, k)] = torch.cuda.Stream()  # default priority
+    return s
+
+
+def encode_size_classes(classes, n_iter=2, mode="exact", damp=0.01, act_order=True):
+    """EF of several Hessian size classes, overlapped on the device.
+
+    classes: list of (Hb [batch, n, n] CUDA float32/float64, build) where
+    build(U, order) returns the ef_encode_dev items of that class (U [batch, n, n],
+    order [batch, n]). Every class gets its own stream; from this one host thread
+    the act orders and one factorization attempt of every class are queued first,
+    then every class's EF, so one class's factorization overlaps another's
+    sweep. Then the factorization flags are read (the only wait), and a class
+    with a failed matrix is factorized again with escalation and re-encoded.
+    The caller's current stream ends up ordered after all of it.
+    Returns one ef_encode_dev result list per class."""
+    cur = torch.cuda.current_stream()
+    streams = [_class_stream(k) for k in range(len(classes))]
+    facs = []
+    for (Hb, _), s in zip(classes, streams):
         s.wait_stream(cur)
-        streams.append(s)
-    results, errors = [None] * len(jobs), []
-
-    def work(k):
-        try:
-            torch.cuda.set_device(dev)
-            with torch.cuda.stream(streams[k]):
-                results[k] = jobs[k]()
-        except BaseException as e:  # re-raised in the caller's thread
-            errors.append(e)
-
-    threads = [threading.Thread(target=work, args=(k,)) for k in range(len(jobs))]
-    for t in threads:
-        t.start()
-    for t in threads:
-        t.join()
+        with torch.cuda.stream(s):
+            order = act_order_dev(Hb, act_order)
+            U, flags = factor_dev_async(Hb, order, damp)
+        facs.append((order, U, flags))
+    outs = []
+    for (_, build), s, (order, U, _) in zip(classes, streams, facs):
+        with torch.cuda.stream(s):
+            outs.append(ef_encode_dev(build(U, order), n_iter, MODES[mode] if isinstance(mode, str)
+                                      else mode))
     for s in streams:
         cur.wait_stream(s)
-    if errors:
-        raise errors[0]
-    return results
+    for res in outs:
+        for raw, rec in res:
+            raw.record_stream(cur)
+            if rec is not None:
+                rec.record_stream(cur)
+    failed = torch.stack([f.max() for (_, _, f) in facs]).cpu().tolist()
+    for k, bad in enumerate(failed):
+        if bad:
+            Hb, build = classes[k]
+            order = facs[k][0]
+            U, _ = factor_dev(Hb, order, damp)
+            outs[k] = ef_encode_dev(build(U, order), n_iter, MODES[mode] if isinstance(mode, str)
+                                    else mode)
+    return outs
 
 
-def ef_encode_many(tensors, n_iter=2, damp=0.01, act_order=True, mode="exact", concurrent=True):
+def ef_encode_many(tensors, n_iter=2, damp=0.01, act_order=True, mode="exact"):
     """EF-encode many tensors in one batched pass.
 
     tensors: list of dicts {name, ttype, x (CUDA f32), qw (CUDA f32 or None),
     H (CUDA f32/f64 [n, n])}. Tensors whose ``H`` is the same object share one
     act order and one factorization (done batched per matrix size). Each size
-    class (its factorization, then the EF of its tensors) runs on its own
-    stream, so one class's factorization overlaps another's sweep.
+    class runs on its own stream (``encode_size_classes``).
     Returns {name: (raw, recon)}."""
     hs = {}
     for t in tensors:
@@ -201,24 +231,22 @@ def ef_encode_many(tensors, n_iter=2, damp=0.01, act_order=True, mode="exact", c
     for key, H in hs.items():
         by_n.setdefault((H.shape[-1], H.dtype), []).append(key)
 
-    def job(keys):
-        def run():
-            Hb = torch.stack([hs[k] for k in keys]) if len(keys) > 1 else hs[keys[0]].unsqueeze(0)
-            order = act_order_dev(Hb.contiguous(), act_order)
-            U, _ = factor_dev(Hb.contiguous(), order, damp)
-            slot = {k: i for i, k in enumerate(keys)}
-            mine = [t for t in tensors if id(t["H"]) in slot]
-            items = [{"ttype": t["ttype"], "x": t["x"], "qw": t.get("qw"),
-                      "U": U[slot[id(t["H"])]], "order": order[slot[id(t["H"])]],
-                      "recon": t.get("recon", True)} for t in mine]
-            outs = ef_encode_dev(items, n_iter, MODES[mode])
-            return {t["name"]: o for t, o in zip(mine, outs)}
-        return run
-
+    classes, members = [], []
     # largest matrices first: their factorization is the longest chain
-    jobs = [job(keys) for _, keys in sorted(by_n.items(), key=lambda kv: -kv[0][0])]
-    res = run_concurrent(jobs) if concurrent else [j() for j in jobs]
+    for _, keys in sorted(by_n.items(), key=lambda kv: -kv[0][0]):
+        slot = {k: i for i, k in enumerate(keys)}
+        mine = [t for t in tensors if id(t["H"]) in slot]
+        Hb = torch.stack([hs[k] for k in keys]) if len(keys) > 1 else hs[keys[0]].unsqueeze(0)
+
+        def build(U, order, mine=mine, slot=slot):
+            return [{"ttype": t["ttype"], "x": t["x"], "qw": t.get("qw"),
+                     "U": U[slot[id(t["H"])]], "order": order[slot[id(t["H"])]],
+                     "recon": t.get("recon", True)} for t in mine]
+        classes.append((Hb.contiguous(), build))
+        members.append(mine)
+    res = encode_size_classes(classes, n_iter, mode, damp, act_order)
     out = {}
-    for r in res:
-        out.update(r)
+    for mine, r in zip(members, res):
+        for t, o in zip(mine, r):
+            out[t["name"]] = o
     return {t["name"]: out[t["name"]] for t in tensors}

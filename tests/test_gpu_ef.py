@@ -189,6 +189,46 @@ def test_many_shares_factor_and_matches_single(ef):
         assert torch.equal(out[nm][0], raw1) and torch.equal(out[nm][1], rec1)
 
 
+def test_factor_async_equals_blocking(ef):
+    Hs = [correlated_hessian(320, 1280, seed=s) for s in range(3)]
+    Hb = torch.from_numpy(np.stack(Hs)).cuda()
+    order = ef.act_order_dev(Hb)
+    Ua, flags = ef.factor_dev_async(Hb, order, 0.01)
+    Ub, _ = ef.factor_dev(Hb, order, 0.01)
+    assert flags.cpu().tolist() == [0, 0, 0]
+    assert torch.equal(Ua, Ub)
+
+
+def test_factor_async_flags_a_failed_matrix(ef):
+    n = 256
+    eig = np.linspace(1.0, 100.0, n)
+    eig[0] = -2.0
+    bad = _spectrum_matrix(n, eig, seed=1)
+    good = correlated_hessian(n, 1024, seed=2)
+    Hb = torch.from_numpy(np.stack([good, bad])).cuda()
+    _, flags = ef.factor_dev_async(Hb, None, 0.01)
+    assert flags.cpu().tolist() == [0, 1]
+
+
+def test_many_redoes_a_class_that_needs_escalation(ef, capfd):
+    """A size class whose factorization fails at the first damp is factorized
+    again with escalation and re-encoded; the other class is untouched."""
+    n1, n2 = 256, 512
+    eig = np.linspace(1.0, 100.0, n1)
+    eig[0] = -2.0
+    Hbad = torch.from_numpy(_spectrum_matrix(n1, eig, seed=1)).cuda()
+    Hgood = torch.from_numpy(correlated_hessian(n2, 2048, seed=3)).cuda()
+    xa = torch.from_numpy(heavy_tailed(64, n1, seed=5)).cuda()
+    xb = torch.from_numpy(heavy_tailed(96, n2, seed=6)).cuda()
+    tens = [{"name": "a", "ttype": "Q2_K", "x": xa, "qw": None, "H": Hbad},
+            {"name": "b", "ttype": "Q4_K", "x": xb, "qw": None, "H": Hgood}]
+    out = ef.ef_encode_many(tens)
+    for t in tens:
+        raw1, rec1 = ef.ef_encode(t["x"], t["ttype"], None, t["H"])
+        assert torch.equal(out[t["name"]][0], raw1) and torch.equal(out[t["name"]][1], rec1)
+    assert "damp escalated" in capfd.readouterr().err
+
+
 @pytest.fixture(scope="module")
 def single_linear_ref():
     """Oracle EF of the single-Linear workload (1024 x 1024, H from 8192 rows with
