@@ -20,16 +20,15 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 #include "cp_device.h"
 #include "cp_host.h"
+#include "kq_blocks.h"
 
 namespace cp {
 
-int kq_quantize(int ttype, const float* x, int64_t nrow, int64_t n, const float* qw, uint8_t* out,
-                hipStream_t st);
-int kq_dequantize(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, float* y, hipStream_t st);
 
 constexpr int BLK = 32;  // columns per sweep block
 
@@ -428,59 +427,122 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_mfma_kernel(const SweepTask* _
   }
 }
 
-// ---------------------------------------------------------------- index helpers
-__global__ void ef_index_kernel(const int* order, int n, int sub, int* inv, int* sbidx) {
-  int jj = blockIdx.x * blockDim.x + threadIdx.x;
-  if (jj >= n) return;
-  int c = order[jj];
-  inv[c] = jj;
-  sbidx[jj] = c / sub;
+// ---------------------------------------------------------------- many-tensor kernels
+// Every step outside the sweep runs as one launch over all tensors of a call
+// (blockIdx.y or .z = row of the tensor table; blocks past a tensor's extent
+// exit), so a call costs a few dozen launches instead of a dozen per tensor.
+
+// Per-tensor device descriptor (the workspace views plus the caller's buffers).
+struct EfDev {
+  const float* x;
+  const float* qw;
+  const int* order;
+  uint8_t* raw;
+  float* recon;
+  float* WpT;
+  float* WcurT;
+  float* Wcur;
+  uint8_t* LT;
+  uint8_t* Lrow;
+  float* dlT;
+  float* mlT;
+  int* inv;
+  int* sbidx;
+  int nrow, n, ttype, sub;
+};
+
+constexpr int kDevPerStore = 24;
+struct EfDevBatch {
+  EfDev t[kDevPerStore];
+};
+static_assert(sizeof(EfDevBatch) <= 4000, "kernel argument block");
+
+__global__ void ef_dev_store_kernel(const EfDevBatch batch, int count, EfDev* dst) {
+  if ((int)threadIdx.x < count) dst[threadIdx.x] = batch.t[threadIdx.x];
 }
 
-// dst[inv[c]][r] = src[r][c]: row-major storage order -> column-major visiting
-// order, through a 64x64 LDS tile (coalesced on both sides).
-template <typename T>
-__global__ __launch_bounds__(256) void ef_to_visit_kernel(const T* __restrict__ src, int nrow, int n,
-                                                          const int* __restrict__ inv,
-                                                          T* __restrict__ dst) {
-  __shared__ T tile[64][65];
+// inv[order[jj]] = jj and sbidx[jj] = order[jj] / sub
+__global__ void ef_index_kernel(const EfDev* __restrict__ tab) {
+  const EfDev& t = tab[blockIdx.y];
+  const int jj = blockIdx.x * blockDim.x + threadIdx.x;
+  if (jj >= t.n) return;
+  const int c = t.order[jj];
+  if ((unsigned)c >= (unsigned)t.n) return;  // not a permutation: no write out of range
+  t.inv[c] = jj;
+  t.sbidx[jj] = c / t.sub;
+}
+
+// dst[inv[c]][r] = src[r][c] (row-major storage order -> column-major visiting
+// order) or its inverse, through a 64x64 LDS tile (coalesced on both sides).
+// WHICH: 0 = x -> WpT, 1 = LT -> Lrow, 2 = WcurT -> Wcur.
+template <int WHICH>
+__global__ __launch_bounds__(256) void ef_transpose_kernel(const EfDev* __restrict__ tab) {
+  typedef typename std::conditional<WHICH == 1, uint8_t, float>::type T;
+  const EfDev& t = tab[blockIdx.z];
+  const int nrow = t.nrow, n = t.n;
   const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  if (c0 >= n || r0 >= nrow) return;
+  __shared__ T tile[64][65];
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int i = ty; i < 64; i += 4) {
-    int r = r0 + i, c = c0 + tx;
-    if (r < nrow && c < n) tile[i][tx] = src[(int64_t)r * n + c];
-  }
-  __syncthreads();
-  for (int j = ty; j < 64; j += 4) {
-    int c = c0 + j, r = r0 + tx;
-    if (r < nrow && c < n) dst[(int64_t)inv[c] * nrow + r] = tile[tx][j];
+  const int* __restrict__ inv = t.inv;
+  if (WHICH == 0) {  // storage -> visiting
+    const float* src = t.x;
+    float* dst = t.WpT;
+    for (int i = ty; i < 64; i += 4) {
+      const int r = r0 + i, c = c0 + tx;
+      if (r < nrow && c < n) tile[i][tx] = src[(int64_t)r * n + c];
+    }
+    __syncthreads();
+    for (int j = ty; j < 64; j += 4) {
+      const int c = c0 + j, r = r0 + tx;
+      const int v = c < n ? inv[c] : -1;
+      if (r < nrow && (unsigned)v < (unsigned)n) dst[(int64_t)v * nrow + r] = tile[tx][j];
+    }
+  } else {  // visiting -> storage
+    const T* src = WHICH == 1 ? (const T*)t.LT : (const T*)t.WcurT;
+    T* dst = WHICH == 1 ? (T*)t.Lrow : (T*)t.Wcur;
+    for (int j = ty; j < 64; j += 4) {
+      const int c = c0 + j, r = r0 + tx;
+      const int v = c < n ? inv[c] : -1;
+      if (r < nrow && (unsigned)v < (unsigned)n) tile[tx][j] = src[(int64_t)v * nrow + r];
+    }
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4) {
+      const int r = r0 + i, c = c0 + tx;
+      if (r < nrow && c < n) dst[(int64_t)r * n + c] = tile[i][tx];
+    }
   }
 }
 
-// dst[r][c] = src[inv[c]][r]: the inverse of ef_to_visit_kernel.
-template <typename T>
-__global__ __launch_bounds__(256) void ef_to_storage_kernel(const T* __restrict__ src, int nrow, int n,
-                                                            const int* __restrict__ inv,
-                                                            T* __restrict__ dst) {
-  __shared__ T tile[64][65];
-  const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int j = ty; j < 64; j += 4) {
-    int c = c0 + j, r = r0 + tx;
-    if (r < nrow && c < n) tile[tx][j] = src[(int64_t)inv[c] * nrow + r];
-  }
-  __syncthreads();
-  for (int i = ty; i < 64; i += 4) {
-    int r = r0 + i, c = c0 + tx;
-    if (r < nrow && c < n) dst[(int64_t)r * n + c] = tile[i][tx];
-  }
+// Commit: the k-quant encode of every tensor of a (type, importance) group,
+// from the original weights (first iteration) or the compensated targets.
+template <int TT, bool IMAT>
+__global__ __launch_bounds__(256) void ef_commit_kernel(const EfDev* __restrict__ tab, int from_wcur) {
+  const EfDev& t = tab[blockIdx.y];
+  constexpr int S = 64 / Kq<TT>::G;
+  const int64_t nsb = t.n / 256, NB = (int64_t)t.nrow * nsb;
+  const int64_t blocks = ((NB + S - 1) / S + kWavesPerBlock - 1) / kWavesPerBlock;
+  if ((int64_t)blockIdx.x >= blocks) return;
+  kq_encode_block<TT, IMAT>(from_wcur ? t.Wcur : t.x, t.qw, NB, nsb, t.raw, blockIdx.x);
+}
+
+template <int TT>
+__global__ __launch_bounds__(256) void ef_decode_kernel(const EfDev* __restrict__ tab) {
+  const EfDev& t = tab[blockIdx.y];
+  if (!t.recon) return;
+  kq_decode_thread<TT>(t.raw, (int64_t)t.nrow * (t.n / 256), t.recon,
+                       (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
 // ---------------------------------------------------------------- committed grid
 // Per (row, storage sub-block): step dl and offset ml of the committed bytes,
-// written transposed [sub][row] (ef.py:87-127).
-__global__ void ef_grid_kernel(int ttype, const uint8_t* __restrict__ raw, int nrow, int n,
-                               float* __restrict__ dlT, float* __restrict__ mlT) {
+// written transposed [sub][row] (ef.py:87-127). One thread per (row, 16 weights).
+__global__ void ef_grid_kernel(const EfDev* __restrict__ tab) {
+  const EfDev& T = tab[blockIdx.y];
+  const int ttype = T.ttype, nrow = T.nrow, n = T.n;
+  const uint8_t* __restrict__ raw = T.raw;
+  float* __restrict__ dlT = T.dlT;
+  float* __restrict__ mlT = T.mlT;
   const int nsub16 = n / 16;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int r = (int)(t % nrow);
@@ -533,8 +595,9 @@ __global__ void ef_grid_kernel(int ttype, const uint8_t* __restrict__ raw, int n
 // Rewrite the code bytes of committed superblocks from stored codes Lrow
 // [nrow][n] (row-major storage order), keeping the scale bytes (ef.py:130-176).
 // One thread per code byte of a superblock.
-__global__ void ef_repack_kernel(int ttype, const uint8_t* __restrict__ Lrow, int64_t NB,
-                                 uint8_t* __restrict__ raw) {
+__global__ void ef_repack_kernel(const EfDev* __restrict__ tab) {
+  const EfDev& T = tab[blockIdx.y];
+  const int ttype = T.ttype;
   int lo_b, hi_b, bp;
   switch (ttype) {
     case CP_Q2_K: lo_b = 16; hi_b = 80; bp = 84; break;
@@ -542,12 +605,13 @@ __global__ void ef_repack_kernel(int ttype, const uint8_t* __restrict__ Lrow, in
     case CP_Q4_K: lo_b = 16; hi_b = 144; bp = 144; break;
     default: lo_b = 0; hi_b = 192; bp = 210; break;
   }
+  const int64_t NB = (int64_t)T.nrow * (T.n / 256);
   const int span = hi_b - lo_b;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t sb = t / span;
   if (sb >= NB) return;
   const int b = lo_b + (int)(t % span);
-  const uint8_t* c = Lrow + sb * 256;
+  const uint8_t* c = T.Lrow + sb * 256;
   uint32_t v;
   if (ttype == CP_Q2_K) {
     int k = b - 16, base = (k >> 5) * 128 + (k & 31);
@@ -573,7 +637,7 @@ __global__ void ef_repack_kernel(int ttype, const uint8_t* __restrict__ Lrow, in
       v = (c[base] >> 4) | (c[base + 32] >> 4) << 2 | (c[base + 64] >> 4) << 4 | (c[base + 96] >> 4) << 6;
     }
   }
-  raw[sb * bp + b] = (uint8_t)v;
+  T.raw[sb * bp + b] = (uint8_t)v;
 }
 
 // ---------------------------------------------------------------- host driver
@@ -602,8 +666,13 @@ static EfLayout ef_layout(int64_t nrow, int64_t n, size_t base) {
   return L;
 }
 
+// workspace: [sweep task table][tensor table][per-tensor buffers]
+static size_t ef_tables_bytes(int count) {
+  return a256((size_t)count * sizeof(SweepTask)) + a256((size_t)count * sizeof(EfDev));
+}
+
 size_t ef_ws_bytes(const cp_ef_tensor* t, int count) {
-  size_t o = a256((size_t)count * sizeof(SweepTask));
+  size_t o = ef_tables_bytes(count);
   for (int i = 0; i < count; ++i) o = ef_layout(t[i].nrow, t[i].n, o).end;
   return o;
 }
@@ -647,9 +716,34 @@ static thread_local PhaseClock g_clock;
     if (g_clock.on) CP_HIP(p < 0 ? g_clock.start(st) : g_clock.mark(p, st)); \
   } while (0)
 
+// A run of table rows sharing (type, importance) for the templated codec launches.
+struct EfGroup {
+  int first, count, ttype;
+  bool imat;
+  int64_t max_nb;  // superblocks of the largest tensor
+};
+
+template <int TT>
+static void launch_commit(const EfDev* tab, const EfGroup& g, int from_wcur, hipStream_t st) {
+  constexpr int S = 64 / Kq<TT>::G;
+  const int64_t blocks = ((g.max_nb + S - 1) / S + kWavesPerBlock - 1) / kWavesPerBlock;
+  const dim3 grid((unsigned)blocks, (unsigned)g.count);
+  if (g.imat)
+    ef_commit_kernel<TT, true><<<grid, 256, 0, st>>>(tab + g.first, from_wcur);
+  else
+    ef_commit_kernel<TT, false><<<grid, 256, 0, st>>>(tab + g.first, from_wcur);
+}
+
+template <int TT>
+static void launch_decode(const EfDev* tab, const EfGroup& g, hipStream_t st) {
+  const dim3 grid((unsigned)((g.max_nb * 16 + 255) / 256), (unsigned)g.count);
+  ef_decode_kernel<TT><<<grid, 256, 0, st>>>(tab + g.first);
+}
+
 int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, void* ws,
                     size_t ws_bytes, hipStream_t st) {
   if (!ts || count <= 0) return set_error(CP_ERR_ARG, "no tensors");
+  if (count > 65535) return set_error(CP_ERR_ARG, "at most 65535 tensors per call (got %d)", count);
   if (n_iter < 1) return set_error(CP_ERR_ARG, "n_iter must be >= 1");
   if (mode != CP_EF_EXACT && mode != CP_EF_MFMA && mode != CP_EF_EXACT_VALU)
     return set_error(CP_ERR_ARG, "unknown EF mode %d", mode);
@@ -657,7 +751,7 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     const cp_ef_tensor& t = ts[i];
     KqGeom g;
     if (!kq_geom(t.ttype, &g)) return set_error(CP_ERR_TTYPE, "tensor %d: unsupported type %d", i, t.ttype);
-    if (t.nrow <= 0 || t.n <= 0 || t.n % 256 || t.nrow > (1 << 30) || t.n > (1 << 20) ||
+    if (t.nrow <= 0 || t.n <= 0 || t.n % 256 || t.nrow > 65535 * 64 || t.n > (1 << 20) ||
         (t.n / 16) * t.nrow >= ((int64_t)1 << 31))
       return set_error(CP_ERR_SHAPE, "tensor %d: bad shape [%lld, %lld]", i, (long long)t.nrow, (long long)t.n);
     if (!t.x || !t.U || !t.order || !t.raw) return set_error(CP_ERR_ARG, "tensor %d: null pointer", i);
@@ -670,91 +764,108 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
   if (!aligned(ws, 256)) return set_error(CP_ERR_ALIGN, "workspace needs 256-byte alignment");
   CP_PHASE(-1);
   char* base = (char*)ws;
-  std::vector<EfLayout> lay(count);
-  std::vector<SweepTask> tasks(count);
   SweepTask* dtasks = (SweepTask*)base;
-  size_t o = a256((size_t)count * sizeof(SweepTask));
+  EfDev* dtab = (EfDev*)(base + a256((size_t)count * sizeof(SweepTask)));
+  std::vector<SweepTask> tasks(count);
+  std::vector<EfDev> devs(count);
+  int max_n = 0, max_rows = 0;
+  size_t o = ef_tables_bytes(count);
   for (int i = 0; i < count; ++i) {
     const cp_ef_tensor& t = ts[i];
-    lay[i] = ef_layout(t.nrow, t.n, o);
-    o = lay[i].end;
+    const EfLayout L = ef_layout(t.nrow, t.n, o);
+    o = L.end;
     int lo, hi, sub;
     grid_range(t.ttype, &lo, &hi, &sub);
-    const EfLayout& L = lay[i];
     const bool affine = t.ttype == CP_Q2_K || t.ttype == CP_Q4_K;
-    tasks[i] = SweepTask{(const float*)(base + L.WpT), t.U, (const float*)(base + L.dlT),
-                         affine ? (const float*)(base + L.mlT) : nullptr,
+    float* mlT = affine ? (float*)(base + L.mlT) : nullptr;
+    tasks[i] = SweepTask{(const float*)(base + L.WpT), t.U, (const float*)(base + L.dlT), mlT,
                          (const int*)(base + L.sbidx), (float*)(base + L.E),
                          (float*)(base + L.WcurT), (uint8_t*)(base + L.LT),
                          (int)t.nrow, (int)t.n, lo, hi};
-    ef_index_kernel<<<(unsigned)((t.n + 255) / 256), 256, 0, st>>>(t.order, (int)t.n, sub,
-                                                                    (int*)(base + L.inv),
-                                                                    (int*)(base + L.sbidx));
-    dim3 tg((unsigned)((t.n + 63) / 64), (unsigned)((t.nrow + 63) / 64));
-    ef_to_visit_kernel<float><<<tg, 256, 0, st>>>(t.x, (int)t.nrow, (int)t.n,
-                                                  (const int*)(base + L.inv), (float*)(base + L.WpT));
+    devs[i] = EfDev{t.x, t.qw, t.order, t.raw, t.recon, (float*)(base + L.WpT),
+                    (float*)(base + L.WcurT), (float*)(base + L.Wcur), (uint8_t*)(base + L.LT),
+                    (uint8_t*)(base + L.Lrow), (float*)(base + L.dlT), mlT, (int*)(base + L.inv),
+                    (int*)(base + L.sbidx), (int)t.nrow, (int)t.n, t.ttype, sub};
+    max_n = (int)t.n > max_n ? (int)t.n : max_n;
+    max_rows = (int)t.nrow > max_rows ? (int)t.nrow : max_rows;
   }
-  // the sweep grid walks the task table in order: longest stripes (largest n)
-  // first, so they do not start last and set the tail
-  std::vector<int> by_len(count);
-  for (int i = 0; i < count; ++i) by_len[i] = i;
+  // tensor table ordered by (type, importance) so each codec group is one run
+  // of rows; the sweep table longest stripes (largest n) first, so they do not
+  // start last and set the tail
+  std::vector<int> by_kind(count), by_len(count);
+  for (int i = 0; i < count; ++i) by_kind[i] = by_len[i] = i;
+  std::stable_sort(by_kind.begin(), by_kind.end(), [&](int a, int b) {
+    if (ts[a].ttype != ts[b].ttype) return ts[a].ttype < ts[b].ttype;
+    return (ts[a].qw != nullptr) < (ts[b].qw != nullptr);
+  });
   std::stable_sort(by_len.begin(), by_len.end(),
                    [&](int a, int b) { return tasks[a].n > tasks[b].n; });
+  std::vector<EfGroup> groups;
+  for (int k = 0; k < count; ++k) {
+    const cp_ef_tensor& t = ts[by_kind[k]];
+    const int64_t nb = t.nrow * (t.n / 256);
+    if (groups.empty() || groups.back().ttype != t.ttype || groups.back().imat != (t.qw != nullptr))
+      groups.push_back(EfGroup{k, 0, t.ttype, t.qw != nullptr, 0});
+    EfGroup& g = groups.back();
+    ++g.count;
+    g.max_nb = nb > g.max_nb ? nb : g.max_nb;
+  }
   for (int c0 = 0; c0 < count; c0 += kTasksPerLaunch) {
     const int cn = count - c0 < kTasksPerLaunch ? count - c0 : kTasksPerLaunch;
     SweepBatch b;
     for (int i = 0; i < cn; ++i) b.t[i] = tasks[by_len[c0 + i]];
     ef_tasks_store_kernel<<<1, 64, 0, st>>>(b, cn, dtasks + c0);
   }
+  for (int c0 = 0; c0 < count; c0 += kDevPerStore) {
+    const int cn = count - c0 < kDevPerStore ? count - c0 : kDevPerStore;
+    EfDevBatch b;
+    for (int i = 0; i < cn; ++i) b.t[i] = devs[by_kind[c0 + i]];
+    ef_dev_store_kernel<<<1, 64, 0, st>>>(b, cn, dtab + c0);
+  }
+  const unsigned col_tiles = (unsigned)((max_n + 63) / 64), row_tiles = (unsigned)((max_rows + 63) / 64);
+  ef_index_kernel<<<dim3((unsigned)((max_n + 255) / 256), (unsigned)count), 256, 0, st>>>(dtab);
+  ef_transpose_kernel<0><<<dim3(col_tiles, row_tiles, (unsigned)count), 256, 0, st>>>(dtab);
   CP_LAUNCHED("EF setup");
   CP_PHASE(0);
 
   for (int it = 0; it < n_iter; ++it) {
-    for (int i = 0; i < count; ++i) {
-      const cp_ef_tensor& t = ts[i];
-      const EfLayout& L = lay[i];
-      const float* src = it == 0 ? t.x : (const float*)(base + L.Wcur);
-      if (int s = kq_quantize(t.ttype, src, t.nrow, t.n, t.qw, t.raw, st)) return s;
-      const int64_t thr = t.nrow * (t.n / 16);
-      ef_grid_kernel<<<(unsigned)((thr + 255) / 256), 256, 0, st>>>(
-          t.ttype, t.raw, (int)t.nrow, (int)t.n, (float*)(base + L.dlT), (float*)(base + L.mlT));
+    for (const EfGroup& g : groups) {
+      switch (g.ttype) {
+        case CP_Q2_K: launch_commit<CP_Q2_K>(dtab, g, it > 0, st); break;
+        case CP_Q3_K: launch_commit<CP_Q3_K>(dtab, g, it > 0, st); break;
+        case CP_Q4_K: launch_commit<CP_Q4_K>(dtab, g, it > 0, st); break;
+        default: launch_commit<CP_Q6_K>(dtab, g, it > 0, st); break;
+      }
     }
+    const int64_t grid_threads = (int64_t)max_rows * (max_n / 16);
+    ef_grid_kernel<<<dim3((unsigned)((grid_threads + 255) / 256), (unsigned)count), 256, 0, st>>>(dtab);
     CP_LAUNCHED("EF commit");
     CP_PHASE(1);
-    int rows = 0;
-    for (int i = 0; i < count; ++i) rows = tasks[i].nrow > rows ? tasks[i].nrow : rows;
     if (mode == CP_EF_EXACT_VALU)
-      ef_sweep_exact_kernel<BLK><<<dim3((unsigned)((rows + 255) / 256), (unsigned)count), 256, 0, st>>>(dtasks);
+      ef_sweep_exact_kernel<BLK><<<dim3((unsigned)((max_rows + 255) / 256), (unsigned)count), 256, 0, st>>>(dtasks);
     else if (mode == CP_EF_EXACT)
-      ef_sweep_r32_kernel<<<dim3((unsigned)((rows + 31) / 32), (unsigned)count), 64, 0, st>>>(dtasks);
+      ef_sweep_r32_kernel<<<dim3((unsigned)((max_rows + 31) / 32), (unsigned)count), 64, 0, st>>>(dtasks);
     else
-      ef_sweep_mfma_kernel<BLK><<<dim3((unsigned)((rows + 63) / 64), (unsigned)count), 64, 0, st>>>(dtasks);
+      ef_sweep_mfma_kernel<BLK><<<dim3((unsigned)((max_rows + 63) / 64), (unsigned)count), 64, 0, st>>>(dtasks);
     CP_LAUNCHED("EF sweep");
     CP_PHASE(2);
-    for (int i = 0; i < count; ++i) {
-      const cp_ef_tensor& t = ts[i];
-      const EfLayout& L = lay[i];
-      dim3 tg((unsigned)((t.n + 63) / 64), (unsigned)((t.nrow + 63) / 64));
-      ef_to_storage_kernel<uint8_t><<<tg, 256, 0, st>>>((const uint8_t*)(base + L.LT), (int)t.nrow,
-                                                        (int)t.n, (const int*)(base + L.inv),
-                                                        (uint8_t*)(base + L.Lrow));
-      KqGeom g;
-      kq_geom(t.ttype, &g);
-      const int span = t.ttype == CP_Q2_K ? 64 : t.ttype == CP_Q3_K ? 96 : t.ttype == CP_Q4_K ? 128 : 192;
-      const int64_t NB = t.nrow * (t.n / 256);
-      ef_repack_kernel<<<(unsigned)((NB * span + 255) / 256), 256, 0, st>>>(
-          t.ttype, (const uint8_t*)(base + L.Lrow), NB, t.raw);
-      if (it + 1 < n_iter)
-        ef_to_storage_kernel<float><<<tg, 256, 0, st>>>((const float*)(base + L.WcurT), (int)t.nrow,
-                                                        (int)t.n, (const int*)(base + L.inv),
-                                                        (float*)(base + L.Wcur));
-    }
+    ef_transpose_kernel<1><<<dim3(col_tiles, row_tiles, (unsigned)count), 256, 0, st>>>(dtab);
+    const int64_t max_nb = (int64_t)max_rows * (max_n / 256);
+    ef_repack_kernel<<<dim3((unsigned)((max_nb * 192 + 255) / 256), (unsigned)count), 256, 0, st>>>(dtab);
+    if (it + 1 < n_iter)
+      ef_transpose_kernel<2><<<dim3(col_tiles, row_tiles, (unsigned)count), 256, 0, st>>>(dtab);
     CP_LAUNCHED("EF repack");
     CP_PHASE(3);
   }
-  for (int i = 0; i < count; ++i)
-    if (ts[i].recon)
-      if (int s = kq_dequantize(ts[i].ttype, ts[i].raw, ts[i].nrow, ts[i].n, ts[i].recon, st)) return s;
+  for (const EfGroup& g : groups) {
+    switch (g.ttype) {
+      case CP_Q2_K: launch_decode<CP_Q2_K>(dtab, g, st); break;
+      case CP_Q3_K: launch_decode<CP_Q3_K>(dtab, g, st); break;
+      case CP_Q4_K: launch_decode<CP_Q4_K>(dtab, g, st); break;
+      default: launch_decode<CP_Q6_K>(dtab, g, st); break;
+    }
+  }
+  CP_LAUNCHED("EF decode");
   CP_PHASE(4);
   return CP_OK;
 }
