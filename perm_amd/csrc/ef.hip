@@ -246,49 +246,70 @@ typedef float f32x32 __attribute__((ext_vector_type(32)));
 // Row of the 32x32 MFMA result held by register v of lane l (column = l % 32).
 __device__ __forceinline__ int mfma32_row(int v, int l) { return 8 * (v >> 2) + 4 * (l >> 5) + (v & 3); }
 
-// Exact mode on the matrix cores with 32-row stripes and 64-column blocks.
-// One wave per 32-row stripe: a stripe's cross-block work is a sequential
-// chain (every column of a row depends on all earlier ones), and a 32-row
-// stripe halves that chain's length per wave against a 64-row one. For every
-// earlier column jj one v_mfma_f32_32x32x1_2b_f32 forms the 32 x 64 products
-// e_jj (x) U[jj][block] -- block 0 of the instruction takes columns 0-31, block 1
-// columns 32-63, both for the stripe's 32 rows -- with the inline-zero
-// accumulator (each product rounded once to float32), and the VALU subtracts
-// them in jj order; the products for jj + 1 are formed while those for jj are
-// subtracted. E and U for the next 8 columns are loaded while the current 8 are
-// applied. The in-block sweep runs on lanes 0-31 (lane = row), reading the
-// diagonal U tile through the scalar path.
-__global__ __launch_bounds__(64, 2) void ef_sweep_r32_kernel(const SweepTask* __restrict__ tasks) {
-  constexpr int B = 64, G = 8;
+// Exact mode on the matrix cores: one wave per stripe of RS rows (32 or 16),
+// 64-column blocks. A stripe's cross-block work is a sequential chain (every
+// column of a row depends on all earlier ones), so the stripe height sets the
+// chain each wave carries; 16-row stripes halve it for calls whose 32-row
+// stripes would not give every SIMD two waves. For every earlier column jj one
+// MFMA with k = 1 forms the RS x 64 products e_jj (x) U[jj][block]:
+// v_mfma_f32_32x32x1_2b_f32 (blocks = column halves) for RS = 32,
+// v_mfma_f32_16x16x1_4b_f32 (blocks = column quarters) for RS = 16, both with
+// the inline-zero accumulator, so each product is rounded once to float32; the
+// VALU subtracts them in jj order. The products for jj + 1 are formed while
+// those for jj are subtracted; E and U for the next 8 columns are loaded while
+// the current 8 are applied. The in-block sweep runs on lanes 0..RS-1 (lane =
+// row) with the block's diagonal U tile in LDS.
+template <int RS>
+struct StripeLayout;
+template <>
+struct StripeLayout<32> {  // register v of lane l -> (row, column) of the stripe's block
+  static constexpr int NV = 32;
+  __device__ static int row(int v, int l) { return mfma32_row(v & 15, l); }
+  __device__ static int col(int v, int l) { return 32 * (v >> 4) + (l & 31); }
+};
+template <>
+struct StripeLayout<16> {
+  static constexpr int NV = 16;
+  __device__ static int row(int v, int l) { return 4 * (l >> 4) + (v & 3); }
+  __device__ static int col(int v, int l) { return 16 * (v >> 2) + (l & 15); }
+};
+
+template <int RS>
+__global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* __restrict__ tasks) {
+  constexpr int B = 64, G = 8, NV = StripeLayout<RS>::NV, CPP = B * RS / 64;
+  typedef float fv __attribute__((ext_vector_type(NV)));
   const SweepTask tk = tasks[blockIdx.y];
-  const int row0 = blockIdx.x * 32;
+  const int row0 = blockIdx.x * RS;
   if (row0 >= tk.nrow) return;
-  const int l = threadIdx.x, cl = l & 31, half = l >> 5;
+  const int l = threadIdx.x, rl = l % RS, part = l / RS;
   const int nrow = tk.nrow, n = tk.n;
-  const int r = row0 + cl;
+  const int r = row0 + rl;
   const bool valid = r < nrow;
   const int rr = valid ? r : nrow - 1;
-  // one LDS buffer: the 32 x 64 target transpose, then the diagonal U tile
+  // one LDS buffer: the RS x 64 target transpose, then the diagonal U tile
   // aligned at its diagonal
   __shared__ __align__(16) float lds[B * B];
   __shared__ int sbo[B];
   float (*st)[B + 1] = reinterpret_cast<float (*)[B + 1]>(lds);
   float (*su)[B] = reinterpret_cast<float (*)[B]>(lds);
-  float* trow = st[cl];
+  float* trow = st[rl];
+  auto mfma = [](float a, float b) -> fv {
+    const fv z = {};
+    if constexpr (RS == 32)
+      return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, z, 0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, z, 0, 0, 0);
+  };
   for (int i1 = 0; i1 < n; i1 += B) {
-    // targets: lane l stages row cl, columns 32*half .. +31; then into the MFMA
-    // layout: register v -> row mfma32_row(v % 16, l), column 32 * (v / 16) + cl
+    // targets: lane l stages row rl, columns part * CPP .. + CPP - 1, then
+    // moves to the MFMA layout
 #pragma unroll
-    for (int k = 0; k < 32; ++k)
-      trow[32 * half + k] = ld_lane(tk.WpT, (int64_t)(i1 + 32 * half + k) * nrow + rr);
+    for (int k = 0; k < CPP; ++k)
+      trow[part * CPP + k] = ld_lane(tk.WpT, (int64_t)(i1 + part * CPP + k) * nrow + rr);
     __syncthreads();
-    f32x32 t;
+    fv t;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      t[v] = st[mfma32_row(v, l)][cl];
-      t[16 + v] = st[mfma32_row(v, l)][32 + cl];
-    }
-    const f32x32 nz = {};
+    for (int v = 0; v < NV; ++v) t[v] = st[StripeLayout<RS>::row(v, l)][StripeLayout<RS>::col(v, l)];
     if (i1 > 0) {
       float ea[G], ua[G], eb[G], ub[G];
       auto load = [&](int g, float (&e)[G], float (&u)[G]) {
@@ -303,24 +324,23 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_r32_kernel(const SweepTask* __
       load(0, ea, ua);
 #pragma unroll
       for (int q = 0; q < G; ++q) eb[q] = ub[q] = 0.0f;
-      f32x32 P0 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[0], ua[0], nz, 0, 0, 0), P1;
+      fv P0 = mfma(ea[0], ua[0]), P1;
       for (int g = 0; g < groups; ++g) {
         if (g + 1 < groups) load(g + 1, eb, ub);
 #pragma unroll
         for (int q = 0; q < G; q += 2) {
           // P0 holds column g*G + q, P1 column g*G + q + 1; the last group's
           // final products are unused
-          P1 = __builtin_amdgcn_mfma_f32_32x32x1f32(ea[q + 1], ua[q + 1], nz, 0, 0, 0);
+          P1 = mfma(ea[q + 1], ua[q + 1]);
 #pragma unroll
-          for (int v = 0; v < 32; ++v) t[v] = t[v] - P0[v];
-          P0 = __builtin_amdgcn_mfma_f32_32x32x1f32(q + 2 < G ? ea[q + 2] : eb[0],
-                                                    q + 2 < G ? ua[q + 2] : ub[0], nz, 0, 0, 0);
+          for (int v = 0; v < NV; ++v) t[v] = t[v] - P0[v];
+          P0 = mfma(q + 2 < G ? ea[q + 2] : eb[0], q + 2 < G ? ua[q + 2] : ub[0]);
 #pragma unroll
-          for (int v = 0; v < 32; ++v) t[v] = t[v] - P1[v];
+          for (int v = 0; v < NV; ++v) t[v] = t[v] - P1[v];
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
         }
 #pragma unroll
         for (int q = 0; q < G; ++q) {
@@ -331,10 +351,7 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_r32_kernel(const SweepTask* __
     }
     __syncthreads();
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      st[mfma32_row(v, l)][cl] = t[v];
-      st[mfma32_row(v, l)][32 + cl] = t[16 + v];
-    }
+    for (int v = 0; v < NV; ++v) st[StripeLayout<RS>::row(v, l)][StripeLayout<RS>::col(v, l)] = t[v];
     __syncthreads();
     float ts[B];
 #pragma unroll
@@ -352,7 +369,7 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_r32_kernel(const SweepTask* __
     }
     sbo[l] = tk.sbidx[i1 + l] * nrow;
     __syncthreads();
-    if (half == 0) sweep_block_rl<B>(tk, i1, r, rr, valid, ts, su, sbo);
+    if (l < RS) sweep_block_rl<B>(tk, i1, r, rr, valid, ts, su, sbo);
     __syncthreads();
   }
 }
@@ -822,6 +839,9 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     for (int i = 0; i < cn; ++i) b.t[i] = devs[by_kind[c0 + i]];
     ef_dev_store_kernel<<<1, 64, 0, st>>>(b, cn, dtab + c0);
   }
+  // 32-row stripes unless they would leave SIMDs with fewer than two waves (256 CUs x 4)
+  int64_t stripes32 = 0;
+  for (int i = 0; i < count; ++i) stripes32 += (ts[i].nrow + 31) / 32;
   const unsigned col_tiles = (unsigned)((max_n + 63) / 64), row_tiles = (unsigned)((max_rows + 63) / 64);
   ef_index_kernel<<<dim3((unsigned)((max_n + 255) / 256), (unsigned)count), 256, 0, st>>>(dtab);
   ef_transpose_kernel<0><<<dim3(col_tiles, row_tiles, (unsigned)count), 256, 0, st>>>(dtab);
@@ -843,8 +863,10 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     CP_PHASE(1);
     if (mode == CP_EF_EXACT_VALU)
       ef_sweep_exact_kernel<BLK><<<dim3((unsigned)((max_rows + 255) / 256), (unsigned)count), 256, 0, st>>>(dtasks);
+    else if (mode == CP_EF_EXACT && stripes32 >= 2 * 1024)
+      ef_sweep_rows_kernel<32><<<dim3((unsigned)((max_rows + 31) / 32), (unsigned)count), 64, 0, st>>>(dtasks);
     else if (mode == CP_EF_EXACT)
-      ef_sweep_r32_kernel<<<dim3((unsigned)((max_rows + 31) / 32), (unsigned)count), 64, 0, st>>>(dtasks);
+      ef_sweep_rows_kernel<16><<<dim3((unsigned)((max_rows + 15) / 16), (unsigned)count), 64, 0, st>>>(dtasks);
     else
       ef_sweep_mfma_kernel<BLK><<<dim3((unsigned)((max_rows + 63) / 64), (unsigned)count), 64, 0, st>>>(dtasks);
     CP_LAUNCHED("EF sweep");
