@@ -262,7 +262,7 @@ def main():
         flops_per_launch = ef_flops / sweep_launches
         ach = flops_per_launch / (avg_ms * 1e-3) / 1e12
         roof = {"kernel": ("ef_sweep_mfma_kernel" if mode == _lib.CP_EF_MFMA
-                           else "ef_sweep_r32_kernel"), "bound": "mfma", "achieved": ach,
+                           else "ef_sweep_rows_kernel"), "bound": "mfma", "achieved": ach,
                 "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_FP32_TFLOPS,
                 "traffic": None, "avg_launch_ms": avg_ms, "launches_per_step": sweep_launches}
 

@@ -13,6 +13,8 @@
 //        lane, so the [t][i] panel is used as loaded.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "cp_host.h"
 
 namespace cp {
@@ -31,16 +33,18 @@ __device__ __forceinline__ int mfma32_row(int v, int l) { return 8 * (v >> 2) + 
 // the lower triangle into the upper one afterwards), split-K over rows of X.
 // A workgroup is 4 waves, each owning a 128 x 128 block as 4 x 4 MFMA 32x32
 // tiles (256 float32 accumulators): the largest block a wave can hold, because
-// the LDS reads per MFMA, not the MFMAs, bound this kernel.
+// the LDS traffic per MFMA, not the MFMAs, bounds this kernel.
 //
 // Rows of X are staged 32 at a time: both 32 x 256 panels (columns of the i-
 // and j-tile; one panel on a diagonal tile) are fetched into registers two
-// stages ahead of use, stored into a 3-slot LDS ring in X's own [t][c] layout,
+// stages ahead of use, stored into a 4-slot LDS ring in X's own [t][c] layout,
 // and read as MFMA operands with ds_read_b64_tr_b16, which returns 4
 // consecutive rows t of one column per lane: v_mfma_f32_32x32x16_bf16 takes 8
-// consecutive t per lane for both operands. Panel rows are 512 bytes, so the
-// four rows of one transposed read would share banks; 64-byte chunks are
-// XOR-swizzled by t & 3 to spread them over all banks.
+// consecutive t per lane for both operands. Panel rows are padded from 512 to
+// 576 bytes so the four rows of one transposed read fall 64 bytes apart in
+// bank space (conflict-free), and every LDS address in the loop is a per-lane
+// base plus an immediate: with one wave per SIMD, address arithmetic between
+// the MFMAs is not hidden by anything.
 //
 // Work items (row split, tile) are ordered split-major and handed out
 // XCD-contiguously: the hardware places workgroup w on XCD w % 8, so
@@ -48,75 +52,88 @@ __device__ __forceinline__ int mfma32_row(int v, int l) { return 8 * (v >> 2) + 
 // rows of X (shared in its L2).
 constexpr int BT = 256;             // H tile edge
 constexpr int KS = 32;              // rows of X per stage
-constexpr int PROW = BT * 2;        // bytes per panel row
-constexpr int PANEL = KS * PROW;    // 16 KB
+constexpr int PROW = BT * 2 + 64;   // bytes per padded panel row
+constexpr int PANEL = KS * PROW;    // 18 KB
 constexpr int HNT = 256;            // threads per workgroup
-constexpr int NSLOT = 3;            // LDS ring
+constexpr int NSLOT = 4;            // LDS ring (stage s in slot s % 4)
 constexpr int CPT = 2048 / HNT;     // 16-byte chunks per thread per stage (two panels)
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef short v8i16 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) v4i16* lds_v4p;
 
-__device__ __forceinline__ int pofs(int t, int c) {  // byte offset of (row t, bf16 column c)
-  const int b = 2 * c;
-  return t * PROW + ((((b >> 6) ^ (t & 3)) << 6) | (b & 63));
-}
+// Global side of the staging: raw buffer loads over the workgroup's row split
+// (base X + r0 * d, num_records = its byte length). A load whose offset is at or
+// past num_records returns zeros, so rows past the split's end and 8-column
+// chunks past d (given an offset past the end) need no branch, and the loop
+// has no control flow between loads: the compiler then waits only for the
+// load a store needs, not for every load in flight.
+//
+// Chunk q of a stage (16 bytes per thread, q < 4 on the i-panel, q >= 4 on the
+// j-panel): row (tid / 32) + 8 (q % 4), column chunk tid % 32.
+constexpr uint32_t kOob = 0x80000000u;  // past any num_records the host allows
 
-// chunk ch of a stage: panel ch / 1024, row (ch % 1024) / 32, 16-byte column chunk ch % 32
-template <bool DIAG>
-__device__ __forceinline__ void stage_load(const uint16_t* X, int64_t N, int d, int64_t t0, int i0,
-                                           int j0, int tid, uint4 (&g)[CPT]) {
+template <int NQ>
+struct Stager {
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t off[NQ];  // chunk q's byte offset at stage 0 (kOob when outside d)
+  uint32_t sbytes;   // bytes per stage (KS rows)
+};
+
+template <int NQ>
+__device__ __forceinline__ Stager<NQ> make_stager(const uint16_t* X, int64_t r0, int64_t nrows,
+                                                  int d, int i0, int j0, int tid) {
+  Stager<NQ> s;
+  const uint32_t rowb = 2u * (uint32_t)d;
+  s.rs = __builtin_amdgcn_make_buffer_rsrc((void*)(X + r0 * d), 0, (int)(nrows * rowb), 0x00020000);
+  const int c8 = 8 * (tid & 31);
+  const uint32_t row0 = (uint32_t)(tid >> 5) * rowb;
 #pragma unroll
-  for (int q = 0; q < (DIAG ? CPT / 2 : CPT); ++q) {
-    const int ch = tid + HNT * q, panel = ch >> 10, row = (ch & 1023) >> 5, c16 = ch & 31;
-    const int64_t t = t0 + row;
-    const int c = (panel ? j0 : i0) + 8 * c16;  // d % 8 == 0: 8 columns all in or all out
-    uint4 z = make_uint4(0, 0, 0, 0);
-    if (t < N && c < d) z = *reinterpret_cast<const uint4*>(X + t * d + c);
-    g[q] = z;
+  for (int q = 0; q < NQ; ++q) {
+    const int c = (q >= 4 ? j0 : i0) + c8;  // d % 8 == 0: the 8 columns are all in or all out
+    s.off[q] = c < d ? row0 + (uint32_t)(8 * (q & 3)) * rowb + 2u * (uint32_t)c : kOob;
   }
+  s.sbytes = (uint32_t)KS * rowb;
+  return s;
 }
 
-template <bool DIAG>
-__device__ __forceinline__ void stage_store(char* slot, int tid, const uint4 (&g)[CPT]) {
-#pragma unroll
-  for (int q = 0; q < (DIAG ? CPT / 2 : CPT); ++q) {
-    const int ch = tid + HNT * q, panel = ch >> 10, row = (ch & 1023) >> 5, c16 = ch & 31;
-    *reinterpret_cast<uint4*>(slot + panel * PANEL + pofs(row, 8 * c16)) = g[q];
-  }
+template <int NQ>
+__device__ __forceinline__ void stage_load_one(const Stager<NQ>& st, int s, uint4 (&g)[CPT], int q) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(st.rs, (int)(st.off[q] + (uint32_t)s * st.sbytes),
+                                                       0, 0);
+  g[q] = make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// MFMA operand for columns col..col+31 and rows krow..krow+15 of a panel:
-// lane l gets column col + l % 32, rows krow + 8 * (l / 32) + 0..7
-__device__ __forceinline__ bf16x8 operand(const char* panel, int krow, int col, int l) {
-  const int g = l >> 4, c = l & 15;
-  const int row = krow + 8 * (g >> 1) + (c >> 2);
-  const int cc = col + 16 * (g & 1) + 4 * (c & 3);
-  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4p)(panel + pofs(row, cc)));
-  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4p)(panel + pofs(row + 4, cc)));
-  const v8i16 r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(bf16x8, r);
-}
+// LDS byte offset of chunk q within a slot, relative to the thread's store base
+// (tid / 32) * PROW + 16 * (tid % 32)
+__device__ __forceinline__ constexpr int chunk_ofs(int q) { return (q >> 2) * PANEL + 8 * (q & 3) * PROW; }
 
 struct Operands {
   bf16x8 a[4], b[4];
 };
 
-__device__ __forceinline__ void read_operands(const char* pa, const char* pb, int half, int wm,
-                                              int wn, int l, Operands& f) {
-#pragma unroll
-  for (int x = 0; x < 4; ++x) f.a[x] = operand(pa, 16 * half, wm + 32 * x, l);
-#pragma unroll
-  for (int y = 0; y < 4; ++y) f.b[y] = operand(pb, 16 * half, wn + 32 * y, l);
-}
-
-__device__ __forceinline__ void multiply(const Operands& f, f32x16 (&acc)[4][4]) {
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 4; ++y)
-      acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[x], f.b[y], acc[x][y], 0, 0, 0);
+// Piece i (0..15) of one half of a stage's operands: the lo or hi four rows of
+// one operand, in the order a0, b0, b1, b2, b3, a1, a2, a3 -- the order the
+// MFMAs (x, y) = (i / 4, i % 4) first use them. ra / rb: this lane's read base
+// in the A / B panel of the slot; the rest of the address is an immediate.
+// Lane l gets column col + l % 32, rows 8 * (l / 32) + 0..7 of the half.
+__device__ __forceinline__ void read_piece(const char* ra, const char* rb, int half, int i,
+                                           Operands& f) {
+  const int op = i >> 1, hi = i & 1;
+  const bool isb = op >= 1 && op <= 4;
+  const int idx = isb ? op - 1 : (op == 0 ? 0 : op - 4);
+  const char* p = (isb ? rb : ra) + (16 * half + 4 * hi) * PROW + 64 * idx;
+  const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4p)p);
+  const v8i16 w = __builtin_shufflevector(v, v, 0, 1, 2, 3, 0, 1, 2, 3);
+  v8i16 cur = __builtin_bit_cast(v8i16, isb ? f.b[idx] : f.a[idx]);
+  if (hi)
+    cur = __builtin_shufflevector(cur, w, 0, 1, 2, 3, 12, 13, 14, 15);
+  else
+    cur = __builtin_shufflevector(w, cur, 0, 1, 2, 3, 12, 13, 14, 15);
+  if (isb)
+    f.b[idx] = __builtin_bit_cast(bf16x8, cur);
+  else
+    f.a[idx] = __builtin_bit_cast(bf16x8, cur);
 }
 
 template <bool DIAG>
@@ -124,37 +141,87 @@ __device__ __forceinline__ void tile_rows(const uint16_t* X, int64_t r0, int64_t
                                           int j0, char* lds, f32x16 (&acc)[4][4]) {
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int wm = (w >> 1) * 128, wn = (w & 1) * 128;
-  const int ns = (int)((r1 - r0 + KS - 1) / KS);
+  constexpr int NQ = DIAG ? CPT / 2 : CPT;  // 16-byte chunks per thread per stage
   constexpr int SLOT = DIAG ? PANEL : 2 * PANEL;
-  auto pa = [&](int s) -> const char* { return lds + (s % NSLOT) * SLOT; };
-  auto pb = [&](int s) -> const char* { return DIAG ? pa(s) : pa(s) + PANEL; };
-  // rows past r1 load as zeros, so a short split needs no special case
+  // stages rounded up to a multiple of 4 (the unrolled loop body): stages past
+  // the split's end load as zeros and add nothing
+  const int ns = (int)((r1 - r0 + 4 * KS - 1) / (4 * KS)) * 4;
+  const Stager<NQ> st = make_stager<NQ>(X, r0, r1 - r0, d, i0, j0, tid);
+  // per-lane LDS bases: transposed reads (row 8 * (g / 2) + c / 4, column
+  // 16 * (g % 2) + 4 * (c % 4) of the wave's block, g = l / 16, c = l % 16) and
+  // stores (row tid / 32, 16-byte chunk tid % 32)
+  const int g4 = l >> 4, c4 = l & 15;
+  const int rlane = (8 * (g4 >> 1) + (c4 >> 2)) * PROW + 2 * (16 * (g4 & 1) + 4 * (c4 & 3));
+  char* const ra0 = lds + rlane + 2 * wm;
+  char* const rb0 = lds + rlane + 2 * wn + (DIAG ? 0 : PANEL);
+  char* const wr0 = lds + (tid >> 5) * PROW + 16 * (tid & 31);
   uint4 g0[CPT], g1[CPT];
-  stage_load<DIAG>(X, r1, d, r0, i0, j0, tid, g0);
-  stage_load<DIAG>(X, r1, d, r0 + KS, i0, j0, tid, g1);
-  stage_store<DIAG>(lds, tid, g0);
-  stage_store<DIAG>(lds + SLOT, tid, g1);
-  stage_load<DIAG>(X, r1, d, r0 + 2 * KS, i0, j0, tid, g0);
-  stage_load<DIAG>(X, r1, d, r0 + 3 * KS, i0, j0, tid, g1);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) stage_load_one(st, 0, g0, q);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) stage_load_one(st, 1, g1, q);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) *reinterpret_cast<uint4*>(wr0 + chunk_ofs(q)) = g0[q];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) *reinterpret_cast<uint4*>(wr0 + SLOT + chunk_ofs(q)) = g1[q];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) stage_load_one(st, 2, g0, q);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) stage_load_one(st, 3, g1, q);
   __syncthreads();
   Operands f0, f1;
-  read_operands(pa(0), pb(0), 0, wm, wn, l, f0);
-  // stage s: store stage s + 2 (fetched two stages ago) into the slot stage
-  // s - 1 used, fetch stage s + 4 into the same registers, and multiply stage
-  // s while reading the next operands (its second half, then the first half of
-  // stage s + 1)
-  auto step = [&](int s, uint4 (&g)[CPT]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) read_piece(ra0, rb0, 0, i, f0);
+  // Stage s (K = s % 4): store stage s + 2 (fetched two stages ago) into slot
+  // K + 2, fetch stage s + 4 into the same registers, and multiply stage s
+  // while reading the next operands (its second half, then the first half of
+  // stage s + 1). Past the end the same steps run on zero stages and slots no
+  // stage reads, so the body has no branches.
+  //
+  // With one wave per SIMD nothing hides a wave's own LDS waits, so the step
+  // is issued as one interleaved stream, pinned in place by scheduling
+  // barriers: each of the 32 MFMAs is followed by one of the 32 transposed
+  // reads of the next operands, and the stores are spread over the step, each
+  // chunk's store followed by the load of the same chunk four stages ahead
+  // (so every store waits only for the oldest load in flight), keeping the
+  // LDS busy while the MFMAs run instead of the two taking turns.
+  auto step = [&](auto kc, int s, uint4 (&g)[CPT]) {
+    constexpr int K = decltype(kc)::value;
     __syncthreads();
-    if (s + 2 < ns) stage_store<DIAG>(lds + ((s + 2) % NSLOT) * SLOT, tid, g);
-    if (s + 4 < ns) stage_load<DIAG>(X, r1, d, r0 + (int64_t)(s + 4) * KS, i0, j0, tid, g);
-    read_operands(pa(s), pb(s), 1, wm, wn, l, f1);
-    multiply(f0, acc);
-    if (s + 1 < ns) read_operands(pa(s + 1), pb(s + 1), 0, wm, wn, l, f0);
-    multiply(f1, acc);
+    const char* ra = ra0 + K * SLOT;
+    const char* rb = rb0 + K * SLOT;
+    const char* na = ra0 + ((K + 1) % NSLOT) * SLOT;
+    const char* nb = rb0 + ((K + 1) % NSLOT) * SLOT;
+    char* dst = wr0 + ((K + 2) % NSLOT) * SLOT;
+    constexpr int SE = 32 / NQ;  // MFMAs per store
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0.a[i >> 2], f0.b[i & 3],
+                                                                   acc[i >> 2][i & 3], 0, 0, 0);
+      read_piece(ra, rb, 1, i, f1);
+      if (i % SE == 0) {
+        *reinterpret_cast<uint4*>(dst + chunk_ofs(i / SE)) = g[i / SE];
+        stage_load_one(st, s + 4, g, i / SE);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1.a[i >> 2], f1.b[i & 3],
+                                                                   acc[i >> 2][i & 3], 0, 0, 0);
+      read_piece(na, nb, 0, i, f0);
+      if (i % SE == 0) {
+        *reinterpret_cast<uint4*>(dst + chunk_ofs(NQ / 2 + i / SE)) = g[NQ / 2 + i / SE];
+        stage_load_one(st, s + 4, g, NQ / 2 + i / SE);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
-  for (int s = 0; s < ns; s += 2) {
-    step(s, g0);
-    if (s + 1 < ns) step(s + 1, g1);
+  for (int s = 0; s < ns; s += 4) {
+    step(std::integral_constant<int, 0>(), s, g0);
+    step(std::integral_constant<int, 1>(), s + 1, g1);
+    step(std::integral_constant<int, 2>(), s + 2, g0);
+    step(std::integral_constant<int, 3>(), s + 3, g1);
   }
 }
 
@@ -280,13 +347,15 @@ __global__ __launch_bounds__(256) void hess_f32_kernel(const float* __restrict__
 
 // Row splits for the triangle kernel: one 96 KB-LDS workgroup per CU, so the
 // time is about rounds x (stages per split + epilogue); the epilogue's
-// atomics cost about 16 stages.
-static int pick_splits(int ntiles, int64_t N) {
-  int best_s = 1;
+// atomics cost about 16 stages. A split spans at most 2^30 bytes of X, so the
+// buffer offsets of its loads (up to eight stages past its end) stay below 2^31.
+static int pick_splits(int ntiles, int64_t N, int64_t d) {
+  int best_s = 0;
   double best = 1e30;
-  for (int s = 1; s <= 512; ++s) {
+  for (int s = 1; s <= 4096; ++s) {
     const int64_t rows = (N + s - 1) / s;
-    if (s > 1 && rows < 256) break;
+    if ((rows + KS - 1) / KS * KS * 2 * d > (int64_t(1) << 30)) continue;
+    if (best_s && rows < 256) break;
     const double stages = (double)((rows + KS - 1) / KS);
     const double rounds = (double)(((int64_t)ntiles * s + 255) / 256);
     const double cost = rounds * (stages + 16.0);
@@ -311,7 +380,10 @@ extern "C" int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, f
   if (x_dtype == 1) {
     const int T = (int)((d + cp::BT - 1) / cp::BT);
     const int ntiles = T * (T + 1) / 2;
-    const int splits = cp::pick_splits(ntiles, N);
+    const int splits = cp::pick_splits(ntiles, N, d);
+    if (splits == 0 || (int64_t)ntiles * splits * 8 > INT32_MAX)
+      return cp::set_error(CP_ERR_SHAPE, "X [%lld, %lld] too large for one accumulation; pass fewer rows",
+                           (long long)N, (long long)d);
     int64_t rps = (N + splits - 1) / splits;
     rps = (rps + cp::KS - 1) / cp::KS * cp::KS;
     const int total = ntiles * splits;

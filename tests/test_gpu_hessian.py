@@ -16,7 +16,7 @@ def hs():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("N,d", [(4096, 1024), (1000, 200), (33, 136), (70000, 256)])
+@pytest.mark.parametrize("N,d", [(4096, 1024), (1000, 200), (33, 136), (70000, 256), (12345, 1032)])
 def test_xtx_matches_closed_form(hs, dtype, N, d):
     print(f"xtx {dtype} N={N} d={d}", flush=True)
     g = torch.Generator(device="cuda").manual_seed(N + d)
