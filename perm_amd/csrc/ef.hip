@@ -128,43 +128,78 @@ __device__ __forceinline__ void sweep_block(const SweepTask& tk, int i1, int r, 
 // right-looking: ts[k] holds the target of column cb + k, so the column being
 // quantized is always ts[0], and subtracting e_cb * U[cb][cb + k] from ts[k]
 // moves it to ts[k - 1] in the same step. Each element still receives its
-// updates one at a time in ascending column order (ef.py:199-213). sud is the
-// block's diagonal U tile aligned at the diagonal, sud[a][k] = U[i1 + a][i1 + a
-// + k] (zero past the tile). The grid step and offset of column cb + EF_Q are
-// fetched into the ring slot that column cb frees (slot = cb % EF_Q, static
-// inside the unrolled group, so no slot is copied while its load is in flight).
+// updates one at a time in ascending column order (ef.py:199-213).
+//
+// The block's diagonal U tile is read aligned at the diagonal, row cb giving
+// U[i1 + cb][i1 + cb + k]. A row is read only by the 16-column piece it falls
+// in, up to that piece's KMAX = 64 - 16 * piece entries, so the tile is kept
+// compact: row a holds KMAX(a) floats from tile_ofs(a) (10 KB instead of 16),
+// entries past the block zero. sg[k][rl] / sm[k][rl] hold the committed grid
+// step and offset of column k of the current half block for the stripe's row
+// rl, staged in LDS so no global load sits on the column-to-column chain. A
+// zero step quantizes to code 0 with e = 0; the divisions run on a safe
+// divisor and are selected away, so the column has no branches.
 constexpr int EF_Q = 2;
+constexpr int TILE_FLOATS = 16 * (64 + 48 + 32 + 16);
 
-// Columns cb0 .. cb0 + 15 of the block; only queue positions below KMAX still
-// hold columns of the block (KMAX = B - cb0).
-template <int KMAX, int B>
-__device__ __forceinline__ void sweep_cols(const SweepTask& tk, int i1, int r, int rr, bool valid,
-                                           float (&ts)[B], const float (*sud)[B], const int* sbo,
-                                           int cb0, float (&dq)[EF_Q], float (&mq)[EF_Q]) {
+__device__ __forceinline__ constexpr int tile_base(int piece) {
+  return piece == 0 ? 0 : piece == 1 ? 16 * 64 : piece == 2 ? 16 * (64 + 48) : 16 * (64 + 48 + 32);
+}
+__device__ __forceinline__ int tile_ofs(int a) {
+  const int piece = a >> 4;
+  return tile_base(piece) + (a & 15) * (64 - 16 * piece);
+}
+
+// Quantization of one column for one row (ef.py:199-208): code q on the
+// committed grid (step dl, offset ml; a zero step gives code 0 and e = 0) and
+// the scaled error e = (t - recon) / U[j][j], in the reference's float32 order.
+__device__ __forceinline__ void quantize_col(const SweepTask& tk, float t, float dl, float ml,
+                                             float diag, float& e, int& q) {
+  const bool nz = dl != 0.0f;
+  const int qv = clampi(rint_magic((t + ml) / (nz ? dl : 1.0f)), tk.lo, tk.hi);
+  q = nz ? qv : 0;
+  const float recon = dl * (float)q - ml;
+  const float ev = (t - recon) / diag;
+  e = nz ? ev : 0.0f;
+}
+
+// Columns cb0 .. cb0 + 15 of the block (KMAX = B - cb0); the grid arrays hold
+// the half block starting at column hb. Software-pipelined: as soon as column
+// cb's error is known, column cb + 1's final target ts[1] - e * U[cb][cb + 1]
+// is formed and its quantization (two divisions, a serial chain) is issued in
+// the same scheduling region as column cb's remaining updates, which fill the
+// chain's latency. The first column of the piece is quantized up front.
+template <int KMAX, int B, int RS>
+__device__ __forceinline__ void sweep_cols(const SweepTask& tk, int i1, int r, int rl, bool valid,
+                                           float (&ts)[B], const float* tile,
+                                           const float (*sg)[RS], const float (*sm)[RS], int cb0,
+                                           int hb) {
   const int nrow = tk.nrow;
+  constexpr int piece = (B - KMAX) / 16;
+  const float* prow = tile + tile_base(piece);  // row cb0 + a at prow + a * KMAX
+  float e, t0 = ts[0];
+  int q;
+  quantize_col(tk, t0, sg[cb0 - hb][rl], sm[cb0 - hb][rl], prow[0], e, q);
 #pragma unroll 1
   for (int h = 0; h < 16; h += EF_Q) {
 #pragma unroll
     for (int j = 0; j < EF_Q; ++j) {
-      const int cb = cb0 + h + j, c = i1 + cb;
-      const float dl = dq[j], ml = mq[j];
-      if (cb + EF_Q < B) {
-        const int64_t o = (int64_t)sbo[cb + EF_Q] + rr;
-        dq[j] = ld_lane(tk.dlT, o);
-        mq[j] = tk.mlT ? ld_lane(tk.mlT, o) : 0.0f;
-      }
-      const float4* urow = reinterpret_cast<const float4*>(sud[cb]);
+      const int a = h + j, cb = cb0 + a, c = i1 + cb;
+      const float4* urow = reinterpret_cast<const float4*>(prow + a * KMAX);
       const float4 u0 = urow[0];
-      const bool nz = dl != 0.0f;
-      const int q = nz ? clampi(rint_magic((ts[0] + ml) / dl), tk.lo, tk.hi) : 0;
-      const float recon = dl * (float)q - ml;
-      const float e = nz ? (ts[0] - recon) / u0.x : 0.0f;
+      // next column of this piece (the last column quantizes itself again,
+      // discarded: the next piece starts with its own first column)
+      const int an = a + 1 < 16 ? a + 1 : a;
+      const float tn = ts[1] - e * u0.y;
+      float en;
+      int qn;
+      quantize_col(tk, tn, sg[cb0 + an - hb][rl], sm[cb0 + an - hb][rl], prow[an * KMAX], en, qn);
       if (valid) {
         ((GlobFw)tk.E)[(int64_t)c * nrow + r] = e;
-        ((GlobFw)tk.WcurT)[(int64_t)c * nrow + r] = ts[0];
+        ((GlobFw)tk.WcurT)[(int64_t)c * nrow + r] = t0;
         ((GlobBw)tk.LT)[(int64_t)c * nrow + r] = (uint8_t)(q - tk.lo);
       }
-      ts[0] = ts[1] - e * u0.y;
+      ts[0] = tn;
       ts[1] = ts[2] - e * u0.z;
       ts[2] = ts[3] - e * u0.w;
 #pragma unroll
@@ -175,28 +210,49 @@ __device__ __forceinline__ void sweep_cols(const SweepTask& tk, int i1, int r, i
         ts[4 * k4 + 1] = ts[4 * k4 + 2] - e * u.z;
         ts[4 * k4 + 2] = ts[4 * k4 + 3] - e * u.w;
       }
+      e = en;
+      q = qn;
+      t0 = tn;
       __builtin_amdgcn_sched_barrier(0);  // one column's tile row in registers at a time
     }
   }
 }
 
-// sbo[k] = (storage sub-block of column i1 + k) * nrow, staged in LDS so that
-// the grid fetches wait on nothing but LDS.
-template <int B>
-__device__ __forceinline__ void sweep_block_rl(const SweepTask& tk, int i1, int r, int rr, bool valid,
-                                               float (&ts)[B], const float (*sud)[B], const int* sbo) {
-  static_assert(B == 64, "four 16-column pieces");
-  float dq[EF_Q], mq[EF_Q];
+// The committed grid step / offset of block columns hb .. hb + 31 for the
+// stripe's rows: lane l covers row l % RS and every (64 / RS)-th column.
+// load_grid issues the loads into registers, store_grid writes them to sg /
+// sm. sbo[k] = (storage sub-block of block column k) * nrow.
+template <int RS>
+struct GridHalf {
+  static constexpr int P = 64 / RS, NC = 32 / P;
+  float d[NC], m[NC];
+};
+
+template <int RS>
+__device__ __forceinline__ void load_grid(const SweepTask& tk, const int* sbo, int hb, int l, int rr,
+                                          GridHalf<RS>& g) {
+  constexpr int P = GridHalf<RS>::P, NC = GridHalf<RS>::NC;
+  const int part = l / RS;
 #pragma unroll
-  for (int j = 0; j < EF_Q; ++j) {
-    const int64_t o = (int64_t)sbo[j] + rr;
-    dq[j] = ld_lane(tk.dlT, o);
-    mq[j] = tk.mlT ? ld_lane(tk.mlT, o) : 0.0f;
+  for (int k = 0; k < NC; ++k) g.d[k] = ld_lane(tk.dlT, (int64_t)sbo[hb + part + P * k] + rr);
+  if (tk.mlT) {
+#pragma unroll
+    for (int k = 0; k < NC; ++k) g.m[k] = ld_lane(tk.mlT, (int64_t)sbo[hb + part + P * k] + rr);
+  } else {
+#pragma unroll
+    for (int k = 0; k < NC; ++k) g.m[k] = 0.0f;
   }
-  sweep_cols<64, B>(tk, i1, r, rr, valid, ts, sud, sbo, 0, dq, mq);
-  sweep_cols<48, B>(tk, i1, r, rr, valid, ts, sud, sbo, 16, dq, mq);
-  sweep_cols<32, B>(tk, i1, r, rr, valid, ts, sud, sbo, 32, dq, mq);
-  sweep_cols<16, B>(tk, i1, r, rr, valid, ts, sud, sbo, 48, dq, mq);
+}
+
+template <int RS>
+__device__ __forceinline__ void store_grid(const GridHalf<RS>& g, int l, float (*sg)[RS], float (*sm)[RS]) {
+  constexpr int P = GridHalf<RS>::P, NC = GridHalf<RS>::NC;
+  const int rl = l % RS, part = l / RS;
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    sg[part + P * k][rl] = g.d[k];
+    sm[part + P * k][rl] = g.m[k];
+  }
 }
 
 template <int B>
@@ -286,12 +342,14 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
   const int r = row0 + rl;
   const bool valid = r < nrow;
   const int rr = valid ? r : nrow - 1;
-  // one LDS buffer: the RS x 64 target transpose, then the diagonal U tile
-  // aligned at its diagonal
-  __shared__ __align__(16) float lds[B * B];
+  // one LDS buffer: the RS x 64 target transpose, then the compact diagonal
+  // U tile; the grid steps / offsets of half a block; about 18 KB in all, so
+  // every SIMD keeps two of these one-wave workgroups
+  static_assert(RS * (B + 1) <= TILE_FLOATS, "target transpose fits the tile buffer");
+  __shared__ __align__(16) float lds[TILE_FLOATS];
   __shared__ int sbo[B];
+  __shared__ float sg[32][RS], sm[32][RS];
   float (*st)[B + 1] = reinterpret_cast<float (*)[B + 1]>(lds);
-  float (*su)[B] = reinterpret_cast<float (*)[B]>(lds);
   float* trow = st[rl];
   auto mfma = [](float a, float b) -> fv {
     const fv z = {};
@@ -303,6 +361,7 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
   for (int i1 = 0; i1 < n; i1 += B) {
     // targets: lane l stages row rl, columns part * CPP .. + CPP - 1, then
     // moves to the MFMA layout
+    sbo[l] = tk.sbidx[i1 + l] * nrow;
 #pragma unroll
     for (int k = 0; k < CPP; ++k)
       trow[part * CPP + k] = ld_lane(tk.WpT, (int64_t)(i1 + part * CPP + k) * nrow + rr);
@@ -311,42 +370,50 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
 #pragma unroll
     for (int v = 0; v < NV; ++v) t[v] = st[StripeLayout<RS>::row(v, l)][StripeLayout<RS>::col(v, l)];
     if (i1 > 0) {
+      // E and U of eight columns per group, two groups in flight (static
+      // buffers a / b, no copies); per column, the MFMA for the next column is
+      // issued before the subtractions that consume the current one, fenced
+      // by scheduling barriers so the two products stay in separate registers
+      // and each MFMA runs under the VALU work of the column before it
       float ea[G], ua[G], eb[G], ub[G];
+      const float* const Eg = tk.E + rr;     // column jj at + jj * nrow
+      const float* const Ug = tk.U + i1 + l; // column jj at + jj * n
       auto load = [&](int g, float (&e)[G], float (&u)[G]) {
+        const float* ep = Eg + (int64_t)g * G * nrow;
+        const float* up = Ug + (int64_t)g * G * n;
 #pragma unroll
         for (int q = 0; q < G; ++q) {
-          const int64_t jj = (int64_t)g * G + q;
-          e[q] = ld_lane(tk.E, jj * nrow + rr);
-          u[q] = ld_lane(tk.U, jj * n + i1 + l);
+          e[q] = ld_lane(ep, (int64_t)q * nrow);
+          u[q] = ld_lane(up, (int64_t)q * n);
         }
       };
-      const int groups = i1 / G;
-      load(0, ea, ua);
-#pragma unroll
-      for (int q = 0; q < G; ++q) eb[q] = ub[q] = 0.0f;
-      fv P0 = mfma(ea[0], ua[0]), P1;
-      for (int g = 0; g < groups; ++g) {
-        if (g + 1 < groups) load(g + 1, eb, ub);
+      fv P0, P1;
+      auto group = [&](const float (&e)[G], const float (&u)[G], const float (&en)[G],
+                       const float (&un)[G]) {
 #pragma unroll
         for (int q = 0; q < G; q += 2) {
-          // P0 holds column g*G + q, P1 column g*G + q + 1; the last group's
-          // final products are unused
-          P1 = mfma(ea[q + 1], ua[q + 1]);
+          // P0 holds column q of the group on entry; the last group's final
+          // product is unused
+          P1 = mfma(e[q + 1], u[q + 1]);
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int v = 0; v < NV; ++v) t[v] = t[v] - P0[v];
-          P0 = mfma(q + 2 < G ? ea[q + 2] : eb[0], q + 2 < G ? ua[q + 2] : ub[0]);
+          __builtin_amdgcn_sched_barrier(0);
+          P0 = mfma(q + 2 < G ? e[q + 2] : en[0], q + 2 < G ? u[q + 2] : un[0]);
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int v = 0; v < NV; ++v) t[v] = t[v] - P1[v];
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
+          __builtin_amdgcn_sched_barrier(0);
         }
-#pragma unroll
-        for (int q = 0; q < G; ++q) {
-          ea[q] = eb[q];
-          ua[q] = ub[q];
-        }
+      };
+      const int groups = i1 / G;  // even: i1 is a multiple of 64
+      load(0, ea, ua);
+      P0 = mfma(ea[0], ua[0]);
+      for (int g = 0; g < groups; g += 2) {
+        load(g + 1, eb, ub);
+        group(ea, ua, eb, ub);
+        load(g + 2 < groups ? g + 2 : g + 1, ea, ua);  // past the end: a valid group, unused
+        group(eb, ub, ea, ua);
       }
     }
     __syncthreads();
@@ -357,19 +424,39 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
 #pragma unroll
     for (int k = 0; k < B; ++k) ts[k] = trow[k];
     __syncthreads();
-    // diagonal tile: lane l fills column l of the aligned rows, 16 loads in flight
+    // the block's grid steps / offsets (both halves into registers) and the
+    // compact diagonal tile share one round trip to memory; lane l fills entry
+    // l of the aligned tile rows (rows of piece p keep 64 - 16 p entries)
+    GridHalf<RS> g0, g1;
+    load_grid<RS>(tk, sbo, 0, l, rr, g0);
+    load_grid<RS>(tk, sbo, 32, l, rr, g1);
 #pragma unroll
-    for (int a0 = 0; a0 < B; a0 += 16) {
+    for (int p = 0; p < 4; ++p) {
       float u[16];
 #pragma unroll
-      for (int a = 0; a < 16; ++a)
-        u[a] = a0 + a + l < B ? ld_lane(tk.U, (int64_t)(i1 + a0 + a) * n + i1 + a0 + a + l) : 0.0f;
+      for (int a = 0; a < 16; ++a) {
+        const int row = 16 * p + a;
+        u[a] = l < 64 - 16 * p && row + l < B
+                   ? ld_lane(tk.U, (int64_t)(i1 + row) * n + i1 + row + l) : 0.0f;
+      }
+      if (l < 64 - 16 * p) {
 #pragma unroll
-      for (int a = 0; a < 16; ++a) su[a0 + a][l] = u[a];
+        for (int a = 0; a < 16; ++a) lds[tile_base(p) + a * (64 - 16 * p) + l] = u[a];
+      }
     }
-    sbo[l] = tk.sbidx[i1 + l] * nrow;
+    store_grid<RS>(g0, l, sg, sm);
     __syncthreads();
-    if (l < RS) sweep_block_rl<B>(tk, i1, r, rr, valid, ts, su, sbo);
+    if (l < RS) {
+      sweep_cols<64, B, RS>(tk, i1, r, rl, valid, ts, lds, sg, sm, 0, 0);
+      sweep_cols<48, B, RS>(tk, i1, r, rl, valid, ts, lds, sg, sm, 16, 0);
+    }
+    __syncthreads();
+    store_grid<RS>(g1, l, sg, sm);
+    __syncthreads();
+    if (l < RS) {
+      sweep_cols<32, B, RS>(tk, i1, r, rl, valid, ts, lds, sg, sm, 32, 32);
+      sweep_cols<16, B, RS>(tk, i1, r, rl, valid, ts, lds, sg, sm, 48, 32);
+    }
     __syncthreads();
   }
 }
