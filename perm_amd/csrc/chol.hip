@@ -71,7 +71,29 @@ struct GemmArgs {
   int64_t sA1, sB1, sC1, sA2, sB2, sC2;
   int nz2;
   int tri;
+  int ntx, nty, nzt;  // column tiles, row tiles, batch entries (set by dgemm())
 };
+
+// Block -> tile: items run matrix by matrix, then by groups of 8 row tiles,
+// column by column, row by row within a group. The hardware places block w on
+// XCD w % 8, so item = (w % 8) * per + w / 8 gives every XCD a contiguous run
+// of items, and the ~64 blocks resident on an XCD share 8 row tiles of A and
+// 8 column tiles of B through its L2 instead of each fetching its own.
+__device__ __forceinline__ bool gemm_tile(const GemmArgs& g, int& bx, int& by, int& bz) {
+  const int total = g.ntx * g.nty * g.nzt;
+  const int per = (total + 7) / 8;
+  const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (t >= total) return false;
+  const int T = g.ntx * g.nty;
+  bz = t / T;
+  const int r = t - bz * T;
+  const int rg = r / (8 * g.ntx);
+  const int gy = min(8, g.nty - rg * 8);
+  const int rem = r - rg * 8 * g.ntx;
+  bx = rem / gy;
+  by = rg * 8 + rem % gy;
+  return true;
+}
 
 constexpr int GBK = 16;       // K tile
 constexpr int GLD = GBK + 2;  // LDS row of a [rows][K] tile: 144 B, fragment reads conflict-free
@@ -100,11 +122,13 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
   constexpr int BLD = BT ? GLD : GNLD;
   __shared__ __align__(16) double As[2][BM][GLD];
   __shared__ __align__(16) double Bs[2][BROWS][BLD];
-  const int z1 = blockIdx.z / g.nz2, z2 = blockIdx.z % g.nz2;
+  int bx, by, bz;
+  if (!gemm_tile(g, bx, by, bz)) return;
+  const int z1 = bz / g.nz2, z2 = bz % g.nz2;
   const double* A = g.A + z1 * g.sA1 + z2 * g.sA2;
   const double* B = g.B + z1 * g.sB1 + z2 * g.sB2;
   double* C = g.C + z1 * g.sC1 + z2 * g.sC2;
-  const int bm = blockIdx.y * BM, bn = blockIdx.x * 64;
+  const int bm = by * BM, bn = bx * 64;
   if ((g.tri & 4) && bn >= bm + BM) return;
   const int t = threadIdx.x, l = t & 63, wm = (t >> 6) * (BM / 4);
   const int lr = l & 15, lg = l >> 4;
@@ -233,14 +257,14 @@ static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
   // 128-row tiles when they still give two blocks per CU, 64-row ones otherwise
   const bool big = (int64_t)nt * ((a0.M + 127) / 128) * nz1 * a0.nz2 >= 512;
   const int bm = big ? 128 : 64;
-  const int chunk = 65535 / a0.nz2;  // grid.z limit
-  for (int z0 = 0; z0 < nz1; z0 += chunk) {
-    GemmArgs a = a0;
-    a.A += z0 * a0.sA1;
-    a.B += z0 * a0.sB1;
-    a.C += z0 * a0.sC1;
-    const int nz = (nz1 - z0 < chunk ? nz1 - z0 : chunk) * a0.nz2;
-    const dim3 grid(nt, (a.M + bm - 1) / bm, nz);
+  GemmArgs a = a0;
+  a.ntx = nt;
+  a.nty = (a.M + bm - 1) / bm;
+  a.nzt = nz1 * a0.nz2;
+  const int64_t total = (int64_t)a.ntx * a.nty * a.nzt;
+  if (total > (int64_t)1 << 30) return set_error(CP_ERR_SHAPE, "fp64 GEMM grid too large");
+  const dim3 grid((unsigned)(8 * ((total + 7) / 8)));
+  {
     if (bt)
       big ? launch_gemm<true, 128>(a, grid, vec, st) : launch_gemm<true, 64>(a, grid, vec, st);
     else
