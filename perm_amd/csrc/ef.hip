@@ -124,35 +124,23 @@ __device__ __forceinline__ void sweep_block(const SweepTask& tk, int i1, int r, 
   }
 }
 
-// In-block sweep with the lane's row of the block in registers (lane = row),
-// right-looking: ts[k] holds the target of column cb + k, so the column being
-// quantized is always ts[0], and subtracting e_cb * U[cb][cb + k] from ts[k]
-// moves it to ts[k - 1] in the same step. Each element still receives its
-// updates one at a time in ascending column order (ef.py:199-213).
-//
-// The block's diagonal U tile is read aligned at the diagonal, row cb giving
-// U[i1 + cb][i1 + cb + k]. A row is read only by the 16-column piece it falls
-// in, up to that piece's KMAX = 64 - 16 * piece entries, so the tile is kept
-// compact: row a holds KMAX(a) floats from tile_ofs(a) (10 KB instead of 16),
-// entries past the block zero. sg[k][rl] / sm[k][rl] hold the committed grid
-// step and offset of column k of the current half block for the stripe's row
-// rl, staged in LDS so no global load sits on the column-to-column chain. A
-// zero step quantizes to code 0 with e = 0; the divisions run on a safe
-// divisor and are selected away, so the column has no branches.
-constexpr int EF_Q = 2;
+// The block's diagonal U tile is kept compact in LDS: a tile row is read only
+// by the columns of its 16-column piece onwards, so row cb (piece p = cb / 16)
+// holds block columns 16 p .. 63 from tile_base(p) + (cb % 16) * (64 - 16 p):
+// 10 KB instead of 16. sg[k][rl] / sm[k][rl] hold the committed grid step and
+// offset of column k of the current half block for the stripe's row rl,
+// staged in LDS so no global load sits on the column-to-column chain.
 constexpr int TILE_FLOATS = 16 * (64 + 48 + 32 + 16);
 
 __device__ __forceinline__ constexpr int tile_base(int piece) {
   return piece == 0 ? 0 : piece == 1 ? 16 * 64 : piece == 2 ? 16 * (64 + 48) : 16 * (64 + 48 + 32);
 }
-__device__ __forceinline__ int tile_ofs(int a) {
-  const int piece = a >> 4;
-  return tile_base(piece) + (a & 15) * (64 - 16 * piece);
-}
 
 // Quantization of one column for one row (ef.py:199-208): code q on the
 // committed grid (step dl, offset ml; a zero step gives code 0 and e = 0) and
 // the scaled error e = (t - recon) / U[j][j], in the reference's float32 order.
+// The divisions run on a safe divisor and are selected away, so there is no
+// branch.
 __device__ __forceinline__ void quantize_col(const SweepTask& tk, float t, float dl, float ml,
                                              float diag, float& e, int& q) {
   const bool nz = dl != 0.0f;
@@ -163,58 +151,79 @@ __device__ __forceinline__ void quantize_col(const SweepTask& tk, float t, float
   e = nz ? ev : 0.0f;
 }
 
-// Columns cb0 .. cb0 + 15 of the block (KMAX = B - cb0); the grid arrays hold
-// the half block starting at column hb. Software-pipelined: as soon as column
-// cb's error is known, column cb + 1's final target ts[1] - e * U[cb][cb + 1]
-// is formed and its quantization (two divisions, a serial chain) is issued in
-// the same scheduling region as column cb's remaining updates, which fill the
-// chain's latency. The first column of the piece is quantized up front.
-template <int KMAX, int B, int RS>
-__device__ __forceinline__ void sweep_cols(const SweepTask& tk, int i1, int r, int rl, bool valid,
-                                           float (&ts)[B], const float* tile,
-                                           const float (*sg)[RS], const float (*sm)[RS], int cb0,
-                                           int hb) {
+// In-block sweep with each row split over the wave: RS rows, 64 / RS lanes per
+// row, lane l holding elements RS * (l / RS) .. + RS - 1 of row l % RS of the
+// block (all 64 lanes work, where the one-lane-per-row queue above keeps
+// 64 - RS of them idle). Column cb's target lives in the lanes of group
+// cb / RS; it is broadcast to the row's other lanes with v_permlane16/32_swap,
+// every lane quantizes it (the same value, the same code and error), and every
+// lane applies the column's update to its own RS elements. Elements already
+// quantized receive updates too and are never read again; past the last
+// group's column only its remaining elements are updated. Each element still
+// receives its updates one at a time in ascending column order (ef.py:199-213).
+template <int RS>
+__device__ __forceinline__ float bcast_group(float x, int own) {
+  const unsigned v = __float_as_uint(x);
+  if constexpr (RS == 32) {
+    const auto s = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return __uint_as_float(own == 0 ? s[0] : s[1]);
+  } else {
+    const auto h = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    const unsigned y = (own & 1) ? h[1] : h[0];
+    const auto s = __builtin_amdgcn_permlane32_swap(y, y, false, false);
+    return __uint_as_float(own < 2 ? s[0] : s[1]);
+  }
+}
+
+// Columns hb .. hb + 31 (one half block; sg / sm hold its grid). tile is the
+// compact diagonal tile; row cb holds columns 16 * (cb / 16) .. 63.
+template <int RS>
+__device__ __forceinline__ void sweep_half_split(const SweepTask& tk, int i1, int rr, int rl, int g,
+                                                 float (&tl)[RS], const float* tile,
+                                                 const float (*sg)[RS], const float (*sm)[RS],
+                                                 int hb) {
   const int nrow = tk.nrow;
-  constexpr int piece = (B - KMAX) / 16;
-  const float* prow = tile + tile_base(piece);  // row cb0 + a at prow + a * KMAX
-  float e, t0 = ts[0];
-  int q;
-  quantize_col(tk, t0, sg[cb0 - hb][rl], sm[cb0 - hb][rl], prow[0], e, q);
-#pragma unroll 1
-  for (int h = 0; h < 16; h += EF_Q) {
+  // Running output pointers (row rr, column i1 + hb + a), opaque to the
+  // compiler so the unrolled columns do not each keep a precomputed address.
+  // Every lane stores: the lanes of a row hold the same values, and a lane past
+  // the last row (rr = nrow - 1) computed exactly that row's values from that
+  // row's data, so duplicate stores write identical bytes; a branch around the
+  // stores would split the unrolled columns into blocks the per-column
+  // scheduling fences cannot hold together.
+  const int64_t o0 = (int64_t)(i1 + hb) * nrow + rr;
+  float* pe = tk.E + o0;
+  float* pw = tk.WcurT + o0;
+  uint8_t* pl = tk.LT + o0;
 #pragma unroll
-    for (int j = 0; j < EF_Q; ++j) {
-      const int a = h + j, cb = cb0 + a, c = i1 + cb;
-      const float4* urow = reinterpret_cast<const float4*>(prow + a * KMAX);
-      const float4 u0 = urow[0];
-      // next column of this piece (the last column quantizes itself again,
-      // discarded: the next piece starts with its own first column)
-      const int an = a + 1 < 16 ? a + 1 : a;
-      const float tn = ts[1] - e * u0.y;
-      float en;
-      int qn;
-      quantize_col(tk, tn, sg[cb0 + an - hb][rl], sm[cb0 + an - hb][rl], prow[an * KMAX], en, qn);
-      if (valid) {
-        ((GlobFw)tk.E)[(int64_t)c * nrow + r] = e;
-        ((GlobFw)tk.WcurT)[(int64_t)c * nrow + r] = t0;
-        ((GlobBw)tk.LT)[(int64_t)c * nrow + r] = (uint8_t)(q - tk.lo);
-      }
-      ts[0] = tn;
-      ts[1] = ts[2] - e * u0.z;
-      ts[2] = ts[3] - e * u0.w;
+  for (int a = 0; a < 32; ++a) {
+    const int cb = hb + a;
+    const int own = cb / RS, i = cb % RS, p = cb / 16;
+    // row cb of the tile, indexed by block column (entries below 16 p are not
+    // stored; only lanes whose elements are finished read them)
+    const float* row = tile + tile_base(p) + (cb % 16) * (64 - 16 * p) - 16 * p;
+    const float tb = bcast_group<RS>(tl[i], own);
+    float e;
+    int q;
+    quantize_col(tk, tb, sg[a][rl], sm[a][rl], row[cb], e, q);
+    *(GlobFw)pe = e;
+    *(GlobFw)pw = tb;
+    *(GlobBw)pl = (uint8_t)(q - tk.lo);
+    pe += nrow;
+    pw += nrow;
+    pl += nrow;
+    asm volatile("" : "+v"(pe), "+v"(pw), "+v"(pl));
+    const int jlo = own == 64 / RS - 1 ? (i + 1) & ~3 : 0;
+    const float4* ul = reinterpret_cast<const float4*>(row + RS * g);
 #pragma unroll
-      for (int k4 = 1; k4 < KMAX / 4; ++k4) {
-        const float4 u = urow[k4];
-        ts[4 * k4 - 1] = ts[4 * k4] - e * u.x;
-        ts[4 * k4] = ts[4 * k4 + 1] - e * u.y;
-        ts[4 * k4 + 1] = ts[4 * k4 + 2] - e * u.z;
-        ts[4 * k4 + 2] = ts[4 * k4 + 3] - e * u.w;
-      }
-      e = en;
-      q = qn;
-      t0 = tn;
-      __builtin_amdgcn_sched_barrier(0);  // one column's tile row in registers at a time
+    for (int j4 = 0; j4 < RS / 4; ++j4) {
+      if (4 * j4 < jlo) continue;  // constant once the column loop is unrolled
+      const float4 u = ul[j4];
+      tl[4 * j4] = tl[4 * j4] - e * u.x;
+      tl[4 * j4 + 1] = tl[4 * j4 + 1] - e * u.y;
+      tl[4 * j4 + 2] = tl[4 * j4 + 2] - e * u.z;
+      tl[4 * j4 + 3] = tl[4 * j4 + 3] - e * u.w;
     }
+    __builtin_amdgcn_sched_barrier(0);  // one column's tile row in registers at a time
   }
 }
 
@@ -339,16 +348,20 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
   if (row0 >= tk.nrow) return;
   const int l = threadIdx.x, rl = l % RS, part = l / RS;
   const int nrow = tk.nrow, n = tk.n;
-  const int r = row0 + rl;
-  const bool valid = r < nrow;
-  const int rr = valid ? r : nrow - 1;
+  // lanes past the last row work on the last row (and store its values again)
+  const int rr = row0 + rl < nrow ? row0 + rl : nrow - 1;
   // one LDS buffer: the RS x 64 target transpose, then the compact diagonal
-  // U tile; the grid steps / offsets of half a block; about 18 KB in all, so
-  // every SIMD keeps two of these one-wave workgroups
+  // U tile; the grid steps / offsets of half a block. About 18 KB in all for
+  // either stripe height (the grid arrays are sized for 32 rows), so a CU
+  // holds at most eight of these one-wave workgroups: the dispatcher fills
+  // CUs up to what fits, and a ninth or tenth wave on some CUs would leave
+  // others idle while the busy ones set the kernel's time.
   static_assert(RS * (B + 1) <= TILE_FLOATS, "target transpose fits the tile buffer");
   __shared__ __align__(16) float lds[TILE_FLOATS];
   __shared__ int sbo[B];
-  __shared__ float sg[32][RS], sm[32][RS];
+  __shared__ float sg_[32][32], sm_[32][32];
+  float (*sg)[RS] = reinterpret_cast<float (*)[RS]>(&sg_[0][0]);
+  float (*sm)[RS] = reinterpret_cast<float (*)[RS]>(&sm_[0][0]);
   float (*st)[B + 1] = reinterpret_cast<float (*)[B + 1]>(lds);
   float* trow = st[rl];
   auto mfma = [](float a, float b) -> fv {
@@ -420,43 +433,36 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
 #pragma unroll
     for (int v = 0; v < NV; ++v) st[StripeLayout<RS>::row(v, l)][StripeLayout<RS>::col(v, l)] = t[v];
     __syncthreads();
-    float ts[B];
+    // lane l: elements RS * (l / RS) .. + RS - 1 of row l % RS
+    float tl[RS];
 #pragma unroll
-    for (int k = 0; k < B; ++k) ts[k] = trow[k];
+    for (int k = 0; k < RS; ++k) tl[k] = trow[part * RS + k];
     __syncthreads();
     // the block's grid steps / offsets (both halves into registers) and the
-    // compact diagonal tile share one round trip to memory; lane l fills entry
-    // l of the aligned tile rows (rows of piece p keep 64 - 16 p entries)
+    // compact diagonal tile share one round trip to memory; lane l fills
+    // column 16 p + l of the tile rows of piece p
     GridHalf<RS> g0, g1;
     load_grid<RS>(tk, sbo, 0, l, rr, g0);
     load_grid<RS>(tk, sbo, 32, l, rr, g1);
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       float u[16];
+      const bool in = l < 64 - 16 * p;
 #pragma unroll
-      for (int a = 0; a < 16; ++a) {
-        const int row = 16 * p + a;
-        u[a] = l < 64 - 16 * p && row + l < B
-                   ? ld_lane(tk.U, (int64_t)(i1 + row) * n + i1 + row + l) : 0.0f;
-      }
-      if (l < 64 - 16 * p) {
+      for (int a = 0; a < 16; ++a)
+        u[a] = in ? ld_lane(tk.U, (int64_t)(i1 + 16 * p + a) * n + i1 + 16 * p + l) : 0.0f;
+      if (in) {
 #pragma unroll
         for (int a = 0; a < 16; ++a) lds[tile_base(p) + a * (64 - 16 * p) + l] = u[a];
       }
     }
     store_grid<RS>(g0, l, sg, sm);
     __syncthreads();
-    if (l < RS) {
-      sweep_cols<64, B, RS>(tk, i1, r, rl, valid, ts, lds, sg, sm, 0, 0);
-      sweep_cols<48, B, RS>(tk, i1, r, rl, valid, ts, lds, sg, sm, 16, 0);
-    }
+    sweep_half_split<RS>(tk, i1, rr, rl, part, tl, lds, sg, sm, 0);
     __syncthreads();
     store_grid<RS>(g1, l, sg, sm);
     __syncthreads();
-    if (l < RS) {
-      sweep_cols<32, B, RS>(tk, i1, r, rl, valid, ts, lds, sg, sm, 32, 32);
-      sweep_cols<16, B, RS>(tk, i1, r, rl, valid, ts, lds, sg, sm, 48, 32);
-    }
+    sweep_half_split<RS>(tk, i1, rr, rl, part, tl, lds, sg, sm, 32);
     __syncthreads();
   }
 }
