@@ -12,7 +12,8 @@
  *    factorization's positive-definiteness check) synchronize that stream.
  *  - Return 0 (CP_OK) or a negative cp_status. cp_last_error() gives a
  *    thread-local message for the last failure on the calling thread.
- *  - Type codes are ggml's: Q2_K = 10, Q3_K = 11, Q4_K = 12, Q6_K = 14.
+ *  - Type codes are ggml's: Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13,
+ *    Q6_K = 14.
  */
 #ifndef COLDPRESS_HIP_H
 #define COLDPRESS_HIP_H
@@ -35,25 +36,28 @@ enum cp_status {
   CP_ERR_WORKSPACE = -7  /* workspace too small                                  */
 };
 
-enum cp_ttype { CP_Q2_K = 10, CP_Q3_K = 11, CP_Q4_K = 12, CP_Q6_K = 14 };
+enum cp_ttype { CP_Q8_0 = 8, CP_Q2_K = 10, CP_Q3_K = 11, CP_Q4_K = 12, CP_Q5_K = 13, CP_Q6_K = 14 };
 
 /* Message for the last failure on this thread ("" if none). */
 const char* cp_last_error(void);
 
-/* Bytes per 256-weight superblock of a container type, or a negative status. */
+/* Bytes per block of a container type (a 256-weight superblock for the k-quants,
+ * a 32-weight block for Q8_0), or a negative status. */
 int cp_kq_block_bytes(int ttype);
 
-/* k-quant encode of x [nrow, n] (n % 256 == 0) into out [nrow, n/256*block_bytes].
- * qw [n] is the importance vector (imatrix means) or NULL for the unweighted path.
- * Replaces kquant.QUANTIZE[tt](x, qw) -- coldpress/kquant.py:732 (encoders
- * quantize_q2_K :347, quantize_q3_K :432, quantize_q4_K :588, quantize_q6_K :632).
- * Bit-exact with the reference encoder. */
+/* Container encode of x [nrow, n] into out [nrow, n/block_weights*block_bytes]
+ * (n % 256 == 0 for the k-quants, n % 32 == 0 for Q8_0). qw [n] is the importance
+ * vector (imatrix means) or NULL for the unweighted path; Q8_0 ignores it, as the
+ * reference does. Replaces kquant.QUANTIZE[tt](x, qw) -- coldpress/kquant.py:732
+ * (encoders quantize_q2_K :347, quantize_q3_K :432, quantize_q4_K :588,
+ * quantize_q5_K :592, quantize_q6_K :632, quantize_q8_0 :706). Bit-exact with the
+ * reference encoder. */
 int cp_kq_quantize(int ttype, const float* x, int64_t nrow, int64_t n, const float* qw,
                    uint8_t* out, void* stream);
 
-/* k-quant decode of raw [nrow, n/256*block_bytes] into y [nrow, n] float32.
- * Replaces kquant.DEQUANTIZE[tt](raw, n) -- coldpress/kquant.py:734 (decoders
- * :416, :489, :596, :681). Bit-exact. */
+/* Container decode of raw [nrow, n/block_weights*block_bytes] into y [nrow, n]
+ * float32. Replaces kquant.DEQUANTIZE[tt](raw, n) -- coldpress/kquant.py:734
+ * (decoders :416, :489, :596, :610, :681, :721). Bit-exact. */
 int cp_kq_dequantize(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, float* y,
                      void* stream);
 
@@ -103,7 +107,7 @@ enum cp_ef_mode {
 };
 
 typedef struct cp_ef_tensor {
-  int ttype;             /* CP_Q2_K, CP_Q3_K, CP_Q4_K or CP_Q6_K                       */
+  int ttype;             /* CP_Q2_K, CP_Q3_K, CP_Q4_K, CP_Q5_K or CP_Q6_K              */
   int64_t nrow, n;       /* weight shape, n % 256 == 0                                  */
   const float* x;        /* [nrow, n] weights                                           */
   const float* qw;       /* [n] importance (imatrix means) or NULL                      */

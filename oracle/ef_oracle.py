@@ -112,11 +112,7 @@ def write_codes(tt, raw, codes, nrow, n):
     elif tt == "Q4_K":
         b[:, 16:144] = kq.pack_nibbles(L)
     elif tt == "Q5_K":
-        high = (L > 15).astype(np.uint8).reshape(-1, 4, 2, 32)
-        sh = (2 * np.arange(4, dtype=np.uint8))[None, :, None]
-        b[:, 16:48] = np.bitwise_or.reduce((high[:, :, 0] << sh) | (high[:, :, 1] << (sh + 1)),
-                                           axis=1)
-        b[:, 48:176] = kq.pack_nibbles(np.where(L > 15, L - 16, L))
+        b[:, 16:48], b[:, 48:176] = kq.pack_q5_codes(L)
     elif tt == "Q6_K":
         b[:, 0:128], b[:, 128:192] = kq.pack_q6_codes(L + 32)
     else:

@@ -353,6 +353,42 @@ def unpack_q6_codes(ql, qh):
     return (low.astype(np.int32) | high.astype(np.int32) << 4).reshape(-1, 256)
 
 
+def pack_q5_codes(L):
+    """Codes 0..31 -> (qh [NB,32], qs [NB,128]): bit 2c of qh[l] is the high bit of
+    element 64c + l, bit 2c+1 that of element 64c + 32 + l; the low four bits go
+    through pack_nibbles (kquant.py:572-583)."""
+    L = L.astype(np.int32)
+    high = (L > 15).astype(np.uint8).reshape(-1, 4, 2, 32)
+    sh = (2 * np.arange(4, dtype=np.uint8))[None, :, None]
+    qh = np.bitwise_or.reduce((high[:, :, 0] << sh) | (high[:, :, 1] << (sh + 1)), axis=1)
+    return qh, pack_nibbles(np.where(L > 15, L - 16, L))
+
+
+def unpack_q5_codes(qh, qs):
+    """-> codes 0..31 int32."""
+    h = qh.reshape(-1, 1, 32)
+    sh = (2 * np.arange(4))[None, :, None]
+    hb = np.stack([(h >> sh) & 1, (h >> (sh + 1)) & 1], axis=2).reshape(-1, 256)
+    return unpack_nibbles(qs).astype(np.int32) + 16 * hb.astype(np.int32)
+
+
+def stored_codes(tt, raw):
+    """Integer codes of every superblock [NB, 256] in the sweep's signed convention
+    (Q3_K -4..3, Q6_K -32..31, the affine types 0..top)."""
+    b = raw.reshape(-1, BYTES_PER_SB[tt])
+    if tt == "Q2_K":
+        return unpack_2bit(b[:, 16:80]).astype(np.int32)
+    if tt == "Q3_K":
+        return unpack_q3_codes(b[:, 0:32], b[:, 32:96])
+    if tt == "Q4_K":
+        return unpack_nibbles(b[:, 16:144]).astype(np.int32)
+    if tt == "Q5_K":
+        return unpack_q5_codes(b[:, 16:48], b[:, 48:176])
+    if tt == "Q6_K":
+        return unpack_q6_codes(b[:, 0:128], b[:, 128:192]) - 32
+    raise ValueError(tt)
+
+
 def _half_field(b, off):
     return b[:, off:off + 2].copy().view(np.float16).astype(F32).reshape(-1)
 
@@ -521,10 +557,7 @@ def _encode_q45(x, qw, q5):
                            dmin16.view(np.uint8).reshape(NB, 2), packed], axis=1)
     if not q5:
         return np.concatenate([head, pack_nibbles(L)], axis=1).reshape(nrow, -1)
-    high = (L > 15).astype(np.uint8).reshape(NB, 4, 2, 32)
-    sh = (2 * np.arange(4, dtype=np.uint8))[None, :, None]
-    qh = np.bitwise_or.reduce((high[:, :, 0] << sh) | (high[:, :, 1] << (sh + 1)), axis=1)
-    body = pack_nibbles(np.where(L > 15, L - 16, L))
+    qh, body = pack_q5_codes(L)
     return np.concatenate([head, qh, body], axis=1).reshape(nrow, -1)
 
 
@@ -544,10 +577,7 @@ def _decode_q45(raw, n, q5):
     d, dmin = _half_field(b, 0), _half_field(b, 2)
     su, mu = unpack_scales_k4(b[:, 4:16])
     if q5:
-        qh = b[:, 16:48].reshape(-1, 1, 32)
-        sh = (2 * np.arange(4))[None, :, None]
-        hb = np.stack([(qh >> sh) & 1, (qh >> (sh + 1)) & 1], axis=2).reshape(-1, 256)
-        L = unpack_nibbles(b[:, 48:176]).astype(np.int32) + 16 * hb.astype(np.int32)
+        L = unpack_q5_codes(b[:, 16:48], b[:, 48:176])
     else:
         L = unpack_nibbles(b[:, 16:144])
     dl = d[:, None] * su.astype(F32)

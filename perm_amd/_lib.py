@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcoldpres
 CP_OK, CP_ERR_SHAPE, CP_ERR_TTYPE, CP_ERR_NOT_PD = 0, -1, -2, -3
 CP_ERR_HIP, CP_ERR_ARG, CP_ERR_ALIGN, CP_ERR_WORKSPACE = -4, -5, -6, -7
 
-TTYPE = {"Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q6_K": 14}
+TTYPE = {"Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
 
 _i64, _i32, _vp, _f64 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_double
 _sz = ctypes.c_size_t

@@ -20,18 +20,21 @@ inline int hip_fail(hipError_t e, const char* what) {
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-// Superblock geometry of the supported containers.
+// Block geometry of the supported containers.
 struct KqGeom {
-  int block_bytes;  // bytes per 256-weight superblock
-  int sub;          // sub-block width
+  int block_bytes;    // bytes per block
+  int sub;            // sub-block width (the scale granularity)
+  int block_weights;  // weights per block: 256 (k-quant superblock) or 32 (Q8_0)
 };
 
 inline bool kq_geom(int ttype, KqGeom* g) {
   switch (ttype) {
-    case CP_Q2_K: *g = {84, 16}; return true;
-    case CP_Q3_K: *g = {110, 16}; return true;
-    case CP_Q4_K: *g = {144, 32}; return true;
-    case CP_Q6_K: *g = {210, 16}; return true;
+    case CP_Q8_0: *g = {34, 32, 32}; return true;
+    case CP_Q2_K: *g = {84, 16, 256}; return true;
+    case CP_Q3_K: *g = {110, 16, 256}; return true;
+    case CP_Q4_K: *g = {144, 32, 256}; return true;
+    case CP_Q5_K: *g = {176, 32, 256}; return true;
+    case CP_Q6_K: *g = {210, 16, 256}; return true;
     default: return false;
   }
 }

@@ -672,9 +672,10 @@ __global__ void ef_grid_kernel(const EfDev* __restrict__ tab) {
     int lo = (k < 8) ? (sc[k] & 0xF) : (sc[k - 8] >> 4);
     int hi = (sc[8 + (k & 3)] >> (2 * (k >> 2))) & 3;
     dl = d * (float)((lo | hi << 4) - 32);
-  } else if (ttype == CP_Q4_K) {
+  } else if (ttype == CP_Q4_K || ttype == CP_Q5_K) {
     if (k & 1) return;  // 32-wide sub-blocks: one thread per pair of 16s
-    const uint8_t* b = raw + ((int64_t)r * (n / 256) + sb) * 144;
+    const int bp = ttype == CP_Q5_K ? 176 : 144;
+    const uint8_t* b = raw + ((int64_t)r * (n / 256) + sb) * bp;
     float d = half_value(b[0] | b[1] << 8), dm = half_value(b[2] | b[3] << 8);
     const uint8_t* sc = b + 4;
     int j = k >> 1, s, m;
@@ -713,6 +714,7 @@ __global__ void ef_repack_kernel(const EfDev* __restrict__ tab) {
     case CP_Q2_K: lo_b = 16; hi_b = 80; bp = 84; break;
     case CP_Q3_K: lo_b = 0; hi_b = 96; bp = 110; break;
     case CP_Q4_K: lo_b = 16; hi_b = 144; bp = 144; break;
+    case CP_Q5_K: lo_b = 16; hi_b = 176; bp = 176; break;
     default: lo_b = 0; hi_b = 192; bp = 210; break;
   }
   const int64_t NB = (int64_t)T.nrow * (T.n / 256);
@@ -737,6 +739,14 @@ __global__ void ef_repack_kernel(const EfDev* __restrict__ tab) {
   } else if (ttype == CP_Q4_K) {
     int k = b - 16, base = (k >> 5) * 64 + (k & 31);
     v = (c[base] & 0xF) | (c[base + 32] & 0xF) << 4;
+  } else if (ttype == CP_Q5_K) {
+    if (b < 48) {  // qh: bit q of byte j is code (32q + j) >= 16
+      v = 0;
+      for (int q = 0; q < 8; ++q) v |= (uint32_t)(c[32 * q + b - 16] >> 4) << q;
+    } else {
+      int k = b - 48, base = (k >> 5) * 64 + (k & 31);
+      v = (c[base] & 0xF) | (c[base + 32] & 0xF) << 4;
+    }
   } else {
     if (b < 128) {
       int h = b >> 6, k = b & 63;
@@ -792,6 +802,7 @@ static void grid_range(int ttype, int* lo, int* hi, int* sub) {
     case CP_Q2_K: *lo = 0; *hi = 3; *sub = 16; break;
     case CP_Q3_K: *lo = -4; *hi = 3; *sub = 16; break;
     case CP_Q4_K: *lo = 0; *hi = 15; *sub = 32; break;
+    case CP_Q5_K: *lo = 0; *hi = 31; *sub = 32; break;
     default: *lo = -32; *hi = 31; *sub = 16; break;
   }
 }
@@ -860,7 +871,8 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
   for (int i = 0; i < count; ++i) {
     const cp_ef_tensor& t = ts[i];
     KqGeom g;
-    if (!kq_geom(t.ttype, &g)) return set_error(CP_ERR_TTYPE, "tensor %d: unsupported type %d", i, t.ttype);
+    if (!kq_geom(t.ttype, &g) || g.block_weights != 256)
+      return set_error(CP_ERR_TTYPE, "tensor %d: unsupported type %d", i, t.ttype);
     if (t.nrow <= 0 || t.n <= 0 || t.n % 256 || t.nrow > 65535 * 64 || t.n > (1 << 20) ||
         (t.n / 16) * t.nrow >= ((int64_t)1 << 31))
       return set_error(CP_ERR_SHAPE, "tensor %d: bad shape [%lld, %lld]", i, (long long)t.nrow, (long long)t.n);
@@ -886,7 +898,7 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     o = L.end;
     int lo, hi, sub;
     grid_range(t.ttype, &lo, &hi, &sub);
-    const bool affine = t.ttype == CP_Q2_K || t.ttype == CP_Q4_K;
+    const bool affine = t.ttype == CP_Q2_K || t.ttype == CP_Q4_K || t.ttype == CP_Q5_K;
     float* mlT = affine ? (float*)(base + L.mlT) : nullptr;
     tasks[i] = SweepTask{(const float*)(base + L.WpT), t.U, (const float*)(base + L.dlT), mlT,
                          (const int*)(base + L.sbidx), (float*)(base + L.E),
@@ -947,6 +959,7 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
         case CP_Q2_K: launch_commit<CP_Q2_K>(dtab, g, it > 0, st); break;
         case CP_Q3_K: launch_commit<CP_Q3_K>(dtab, g, it > 0, st); break;
         case CP_Q4_K: launch_commit<CP_Q4_K>(dtab, g, it > 0, st); break;
+        case CP_Q5_K: launch_commit<CP_Q5_K>(dtab, g, it > 0, st); break;
         default: launch_commit<CP_Q6_K>(dtab, g, it > 0, st); break;
       }
     }
@@ -977,6 +990,7 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
       case CP_Q2_K: launch_decode<CP_Q2_K>(dtab, g, st); break;
       case CP_Q3_K: launch_decode<CP_Q3_K>(dtab, g, st); break;
       case CP_Q4_K: launch_decode<CP_Q4_K>(dtab, g, st); break;
+      case CP_Q5_K: launch_decode<CP_Q5_K>(dtab, g, st); break;
       default: launch_decode<CP_Q6_K>(dtab, g, st); break;
     }
   }

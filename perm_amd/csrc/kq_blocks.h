@@ -3,8 +3,8 @@
 // the many-tensor kernels of the EF driver.
 //
 // Encoder mapping: one lane per sub-block. A wave64 holds S = 64/G superblocks
-// (G = 16 lanes per superblock for the 16-wide sub-blocks, 8 for Q4_K's
-// 32-wide ones). Sub-block fits run in-lane on registers; superblock-level
+// (G = 16 lanes per superblock for the 16-wide sub-blocks, 8 for the 32-wide
+// ones of Q4_K and Q5_K). Sub-block fits run in-lane on registers; superblock-level
 // steps (maxima, super-scale fits, the 256-wide sum of squares) run across the
 // G lanes of the superblock with xor-butterfly reductions that reproduce
 // numpy's pairwise order. Codes and per-superblock fields are staged in LDS
@@ -35,6 +35,10 @@ struct Kq<CP_Q4_K> {
   static constexpr int G = 8, SUBW = 32, BP = 144;
 };
 template <>
+struct Kq<CP_Q5_K> {
+  static constexpr int G = 8, SUBW = 32, BP = 176;
+};
+template <>
 struct Kq<CP_Q6_K> {
   static constexpr int G = 16, SUBW = 16, BP = 210;
 };
@@ -42,7 +46,7 @@ struct Kq<CP_Q6_K> {
 // Per-superblock fields staged in LDS before packing.
 //  Q2_K: a[k] = scale byte (sc & 0xF) | (min & 0xF) << 4
 //  Q3_K: a[k] = 6-bit scale 0..63
-//  Q4_K: a[0..7] = 6-bit scales, a[8..15] = 6-bit mins
+//  Q4_K, Q5_K: a[0..7] = 6-bit scales, a[8..15] = 6-bit mins
 //  Q6_K: a[k] = int8 scale
 struct SbFields {
   uint8_t a[16];
@@ -115,7 +119,7 @@ __device__ __forceinline__ uint32_t pack_byte(const uint8_t* c, const SbFields& 
       return v;
     }
     return (f.d >> (8 * (b - 108))) & 0xFF;
-  } else if constexpr (TT == CP_Q4_K) {
+  } else if constexpr (TT == CP_Q4_K || TT == CP_Q5_K) {
     if (b < 2) return (f.d >> (8 * b)) & 0xFF;
     if (b < 4) return (f.dmin >> (8 * (b - 2))) & 0xFF;
     if (b < 16) {
@@ -124,7 +128,16 @@ __device__ __forceinline__ uint32_t pack_byte(const uint8_t* c, const SbFields& 
       if (m < 8) return (f.a[8 + m - 4] | (f.a[8 + m] >> 4) << 6) & 0xFF;
       return (f.a[m - 4] & 0xF) | (f.a[8 + m - 4] & 0xF) << 4;
     }
-    int k = b - 16, base = (k >> 5) * 64 + (k & 31);
+    constexpr int body = TT == CP_Q5_K ? 48 : 16;
+    if (TT == CP_Q5_K && b < body) {
+      // qh: bit 2c of byte j is code (64c + j) >= 16, bit 2c+1 is code (64c + 32 + j) >= 16
+      int j = b - 16;
+      uint32_t v = 0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v |= (uint32_t)(c[32 * q + j] >> 4) << q;
+      return v;
+    }
+    int k = b - body, base = (k >> 5) * 64 + (k & 31);
     return (c[base] & 0xF) | (c[base + 32] & 0xF) << 4;
   } else {  // Q6_K
     if (b < 128) {
@@ -263,13 +276,19 @@ __device__ __forceinline__ void kq_encode_block(const float* __restrict__ x,
     }
     F.a[g] = (uint8_t)Ls;
     if (g == 0) F.d = d16;
-  } else if constexpr (TT == CP_Q4_K) {
+  } else if constexpr (TT == CP_Q4_K || TT == CP_Q5_K) {
+    // Q5_K is Q4_K with 32 levels and its own reference-path search (kquant.py:508-593)
+    constexpr int TOP = TT == CP_Q5_K ? 31 : 15;
     float scale, mn, d, dmin;
     int Ls, Lm;
     if constexpr (IMAT) {
-      fit_affine<32>(xv, wt, 15, -0.9f, 0.05f, 36, false, true, &scale, &mn, L);
+      fit_affine<32>(xv, wt, TOP, -0.9f, 0.05f, 36, false, true, &scale, &mn, L);
       float sw = psum<32>(wt);
       gfit_nonneg_pair<8>(scale, mn, sw, 63, g, &d, &Ls, &dmin, &Lm);
+      if constexpr (TT == CP_Q5_K) {
+        Ls = Ls < 63 ? Ls : 63;
+        Lm = Lm < 63 ? Lm : 63;
+      }
     } else {
       float sq[32];
 #pragma unroll
@@ -277,7 +296,10 @@ __device__ __forceinline__ void kq_encode_block(const float* __restrict__ x,
       float av = sqrtf(psum<32>(sq) / 32.0f);
 #pragma unroll
       for (int i = 0; i < 32; ++i) wt[i] = av + fabsf(xv[i]);
-      fit_affine<32>(xv, wt, 15, -1.0f, 0.1f, 20, false, false, &scale, &mn, L);
+      if constexpr (TT == CP_Q5_K)
+        fit_affine<32>(xv, wt, TOP, -0.5f, 0.1f, 15, false, false, &scale, &mn, L);
+      else
+        fit_affine<32>(xv, wt, TOP, -1.0f, 0.1f, 20, false, false, &scale, &mn, L);
       float smax = gmax<8>(scale), mmax = gmax<8>(mn);
       float is = smax > 0.0f ? 63.0f / smax : 0.0f;
       float im = mmax > 0.0f ? 63.0f / mmax : 0.0f;
@@ -293,7 +315,7 @@ __device__ __forceinline__ void kq_encode_block(const float* __restrict__ x,
     float dl = half_value(d16) * (float)Ls, ml = half_value(m16) * (float)Lm;
     if (dl != 0.0f) {
 #pragma unroll
-      for (int i = 0; i < 32; ++i) L[i] = clampi(rint_magic((xv[i] + ml) / dl), 0, 15);
+      for (int i = 0; i < 32; ++i) L[i] = clampi(rint_magic((xv[i] + ml) / dl), 0, TOP);
     }
     F.a[g] = (uint8_t)Ls;
     F.a[8 + g] = (uint8_t)Lm;
@@ -364,7 +386,7 @@ __device__ __forceinline__ void kq_encode_block(const float* __restrict__ x,
 // ---------------------------------------------------------------- decoders
 // One thread per 16 consecutive weights of a superblock (16 threads per
 // superblock); y = (d*sc)*q - (dmin*m) in float32 (kquant.py:416-427, :489-503,
-// :596-607, :681-701).
+// :596-627, :681-701).
 // Decode 16 weights of one superblock: global thread t covers superblock t / 16.
 template <int TT>
 __device__ __forceinline__ void kq_decode_thread(const uint8_t* __restrict__ raw, int64_t NB,
@@ -397,7 +419,8 @@ __device__ __forceinline__ void kq_decode_thread(const uint8_t* __restrict__ raw
       int hb = (b[e & 31] >> (e >> 5)) & 1;
       out[i] = dl * (float)(q - (hb ? 0 : 4));
     }
-  } else if constexpr (TT == CP_Q4_K) {
+  } else if constexpr (TT == CP_Q4_K || TT == CP_Q5_K) {
+    constexpr int body = TT == CP_Q5_K ? 48 : 16;
     float d = half_value(b[0] | b[1] << 8), dm = half_value(b[2] | b[3] << 8);
     const uint8_t* sc = b + 4;
     int j = k >> 1, s, m;
@@ -412,7 +435,8 @@ __device__ __forceinline__ void kq_decode_thread(const uint8_t* __restrict__ raw
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       int e = 16 * k + i, c = e >> 6, r = e & 63;
-      int q = (r < 32) ? (b[16 + c * 32 + r] & 0xF) : (b[16 + c * 32 + r - 32] >> 4);
+      int q = (r < 32) ? (b[body + c * 32 + r] & 0xF) : (b[body + c * 32 + r - 32] >> 4);
+      if constexpr (TT == CP_Q5_K) q |= ((b[16 + (r & 31)] >> (2 * c + (r >> 5))) & 1) << 4;
       out[i] = dl * (float)q - ml;
     }
   } else {  // Q6_K

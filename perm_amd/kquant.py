@@ -1,30 +1,40 @@
-"""GGUF k-quant codec on the GPU, with the API of coldpress/kquant.py.
+"""GGUF container codec (k-quants and Q8_0) on the GPU, with the API of
+coldpress/kquant.py.
 
 ``QUANTIZE[tt](x, qw)`` and ``DEQUANTIZE[tt](raw, n)`` keep the reference's
 signatures and results (coldpress/kquant.py:732-741): bit-identical container
 bytes and reconstructions. Inputs may be numpy arrays (results come back as
 numpy) or torch tensors (results stay on the device).
 
-x: [nrow, n] float32, n % 256 == 0; qw: [n] float32 importance (imatrix means)
-or None. The same qw applies to every row.
+x: [nrow, n] float32, n % 256 == 0 (n % 32 == 0 for Q8_0); qw: [n] float32
+importance (imatrix means) or None, ignored by Q8_0. The same qw applies to
+every row.
 """
 import torch
 
 from . import _lib
 
 QK_K = 256
-BYTES_PER_SB = {"Q2_K": 84, "Q3_K": 110, "Q4_K": 144, "Q6_K": 210}
-SUB_W = {"Q2_K": 16, "Q3_K": 16, "Q4_K": 32, "Q6_K": 16}
+# k-quant superblocks: 256 weights each
+BYTES_PER_SB = {"Q2_K": 84, "Q3_K": 110, "Q4_K": 144, "Q5_K": 176, "Q6_K": 210}
+SUB_W = {"Q2_K": 16, "Q3_K": 16, "Q4_K": 32, "Q5_K": 32, "Q6_K": 16}
+# every container: (weights, bytes) per block
+BLOCK = {**{tt: (QK_K, b) for tt, b in BYTES_PER_SB.items()}, "Q8_0": (32, 34)}
+
+
+def row_bytes(ttype, n):
+    """Container bytes of one row of n weights."""
+    w, b = BLOCK[ttype]
+    return (n // w) * b
 
 
 def quantize_dev(ttype, x, qw=None, out=None):
     """Device-side encode: x, qw (or None) contiguous float32 CUDA tensors; returns
-    (or fills) a uint8 CUDA tensor [nrow, n/256*bytes]."""
+    (or fills) a uint8 CUDA tensor [nrow, row_bytes(ttype, n)]."""
     lib = _lib.load()
     nrow, n = x.shape
     if out is None:
-        out = torch.empty((nrow, (n // QK_K) * BYTES_PER_SB[ttype]), dtype=torch.uint8,
-                          device=x.device)
+        out = torch.empty((nrow, row_bytes(ttype, n)), dtype=torch.uint8, device=x.device)
     st = lib.cp_kq_quantize(_lib.TTYPE[ttype], _lib.ptr(x), nrow, n, _lib.ptr(qw),
                             _lib.ptr(out), _lib.stream_ptr())
     _lib.check(st, AssertionError if ttype == "Q2_K" else ValueError)
@@ -48,7 +58,7 @@ def _quantizer(ttype):
         if xd.dim() != 2:
             raise ValueError("x must be [nrow, n_per_row]")
         qd = None
-        if qw is not None:
+        if qw is not None and ttype != "Q8_0":  # Q8_0 has no weighted path (kquant.py:706)
             qd, _ = _lib.to_device(qw, torch.float32)
             qd = qd.reshape(-1)
             if qd.numel() != xd.shape[1]:
@@ -69,8 +79,8 @@ def _dequantizer(ttype):
     return dequantize
 
 
-QUANTIZE = {tt: _quantizer(tt) for tt in BYTES_PER_SB}
-DEQUANTIZE = {tt: _dequantizer(tt) for tt in BYTES_PER_SB}
+QUANTIZE = {tt: _quantizer(tt) for tt in BLOCK}
+DEQUANTIZE = {tt: _dequantizer(tt) for tt in BLOCK}
 
 
 def roundtrip(x, ttype, qw=None):

@@ -14,7 +14,8 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 GOLDEN = os.path.join(ROOT, "tests", "golden", "kquant_golden.npz")
-TYPES = ["Q2_K", "Q3_K", "Q4_K", "Q6_K"]
+TYPES = ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"]
+CODEC_TYPES = TYPES + ["Q8_0"]
 
 
 def pytest_configure(config):

@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import TYPES, heavy_tailed
+from conftest import CODEC_TYPES, heavy_tailed
 from oracle import kquant_oracle as K
 
 pytestmark = pytest.mark.gpu
@@ -20,7 +20,7 @@ def _say(msg):
     print(msg, flush=True)
 
 
-@pytest.mark.parametrize("tt", TYPES)
+@pytest.mark.parametrize("tt", CODEC_TYPES)
 def test_golden_bytes(golden, kq, tt):
     for name in ("heavy", "linear", "edge"):
         x = golden[f"x/{name}"]
@@ -37,7 +37,7 @@ def test_golden_bytes(golden, kq, tt):
                 assert np.array_equal(rec.view(np.uint32), golden[rk].view(np.uint32))
 
 
-@pytest.mark.parametrize("tt", TYPES)
+@pytest.mark.parametrize("tt", CODEC_TYPES)
 @pytest.mark.parametrize("weighted", [False, True])
 def test_matches_oracle_seeded(kq, tt, weighted):
     nrow, n = 48, 2048
@@ -55,7 +55,7 @@ def test_matches_oracle_seeded(kq, tt, weighted):
         assert np.array_equal(rec.view(np.uint32), K.DEQUANTIZE[tt](want, n).view(np.uint32))
 
 
-@pytest.mark.parametrize("tt", TYPES)
+@pytest.mark.parametrize("tt", CODEC_TYPES)
 def test_ragged_superblock_counts(kq, tt):
     """Superblock counts that leave partial waves (1, 3, 5, 7, 9 superblocks)."""
     for nrow, n in [(1, 256), (3, 256), (1, 1280), (7, 256), (3, 768)]:
@@ -66,6 +66,31 @@ def test_ragged_superblock_counts(kq, tt):
             with np.errstate(all="ignore"):
                 want = K.QUANTIZE[tt](x, q)
             assert np.array_equal(kq.QUANTIZE[tt](x, q), want)
+
+
+def test_q8_0_rows_of_whole_blocks(kq):
+    """Q8_0 rows need only whole 32-weight blocks: row lengths that leave a wave's
+    8-block chunk partly filled (odd and even block counts), the overflow-free
+    extremes of the scale, and ties at half a step."""
+    for nrow, n in [(1, 32), (3, 96), (5, 160), (2, 224), (7, 288), (1, 4096 + 32)]:
+        _say(f"Q8_0 [{nrow},{n}]")
+        x = heavy_tailed(nrow, n, seed=nrow * 100 + n)
+        want = K.QUANTIZE["Q8_0"](x)
+        assert np.array_equal(kq.QUANTIZE["Q8_0"](x), want)
+        rec = kq.DEQUANTIZE["Q8_0"](want, n)
+        assert np.array_equal(rec.view(np.uint32), K.DEQUANTIZE["Q8_0"](want, n).view(np.uint32))
+    x = np.zeros((4, 64), np.float32)
+    x[0, :32] = np.float32(1e-38) * np.arange(32)     # 1/d overflows: the reference stores 0 codes
+    x[1, :32] = np.arange(32) - 15.5                    # d = 1: codes on exact half-steps
+    x[1, 0] = 127.0
+    x[2, :32] = 65504.0 * 127                          # fp16 scale at its maximum
+    x[2, 32:] = -1e30                                  # scale overflows fp16
+    x[3] = -0.0
+    with np.errstate(all="ignore"):
+        want = K.QUANTIZE["Q8_0"](x)
+    assert np.array_equal(kq.QUANTIZE["Q8_0"](x), want)
+    with pytest.raises(ValueError):
+        kq.QUANTIZE["Q8_0"](np.zeros((2, 48), np.float32))
 
 
 def test_device_tensors_stay_on_device(kq):
@@ -94,13 +119,14 @@ def test_full_size_roundtrip_properties(kq):
     rng = np.random.default_rng(0)
     x = torch.from_numpy((rng.standard_normal((3072, 1024)) * 0.02).astype(np.float32)).cuda()
     qw = torch.from_numpy(np.abs(rng.standard_normal(1024)).astype(np.float32) + 0.1).cuda()
-    for tt in TYPES:
+    for tt in CODEC_TYPES:
         _say(f"full-size {tt}")
         raw = kq.QUANTIZE[tt](x, qw)
         rec = kq.DEQUANTIZE[tt](raw, 1024)
         assert torch.isfinite(rec).all()
         rel = (torch.linalg.norm(rec - x) / torch.linalg.norm(x)).item()
-        assert rel < {"Q2_K": 0.6, "Q3_K": 0.35, "Q4_K": 0.2, "Q6_K": 0.05}[tt]
+        assert rel < {"Q2_K": 0.6, "Q3_K": 0.35, "Q4_K": 0.2, "Q5_K": 0.1, "Q6_K": 0.05,
+                      "Q8_0": 0.01}[tt]
         # oracle parity on a row slice of the same tensor
         sl = slice(1000, 1032)
         want = K.QUANTIZE[tt](x[sl].cpu().numpy(), qw.cpu().numpy())

@@ -59,7 +59,7 @@ def test_factor_gives_up_after_max_tries():
         E.inv_upper_factor(H, 0.01, max_tries=3)
 
 
-@pytest.mark.parametrize("tt", ["Q2_K", "Q3_K", "Q4_K", "Q6_K"])
+@pytest.mark.parametrize("tt", ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"])
 def test_grid_and_repack_against_golden(golden, tt):
     """Decoding the committed grid reproduces the reference decoder; re-packing the
     decoded codes reproduces the golden bytes."""
@@ -76,16 +76,7 @@ def test_grid_and_repack_against_golden(golden, tt):
     assert codes.min() >= lo and codes.max() <= hi
     assert np.array_equal(np.where(nz, dle * codes.astype(F32) - mle, rec), rec)
     # where dl == 0 the code cannot be read back from rec; take it from the bytes
-    if tt == "Q2_K":
-        packed = K.unpack_2bit(raw.reshape(-1, 84)[:, 16:80]).reshape(nrow, n).astype(np.int32)
-    elif tt == "Q3_K":
-        b = raw.reshape(-1, 110)
-        packed = K.unpack_q3_codes(b[:, 0:32], b[:, 32:96]).reshape(nrow, n)
-    elif tt == "Q4_K":
-        packed = K.unpack_nibbles(raw.reshape(-1, 144)[:, 16:144]).reshape(nrow, n).astype(np.int32)
-    else:
-        b = raw.reshape(-1, 210)
-        packed = K.unpack_q6_codes(b[:, 0:128], b[:, 128:192]).reshape(nrow, n) - 32
+    packed = K.stored_codes(tt, raw).reshape(nrow, n)
     codes = np.where(nz, codes, packed)
     assert np.array_equal(E.write_codes(tt, raw, codes, nrow, n), raw)
 
@@ -112,7 +103,7 @@ def _scalar_sweep(xp, U, dl, ml, lo, hi, sub, order):
     return codes
 
 
-@pytest.mark.parametrize("tt", ["Q2_K", "Q3_K", "Q4_K", "Q6_K"])
+@pytest.mark.parametrize("tt", ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"])
 def test_sweep_matches_scalar_recurrence(tt):
     n, nrow = 256, 3
     W = heavy_tailed(nrow, n, seed=7)
@@ -127,7 +118,7 @@ def test_sweep_matches_scalar_recurrence(tt):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("tt", ["Q2_K", "Q3_K", "Q4_K", "Q6_K"])
+@pytest.mark.parametrize("tt", ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"])
 def test_diagonal_hessian_reduces_to_codec(tt):
     """With a diagonal H nothing propagates: every superblock whose sub-block steps are
     all non-zero gets exactly the codec's own requantized bytes."""
