@@ -167,6 +167,48 @@ int cp_permute_gather(const void* src, void* dst, const int32_t* row_perm,
                       const int32_t* col_perm, int64_t rows, int64_t cols, int elem_bytes,
                       void* stream);
 
+/* ---- PERM container objective (coldpress/perm/objective.py) ---- */
+
+typedef struct cp_err_tensor {
+  int ttype;             /* any cp_ttype                                                */
+  int x_dtype;           /* 0 = float32, 1 = float16 (GGUF F16 weights)                 */
+  int64_t nrow, n;       /* x is [nrow, n] row-major, n a multiple of the block width   */
+  const void* x;
+  const float* qw;       /* [n] importance (imatrix means) or NULL                      */
+  const int32_t* perm;   /* [n] column permutation, or NULL for the identity            */
+  const double* wvec;    /* [n] error weights (indexed through perm) or NULL            */
+  const int32_t* rows;   /* [rows_used] sorted row sample, or NULL for every row        */
+  int64_t rows_used;
+} cp_err_tensor;
+
+/* Workspace bytes cp_tensor_err_batch needs (0 for an invalid type). */
+size_t cp_tensor_err_ws_bytes(const cp_err_tensor* tensors, int count);
+
+/* out[i] (device float64) = the quantization error of tensor i, for ``count``
+ * tensors in one pass. Replaces objective.tensor_err(x, ttype, qw, perm, wvec,
+ * rows_sample, seed) -- coldpress/perm/objective.py:17-39 -- once the caller has
+ * drawn the row sample (objective.py:21-24) and dropped the F16/F32/BF16 types
+ * (error 0). Bit-identical to the reference: the column sums run row after row
+ * and the weighted total is numpy's pairwise float64 sum. An index outside its
+ * range is never dereferenced; that tensor's result is NaN. */
+int cp_tensor_err_batch(const cp_err_tensor* tensors, int count, void* ws, size_t ws_bytes,
+                        double* out, void* stream);
+
+/* Workspace bytes of cp_col_sq_sums / cp_col_log_rms. */
+size_t cp_col_sums_ws_bytes(int64_t nrow, int64_t n, int64_t row_step);
+
+/* acc[c] (device float64) = sum over rows of x[r][c]^2 in float64, summed in chunks
+ * of row_step rows with the chunk sums added in order (objective.py:44-48).
+ * Bit-identical. */
+int cp_col_sq_sums(const void* x, int x_dtype, int64_t nrow, int64_t n, int64_t row_step,
+                   double* acc, void* ws, size_t ws_bytes, void* stream);
+
+/* out[c] = log(sqrt(acc[c] / nrow) + 1e-12) -- objective.col_log_rms(x, row_step),
+ * coldpress/perm/objective.py:42-49. The sums are bit-identical; log is the
+ * device libm's (within 2 ulp of the host's). */
+int cp_col_log_rms(const void* x, int x_dtype, int64_t nrow, int64_t n, int64_t row_step,
+                   double* out, void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,4 +11,6 @@ Modules
   ef_oracle      -- coldpress/ef.py:46-218: inverse-Cholesky factor, committed
                     grid, code repack, the EF column sweep
   hess_oracle    -- coldpress/hessians.py:137-154: X^T X accumulation
+  perm_oracle    -- coldpress/perm: Qwen3 index moves, the container objective
+                    (objective.py) and the space-map optimizer (qwen3.py)
 """

@@ -35,6 +35,16 @@ class EfTensor(ctypes.Structure):
 
 _ef_p = ctypes.POINTER(EfTensor)
 
+
+class ErrTensor(ctypes.Structure):
+    """struct cp_err_tensor (include/coldpress_hip.h)."""
+    _fields_ = [("ttype", ctypes.c_int), ("x_dtype", ctypes.c_int), ("nrow", ctypes.c_int64),
+                ("n", ctypes.c_int64), ("x", _vp), ("qw", _vp), ("perm", _vp), ("wvec", _vp),
+                ("rows", _vp), ("rows_used", ctypes.c_int64)]
+
+
+_err_p = ctypes.POINTER(ErrTensor)
+
 # name -> (restype, argtypes); every symbol include/coldpress_hip.h declares
 SIGNATURES = {
     "cp_last_error": (ctypes.c_char_p, []),
@@ -55,6 +65,11 @@ SIGNATURES = {
     "cp_ef_profile": (None, [_i32]),
     "cp_ef_phase_ms": (_i32, [_vp, _i32]),
     "cp_permute_gather": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
+    "cp_tensor_err_ws_bytes": (_sz, [_err_p, _i32]),
+    "cp_tensor_err_batch": (_i32, [_err_p, _i32, _vp, _sz, _vp, _vp]),
+    "cp_col_sums_ws_bytes": (_sz, [_i64, _i64, _i64]),
+    "cp_col_sq_sums": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "cp_col_log_rms": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
 }
 
 

@@ -12,71 +12,14 @@
 
 namespace cp {
 
-// ---------------------------------------------------------------- Q8_0
-// Blocks of 32 weights: d = max|x|/127 (fp16), codes int8 = round-half-away(x/d)
-// (kquant.py:706-727). A wave covers 256 consecutive weights (8 blocks) with one
-// float4 per lane; the 8 lanes of a block reduce max|x| with xor shuffles (max is
-// exact in any order). The wave's 8*34 = 272 output bytes are assembled in LDS
-// and leave as 68 dword stores.
-constexpr int kQ8Bytes = 34;
-
-// numpy's float32 -> int8 cast of sign(v)*floor(|v|+0.5) on x86: truncation to
-// int32 (0x80000000 for NaN, inf and |v| >= 2^31), then the low byte. Finite
-// scales keep |v| <= 127; a scale whose reciprocal overflows (max|x| < 3.7e-37)
-// sends v to +-inf or NaN, and the reference then stores code 0.
-__device__ __forceinline__ uint32_t q8_code(float x, float inv) {
-  const float v = x * inv;
-  const float a = floorf(fabsf(v) + 0.5f);
-  int q = a < 2147483648.0f ? (int)a : 0;
-  q = v < 0.0f ? -q : q;
-  return (uint32_t)q & 0xFFu;
-}
-
 __global__ __launch_bounds__(256) void q8_encode_kernel(const float* __restrict__ x, int64_t nblk,
                                                         uint8_t* __restrict__ out) {
-  __shared__ uint32_t s_out[kWavesPerBlock][68];
-  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t chunk = (int64_t)blockIdx.x * kWavesPerBlock + wv;  // 8 blocks per chunk
-  const int64_t blk = chunk * 8 + (lane >> 3);
-  const bool valid = blk < nblk;
-  float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  if (valid) v = reinterpret_cast<const float4*>(x)[chunk * 64 + lane];
-  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
-  amax = fmaxf(amax, __shfl_xor(amax, 2));
-  amax = fmaxf(amax, __shfl_xor(amax, 4));
-  const float d = amax / 127.0f;
-  const float inv = d != 0.0f ? 1.0f / d : 0.0f;
-  const uint32_t codes = q8_code(v.x, inv) | q8_code(v.y, inv) << 8 | q8_code(v.z, inv) << 16 |
-                         q8_code(v.w, inv) << 24;
-  uint16_t* so = reinterpret_cast<uint16_t*>(s_out[wv]);
-  const int h = (lane >> 3) * (kQ8Bytes / 2) + 1 + 2 * (lane & 7);  // in halfwords
-  so[h] = (uint16_t)codes;
-  so[h + 1] = (uint16_t)(codes >> 16);
-  if ((lane & 7) == 0) so[h - 1] = half_bits(d);
-  __syncthreads();
-  if (chunk * 8 >= nblk) return;
-  const int64_t nvalid = nblk - chunk * 8 < 8 ? nblk - chunk * 8 : 8;
-  const int bytes = (int)nvalid * kQ8Bytes;
-  uint8_t* dst = out + chunk * 8 * kQ8Bytes;
-  for (int dw = lane; dw < bytes / 4; dw += 64) reinterpret_cast<uint32_t*>(dst)[dw] = s_out[wv][dw];
-  if ((bytes & 3) && lane == 0)
-    reinterpret_cast<uint16_t*>(dst)[bytes / 2 - 1] = so[bytes / 2 - 1];
+  q8_encode_block(x, nblk, out, blockIdx.x);
 }
 
-// One thread per 4 consecutive weights: y = d * code in float32.
 __global__ __launch_bounds__(256) void q8_decode_kernel(const uint8_t* __restrict__ raw,
                                                         int64_t nblk, float* __restrict__ y) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t blk = t >> 3;
-  if (blk >= nblk) return;
-  const uint16_t* b = reinterpret_cast<const uint16_t*>(raw + blk * kQ8Bytes);
-  const int j = (int)(t & 7);
-  const float d = half_value(b[0]);
-  const uint32_t c = (uint32_t)b[1 + 2 * j] | (uint32_t)b[2 + 2 * j] << 16;
-  reinterpret_cast<float4*>(y)[t] =
-      make_float4(d * (float)(int8_t)(c & 0xFF), d * (float)(int8_t)((c >> 8) & 0xFF),
-                  d * (float)(int8_t)((c >> 16) & 0xFF), d * (float)(int8_t)(c >> 24));
+  q8_decode_thread(raw, nblk, y, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
 template <int TT, bool IMAT>

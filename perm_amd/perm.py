@@ -139,3 +139,131 @@ def unpermute_layer(Wp, perms, layer, dims):
             "attn_output": gather(Wp["attn_output"], P, o_idx),
             "ffn_gate": gather(Wp["ffn_gate"], Pf, P), "ffn_up": gather(Wp["ffn_up"], Pf, P),
             "ffn_down": gather(Wp["ffn_down"], P, Pf)}
+
+
+# ---------------------------------------------------------------- optimizer
+
+def res_space_tensors(weights, dims):
+    """Tensors whose input axis is the residual space, in the reference's order
+    (qwen3.py:252-257)."""
+    names = ["token_embd.weight", "output.weight"]
+    for l in range(dims["n_layers"]):
+        for k in RES_INPUT_KINDS:
+            names.append(f"blk.{l}.{k}.weight")
+    return [n for n in names if n in weights]
+
+
+def build_res_keys(weights, dims, profiles=None):
+    """Candidate residual sort keys from the per-tensor column profiles
+    (qwen3.py:269-281)."""
+    from .objective import col_log_rms
+    keys, profs = {}, []
+    for n in res_space_tensors(weights, dims):
+        profs.append((n, profiles[n] if profiles is not None else col_log_rms(weights[n])))
+    stand = [(p - p.mean()) / (p.std() + 1e-9) for _, p in profs]
+    keys["mean-logrms"] = np.mean(stand, axis=0)
+    emb = [p for n, p in profs if n == "token_embd.weight"]
+    if emb:
+        keys["embd-logrms"] = emb[0]
+    blk = [s for (n, _), s in zip(profs, stand) if n.startswith("blk.")]
+    if blk:
+        keys["blk-logrms"] = np.mean(blk, axis=0)
+    return keys
+
+
+def optimize(weights, ttypes, qws, dims, rows_sample=16384, log=print):
+    """Choose the res / ffn / vo permutations minimising the container objective
+    (coldpress/perm/spacemaps/qwen3.py:284-355), with every objective evaluation on
+    the GPU: one batched pass per residual candidate (all residual-space tensors),
+    one for the ffn_down baselines of every layer, one for their candidates, and the
+    same two for attn_output.
+
+    weights : {gguf_name: [nrow, ne0] float16/float32, numpy or torch}; host arrays are
+              uploaded once and stay resident for the whole search
+    ttypes  : {gguf_name: target container type}
+    qws     : {gguf_name: imatrix means [ne0]} (missing -> unweighted path)
+    Returns (perms, report) with the reference's keys (report adds "key", the chosen
+    residual candidate)."""
+    import time
+    from .objective import col_log_rms, tensor_err_many, weights_dev
+    t0 = time.time()
+    dev = {n: weights_dev(w)[0] for n, w in weights.items()}
+    res_names = res_space_tensors(dev, dims)
+
+    def res_obj(perm):
+        return _ordered_sum(tensor_err_many(
+            [dict(x=dev[n], ttype=ttypes[n], qw=qws.get(n), perm=perm, rows_sample=rows_sample)
+             for n in res_names]))
+
+    base = res_obj(None)
+    res_perm, res_val, res_name = np.arange(dims["d_model"]), base, "identity"
+    profiles = {n: col_log_rms(dev[n]) for n in res_names}
+    for kname, key in build_res_keys(dev, dims, profiles).items():
+        perm = np.argsort(key, kind="stable")
+        val = res_obj(perm)
+        log(f"  res sort[{kname}]: {val:.6g} ({(val / base - 1) * 100:+.2f}%)")
+        if val < res_val:
+            res_perm, res_val, res_name = perm, val, kname
+    log(f"  res -> {res_name} ({(res_val / base - 1) * 100:+.2f}%)")
+
+    L = dims["n_layers"]
+    hd, nkv, nh = dims["head_dim"], dims["n_kv"], dims["n_heads"]
+    group = nh // nkv
+    fns = [f"blk.{l}.ffn_down.weight" for l in range(L)]
+    ons = [f"blk.{l}.attn_output.weight" for l in range(L)]
+    fcand = [np.argsort(col_log_rms(dev[fn]), kind="stable") for fn in fns]
+    heads_all, ocand = [], []
+    for on in ons:
+        prof = col_log_rms(dev[on])  # column sums are per column: slices share them
+        heads = []
+        for h in range(nkv):
+            key = np.zeros(hd)
+            for q in [q for q in range(nh) if q // group == h]:
+                key = key + prof[q * hd:(q + 1) * hd]
+            heads.append(np.argsort(key, kind="stable"))
+        full = np.arange(nh * hd)
+        for q in range(nh):
+            full[q * hd:(q + 1) * hd] = q * hd + heads[q // group]
+        heads_all.append(heads)
+        ocand.append(full)
+    errs = tensor_err_many(
+        [dict(x=dev[fn], ttype=ttypes[fn], qw=qws.get(fn)) for fn in fns]
+        + [dict(x=dev[fn], ttype=ttypes[fn], qw=qws.get(fn), perm=p) for fn, p in zip(fns, fcand)]
+        + [dict(x=dev[on], ttype=ttypes[on], qw=qws.get(on)) for on in ons]
+        + [dict(x=dev[on], ttype=ttypes[on], qw=qws.get(on), perm=p) for on, p in zip(ons, ocand)])
+    fb_all, fv_all = errs[0:L], errs[L:2 * L]
+    ob_all, ov_all = errs[2 * L:3 * L], errs[3 * L:4 * L]
+    ffn_perms, ffn_val, ffn_base = [], 0.0, 0.0
+    vo_perms, vo_val, vo_base = [], 0.0, 0.0
+    for l in range(L):
+        fb, fp, fv = fb_all[l], fcand[l], fv_all[l]
+        if fv >= fb:
+            fp, fv = np.arange(dims["d_ffn"]), fb
+        ffn_perms.append(fp)
+        ffn_val += fv
+        ffn_base += fb
+        ob, heads, ov = ob_all[l], heads_all[l], ov_all[l]
+        if ov >= ob:
+            heads = [np.arange(hd) for _ in range(nkv)]
+            ov = ob
+        vo_perms.append(heads)
+        vo_val += ov
+        vo_base += ob
+
+    def rel(v, b):
+        return v / b - 1 if b else 0.0
+
+    perms = {"res": res_perm, "ffn": ffn_perms, "vo": vo_perms}
+    report = {"res": {"base": base, "opt": res_val, "rel": rel(res_val, base), "key": res_name},
+              "ffn": {"base": ffn_base, "opt": ffn_val, "rel": rel(ffn_val, ffn_base)},
+              "vo": {"base": vo_base, "opt": vo_val, "rel": rel(vo_val, vo_base)},
+              "rows_sample": rows_sample, "seconds": time.time() - t0}
+    return perms, report
+
+
+def _ordered_sum(vals):
+    """The reference's running total: 0.0 + v0 + v1 + ... in order (qwen3.py:260-266)."""
+    total = 0.0
+    for v in vals:
+        total += v
+    return total

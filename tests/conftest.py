@@ -42,3 +42,23 @@ def correlated_hessian(n, T, seed):
 @pytest.fixture(scope="session")
 def golden():
     return np.load(GOLDEN)
+
+
+# The reference optimizer test's model (test_perm_optimize.py:14-42): 2 layers,
+# d_model 256, d_ffn 512, vocab 512, 4 q heads / 2 kv heads of 64, f16 weights.
+OPT_DIMS = {"d_model": 256, "d_ffn": 512, "n_layers": 2, "n_heads": 4, "n_kv": 2, "head_dim": 64}
+
+
+def small_qwen3_model(seed=0):
+    D, FFN, V, HD, NKV, NH = 256, 512, 512, 64, 2, 4
+    shapes = {"token_embd.weight": (V, D), "output.weight": (V, D)}
+    for l in range(2):
+        shapes[f"blk.{l}.attn_q.weight"] = (NH * HD, D)
+        shapes[f"blk.{l}.attn_k.weight"] = (NKV * HD, D)
+        shapes[f"blk.{l}.attn_v.weight"] = (NKV * HD, D)
+        shapes[f"blk.{l}.attn_output.weight"] = (D, NH * HD)
+        shapes[f"blk.{l}.ffn_gate.weight"] = (FFN, D)
+        shapes[f"blk.{l}.ffn_up.weight"] = (FFN, D)
+        shapes[f"blk.{l}.ffn_down.weight"] = (D, FFN)
+    rng = np.random.default_rng(seed)
+    return {n: (rng.standard_normal(s) ** 3 * 0.1).astype(np.float16) for n, s in shapes.items()}
