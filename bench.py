@@ -158,6 +158,125 @@ def cpu_baseline(W, H, slot, layers, total_weights):
     }
 
 
+PERM_METRIC = "PERM container-objective search Mweights/s (Qwen3-0.6B space map), 1 GPU"
+
+
+def perm_search_weights(dims, rows_sample, n_keys):
+    """Weights the search round-trips through the codec: (1 + n_keys) residual
+    evaluations over every residual-space tensor (the embedding at its row sample),
+    then two ffn_down and two attn_output evaluations per layer."""
+    from perm_amd import workloads as wl
+    L, d = dims["n_layers"], dims["d_model"]
+    res = min(rows_sample, wl.QWEN3_06B_VOCAB) * d + L * d * sum(
+        r for name, r, _n, fam in wl.QWEN3_06B_LAYER if fam in ("qkv_in", "gateup_in"))
+    return (1 + n_keys) * res + L * 2 * d * dims["d_ffn"] + \
+        L * 2 * d * dims["n_heads"] * dims["head_dim"]
+
+
+def perm_cpu_baseline(weights, ttypes, qws, rows_sample, n_keys, dims):
+    """The numpy oracle's tensor_err (a port of objective.py + kquant.py) called as the
+    search calls it on the embedding (its 16384-row sample) and on every tensor of
+    layer 0 (residual-space tensors with a column permutation, ffn_down and
+    attn_output whole), timed per class and extrapolated by round-tripped weights."""
+    import numpy as np
+    from oracle import perm_oracle as Po
+    from perm_amd import workloads as wl
+    L = dims["n_layers"]
+    rng = np.random.default_rng(1)
+    spent, total_t = 0.0, 0.0
+    classes = [("token_embd.weight", 1 + n_keys, 1)]
+    for name, _r, _n, fam in wl.QWEN3_06B_LAYER:
+        classes.append((f"blk.0.{name}.weight",
+                        (1 + n_keys) if fam in ("qkv_in", "gateup_in") else 2, L))
+    for name, reps, layers in classes:
+        x = weights[name].cpu().numpy()
+        perm = rng.permutation(x.shape[1])
+        t0 = time.perf_counter()
+        Po.tensor_err(x, ttypes[name], qws.get(name), perm=perm,
+                      rows_sample=rows_sample if name == "token_embd.weight" else None)
+        dt = time.perf_counter() - t0
+        spent += dt
+        total_t += dt * reps * layers
+        log(f"cpu {name} {ttypes[name]}: {dt:.2f}s")
+    work = perm_search_weights(dims, rows_sample, n_keys)
+    return {"value": work / total_t / 1e6, "unit": "Mweights/s", "cores": 1, "kind": "port",
+            "sample": (f"numpy oracle tensor_err (port of objective.py / kquant.py) called as the "
+                       f"search calls it on the 16384-row embedding sample and on each of layer "
+                       f"0's 7 tensors ({spent:.1f} s of CPU work), scaled by evaluations and "
+                       f"layers to the search's {work} round-tripped weights (est. {total_t:.0f} s; "
+                       f"the column profiles and the sort are not counted); single-threaded numpy"),
+            "host_cpus": os.cpu_count()}
+
+
+def perm_main(args):
+    """The Qwen3-0.6B PERM search (coldpress/perm/spacemaps/qwen3.py:284-355) with every
+    objective evaluation on the GPU: one step = one full search."""
+    import ctypes
+    import torch
+    from perm_amd import _lib, objective, perm as gp
+    from perm_amd import workloads as wl
+    lib = _lib.load()
+    dims = dict(wl.QWEN3_06B_DIMS, n_layers=args.layers)
+    rows_sample = 16384
+    log(f"building PERM workload: {args.layers} layers + embedding, f16")
+    w = wl.qwen3_gguf_weights(layers=args.layers)
+    ttypes = wl.qwen3_mixed_typemap(w)
+    qws = wl.imatrix_means(w)
+    n_keys = 3
+    work = perm_search_weights(dims, rows_sample, n_keys)
+    quiet = lambda *_: None  # noqa: E731
+    for i in range(args.warmup):
+        gp.optimize(w, ttypes, qws, dims, rows_sample=rows_sample, log=quiet)
+        torch.cuda.synchronize()
+        log(f"warmup {i + 1}/{args.warmup} done")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        perms, report = gp.optimize(w, ttypes, qws, dims, rows_sample=rows_sample, log=quiet)
+        log(f"step {i + 1}/{args.steps} done")
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+
+    # one profiled residual evaluation (the search's largest pass): phases by HIP events
+    names = gp.res_space_tensors(w, dims)
+    items = [dict(x=w[n], ttype=ttypes[n], qw=qws.get(n), perm=perms["res"],
+                  rows_sample=rows_sample) for n in names]
+    lib.cp_err_profile(1)
+    objective.tensor_err_many(items)
+    buf = (ctypes.c_float * 5)()
+    lib.cp_err_phase_ms(ctypes.cast(buf, ctypes.c_void_p), 5)
+    lib.cp_err_profile(0)
+    ph = list(buf)
+    res_w = sum(min(rows_sample, w[n].shape[0]) * w[n].shape[1] for n in names)
+    # the encode kernels are VALU-bound; the column sums read 8 B and the gather
+    # moves 6 B (f16 in, f32 out) per weight -- the HBM-bound phases
+    colsum_bw = res_w * 8 / (ph[3] * 1e-3) / 1e9
+    roof = {"kernel": "err_colsum_kernel", "bound": "hbm", "achieved": colsum_bw,
+            "peak": 8000.0, "unit": "GB/s", "frac": colsum_bw / 8000.0, "traffic": None,
+            "avg_launch_ms": ph[3], "launches_per_step": None,
+            "note": "the search's dominant phase is the VALU-bound encode (phases_ms)"}
+    result = {
+        "metric": PERM_METRIC, "value": work / (wall / args.steps) / 1e6, "unit": "Mweights/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random-init f16 weights with per-channel log-normal scales)",
+        "config": {"workload": f"qwen3-0.6b-shaped PERM search, {args.layers} layers + "
+                               f"151936x1024 embedding, Q6_K/Q3_K/Q2_K, rows_sample 16384",
+                   "layers": args.layers, "roundtrip_weights": work, "rows_sample": rows_sample,
+                   "candidates": {"res": n_keys, "ffn": 1, "vo": 1}},
+        "report": {k: v for k, v in report.items() if k != "seconds"},
+        "res_pass": {"weights": res_w, "phases_ms": {
+            "gather": ph[0], "encode": ph[1], "decode": ph[2], "colsum": ph[3], "total": ph[4]}},
+        "roofline": roof,
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline (numpy oracle tensor_err on 256-row slices)")
+        result["cpu_baseline"] = perm_cpu_baseline(w, ttypes, qws, rows_sample, n_keys, dims)
+        result["gpu_over_cpu"] = result["value"] / result["cpu_baseline"]["value"]
+    print(json.dumps(result))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -168,6 +287,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ef-mode", choices=["mfma", "exact"], default="exact",
                     help="cross-block error propagation: MFMA GEMM or the reference's exact order")
+    ap.add_argument("--workload", choices=["ef", "perm-search"], default="ef",
+                    help="ef: the EF encode + Hessians line (default); perm-search: the PERM "
+                         "space-map search on the GPU objective")
     args = ap.parse_args()
     if args.gpus != 1:
         msg = (f"bench.py runs on one GPU only (got --gpus {args.gpus}); the encoder path "
@@ -181,6 +303,9 @@ def main():
     from perm_amd import workloads as wl
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a GPU")
+    if args.workload == "perm-search":
+        perm_main(args)
+        return
     lib = _lib.load()
     dev = "cuda"
     layers = args.layers

@@ -1,6 +1,7 @@
 /* coldpress_hip.h -- C ABI of libcoldpress_hip.so, the MI355X (gfx950) encoder
- * hot path of coldpress: k-quant codec, Hessian X^T X, damped inverse-Hessian
- * factor, and GPTQ-style error feedback (EF) into committed k-quant grids.
+ * hot path of coldpress: GGUF container codec, Hessian X^T X, damped
+ * inverse-Hessian factor, GPTQ-style error feedback (EF) into committed k-quant
+ * grids, and the PERM channel moves and container objective.
  *
  * Conventions
  *  - Every pointer argument named x, qw, raw, out, y, H, U, W, order, X ... is a
@@ -194,8 +195,32 @@ size_t cp_tensor_err_ws_bytes(const cp_err_tensor* tensors, int count);
 int cp_tensor_err_batch(const cp_err_tensor* tensors, int count, void* ws, size_t ws_bytes,
                         double* out, void* stream);
 
+/* Per-thread switch for phase timing of cp_tensor_err_batch calls (hipEvents on
+ * the call's stream). No counterpart in the reference. */
+void cp_err_profile(int enable);
+
+/* Milliseconds of the calling thread's last profiled cp_tensor_err_batch call per
+ * phase: out[0] gather, out[1] encode, out[2] decode, out[3] column sums, out[4]
+ * weighted total. Waits for the call's last event. Returns the phases written. */
+int cp_err_phase_ms(float* out, int nphase);
+
+typedef struct cp_col_tensor {
+  const void* x;         /* [nrow, n] row-major                                         */
+  int x_dtype;           /* 0 = float32, 1 = float16                                    */
+  int64_t nrow, n;
+  double* out;           /* [n] device float64 result                                   */
+} cp_col_tensor;
+
 /* Workspace bytes of cp_col_sq_sums / cp_col_log_rms. */
 size_t cp_col_sums_ws_bytes(int64_t nrow, int64_t n, int64_t row_step);
+
+/* Workspace bytes of cp_col_sq_sums_batch. */
+size_t cp_col_sums_batch_ws_bytes(const cp_col_tensor* tensors, int count, int64_t row_step);
+
+/* cp_col_sq_sums (log_rms = 0) or cp_col_log_rms (log_rms = 1) for ``count``
+ * tensors in one pass (the profiles a space-map search sorts by). */
+int cp_col_sq_sums_batch(const cp_col_tensor* tensors, int count, int64_t row_step, int log_rms,
+                         void* ws, size_t ws_bytes, void* stream);
 
 /* acc[c] (device float64) = sum over rows of x[r][c]^2 in float64, summed in chunks
  * of row_step rows with the chunk sums added in order (objective.py:44-48).

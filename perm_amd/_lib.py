@@ -45,6 +45,15 @@ class ErrTensor(ctypes.Structure):
 
 _err_p = ctypes.POINTER(ErrTensor)
 
+
+class ColTensor(ctypes.Structure):
+    """struct cp_col_tensor (include/coldpress_hip.h)."""
+    _fields_ = [("x", _vp), ("x_dtype", ctypes.c_int), ("nrow", ctypes.c_int64),
+                ("n", ctypes.c_int64), ("out", _vp)]
+
+
+_col_p = ctypes.POINTER(ColTensor)
+
 # name -> (restype, argtypes); every symbol include/coldpress_hip.h declares
 SIGNATURES = {
     "cp_last_error": (ctypes.c_char_p, []),
@@ -67,7 +76,11 @@ SIGNATURES = {
     "cp_permute_gather": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "cp_tensor_err_ws_bytes": (_sz, [_err_p, _i32]),
     "cp_tensor_err_batch": (_i32, [_err_p, _i32, _vp, _sz, _vp, _vp]),
+    "cp_err_profile": (None, [_i32]),
+    "cp_err_phase_ms": (_i32, [_vp, _i32]),
     "cp_col_sums_ws_bytes": (_sz, [_i64, _i64, _i64]),
+    "cp_col_sums_batch_ws_bytes": (_sz, [_col_p, _i32, _i64]),
+    "cp_col_sq_sums_batch": (_i32, [_col_p, _i32, _i64, _i32, _vp, _sz, _vp]),
     "cp_col_sq_sums": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "cp_col_log_rms": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
 }

@@ -26,6 +26,7 @@
 #include "cp_device.h"
 #include "cp_host.h"
 #include "kq_blocks.h"
+#include "phase_clock.h"
 
 namespace cp {
 
@@ -807,35 +808,10 @@ static void grid_range(int ttype, int* lo, int* hi, int* sub) {
   }
 }
 
-// Optional per-phase timing of an EF call with hipEvents on its stream
-// (cp_ef_profile / cp_ef_phase_ms): setup, commit, sweep, repack, decode.
-struct PhaseClock {
-  bool on = false;
-  std::vector<hipEvent_t> ev;
-  std::vector<int> label;  // label[i]: phase of the interval ending at ev[i]
-  int used = 0;
-  hipError_t start(hipStream_t st) {
-    used = 0;
-    label.clear();
-    return mark(-1, st);
-  }
-  hipError_t mark(int phase, hipStream_t st) {
-    if (used == (int)ev.size()) {
-      hipEvent_t e;
-      hipError_t r = hipEventCreate(&e);
-      if (r != hipSuccess) return r;
-      ev.push_back(e);
-    }
-    label.push_back(phase);
-    return hipEventRecord(ev[used++], st);
-  }
-};
+// Optional per-phase timing of an EF call (cp_ef_profile / cp_ef_phase_ms):
+// setup, commit, sweep, repack, decode.
 static thread_local PhaseClock g_clock;
-
-#define CP_PHASE(p)                                                   \
-  do {                                                                \
-    if (g_clock.on) CP_HIP(p < 0 ? g_clock.start(st) : g_clock.mark(p, st)); \
-  } while (0)
+#define CP_PHASE(p) CP_PHASE_MARK(g_clock, p)
 
 // A run of table rows sharing (type, importance) for the templated codec launches.
 struct EfGroup {
@@ -1000,15 +976,7 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
 }
 
 int ef_phase_ms(float* out, int nphase) {
-  for (int p = 0; p < nphase; ++p) out[p] = 0.0f;
-  if (g_clock.used < 2) return 0;
-  CP_HIP(hipEventSynchronize(g_clock.ev[g_clock.used - 1]));
-  for (int i = 1; i < g_clock.used; ++i) {
-    float ms = 0.0f;
-    CP_HIP(hipEventElapsedTime(&ms, g_clock.ev[i - 1], g_clock.ev[i]));
-    const int p = g_clock.label[i];
-    if (p >= 0 && p < nphase) out[p] += ms;
-  }
+  CP_HIP(g_clock.read(out, nphase));
   return nphase < 5 ? nphase : 5;
 }
 

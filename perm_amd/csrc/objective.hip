@@ -20,8 +20,15 @@
 #include <vector>
 
 #include "kq_blocks.h"
+#include "phase_clock.h"
 
 namespace cp {
+
+// Table-held pointers are generic to the compiler; reads through these global
+// address-space types become global loads (a flat load also waits on LDS traffic
+// and forces the loads ahead of it to drain).
+typedef const float __attribute__((address_space(1)))* GF32;
+typedef const uint16_t __attribute__((address_space(1)))* GU16;
 
 struct ErrDev {
   const void* x;
@@ -42,14 +49,16 @@ struct ErrDev {
 
 // --------------------------------------------------------------- gather
 // Four consecutive columns of one gathered row per thread (n % 32 == 0, so the
-// four never straddle rows). Out-of-range indices read element 0 and flag the
-// tensor; its result becomes NaN.
+// four never straddle rows). Negative indices count from the end, as numpy's do;
+// indices still out of range read element 0 and flag the tensor, whose result
+// becomes NaN.
 __global__ __launch_bounds__(256) void err_gather_kernel(const ErrDev* __restrict__ tab) {
   const ErrDev& T = tab[blockIdx.y];
   const int n = T.n;
   if (blockIdx.x == 0 && T.qwp) {
     for (int j = threadIdx.x; j < n; j += 256) {
       int c = T.perm ? T.perm[j] : j;
+      c = c < 0 ? c + n : c;  // numpy's negative indices
       if (c < 0 || c >= n) {
         *T.bad = 1;
         c = 0;
@@ -61,12 +70,14 @@ __global__ __launch_bounds__(256) void err_gather_kernel(const ErrDev* __restric
   if (e >= (int64_t)T.R * n) return;
   const int i = (int)(e / n), j = (int)(e - (int64_t)i * n);
   int64_t src = T.rows ? T.rows[i] : i;
+  src = src < 0 ? src + T.nrow_src : src;
   bool bad = src < 0 || src >= T.nrow_src;
   src = bad ? 0 : src;
   float v[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     int c = T.perm ? T.perm[j + k] : j + k;
+    c = c < 0 ? c + n : c;
     if (c < 0 || c >= n) {
       bad = true;
       c = 0;
@@ -110,34 +121,53 @@ __global__ __launch_bounds__(256) void err_decode_kernel(const ErrDev* __restric
 
 // --------------------------------------------------------------- column sums
 // One lane per column: colerr[c] = (((0 + d2[0,c]) + d2[1,c]) + ...), d2 the
-// float64 square of the float64 difference. Eight rows of loads are issued
-// before their adds.
+// float64 square of the float64 difference, loads pipelined by chain_rows.
+// The sequential chain of one column over rows [r0, r1), loads running one block
+// of B rows ahead of the adds. The block after next is always loaded (clamped to
+// the last full block), so no branch sits between a load and its use and the
+// loads never have to drain early.
+template <int B, class T, class Ld, class Use>
+__device__ __forceinline__ void chain_rows(int64_t r0, int64_t r1, const Ld& ld, const Use& use) {
+  const int64_t nfull = (r1 - r0) / B;
+  T a[B], b[B];
+  auto fill = [&](T (&v)[B], int64_t r) {
+#pragma unroll
+    for (int i = 0; i < B; ++i) v[i] = ld(r + i);
+  };
+  auto drain = [&](const T (&v)[B]) {
+#pragma unroll
+    for (int i = 0; i < B; ++i) use(v[i]);
+  };
+  if (nfull > 0) fill(a, r0);
+  int64_t k = 0;
+  for (; k + 1 < nfull; k += 2) {
+    fill(b, r0 + (k + 1) * B);
+    drain(a);
+    const int64_t ra = r0 + (k + 2) * B;
+    fill(a, ra < r1 - B ? ra : r1 - B);  // past the end: a valid block, never used
+    drain(b);
+  }
+  if (k < nfull) drain(a);
+  for (int64_t r = r0 + nfull * B; r < r1; ++r) {
+    T v = ld(r);
+    use(v);
+  }
+}
+
 __global__ __launch_bounds__(64) void err_colsum_kernel(const ErrDev* __restrict__ tab) {
   const ErrDev& T = tab[blockIdx.y];
   const int c = blockIdx.x * 64 + threadIdx.x;
-  const int n = T.n, R = T.R;
+  const int64_t n = T.n;
   if (c >= n) return;
-  const float* xs = T.xs + c;
-  const float* rc = T.recon + c;
+  const GF32 xs = (GF32)T.xs;
+  const GF32 rc = (GF32)T.recon;
   double acc = 0.0;
-  int r = 0;
-  for (; r + 8 <= R; r += 8) {
-    float a[8], b[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      a[k] = xs[(int64_t)(r + k) * n];
-      b[k] = rc[(int64_t)(r + k) * n];
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const double d = (double)b[k] - (double)a[k];
-      acc = acc + d * d;
-    }
-  }
-  for (; r < R; ++r) {
-    const double d = (double)rc[(int64_t)r * n] - (double)xs[(int64_t)r * n];
-    acc = acc + d * d;
-  }
+  chain_rows<16, float2>(
+      0, T.R, [&](int64_t r) { return make_float2((xs + r * n)[c], (rc + r * n)[c]); },
+      [&](float2 v) {
+        const double d = (double)v.y - (double)v.x;
+        acc = acc + d * d;
+      });
   T.colerr[c] = acc;
 }
 
@@ -218,7 +248,11 @@ __global__ __launch_bounds__(64) void err_final_kernel(const ErrDev* __restrict_
   if (T.wvec) {
     const int32_t* perm = T.perm;
     const double* wv = T.wvec;
-    s = pw_sum([=](int64_t i) { return ce[i] * wv[perm ? perm[i] : i]; }, T.n);
+    const int64_t n = T.n;
+    s = pw_sum([=](int64_t i) {
+      const int64_t c = perm ? perm[i] : i;
+      return ce[i] * wv[c < 0 ? c + n : c];
+    }, T.n);
   } else if (T.qwp) {
     const float* q = T.qwp;
     s = pw_sum([=](int64_t i) { return ce[i] * (double)q[i]; }, T.n);
@@ -235,43 +269,53 @@ __global__ void err_clear_kernel(int* __restrict__ bad, int count) {
 
 // --------------------------------------------------------------- col_log_rms
 // One lane per (column, chunk of row_step rows): the chunk's float64 sum of
-// squares row after row. A second pass adds the chunk sums in order.
+// squares row after row, for many tensors in one launch. A second pass adds the
+// chunk sums in order (and takes log(sqrt(acc / nrow) + 1e-12) when asked).
+struct ColDev {
+  const void* x;
+  double* part;  // [nchunk, n] chunk sums
+  double* out;   // [n]
+  int64_t nrow;
+  int n, x_f16, nchunk, col_groups;
+};
+
 template <bool F16>
-__global__ __launch_bounds__(64) void col_chunk_kernel(const void* __restrict__ x, int64_t nrow,
-                                                       int n, int64_t row_step,
-                                                       double* __restrict__ part) {
-  const int c = blockIdx.x * 64 + threadIdx.x;
-  if (c >= n) return;
-  const int64_t r0 = (int64_t)blockIdx.y * row_step;
-  const int64_t r1 = r0 + row_step < nrow ? r0 + row_step : nrow;
-  auto ld = [&](int64_t r) -> double {
-    const int64_t o = r * n + c;
-    return F16 ? (double)half_value(reinterpret_cast<const uint16_t*>(x)[o])
-               : (double)reinterpret_cast<const float*>(x)[o];
-  };
+__global__ __launch_bounds__(64) void col_chunk_kernel(const ColDev* __restrict__ tab,
+                                                       int64_t row_step) {
+  const ColDev& T = tab[blockIdx.y];
+  const int chunk = (int)(blockIdx.x / T.col_groups);
+  if (chunk >= T.nchunk) return;
+  const int c = (int)(blockIdx.x - chunk * T.col_groups) * 64 + threadIdx.x;
+  if (c >= T.n) return;
+  const int64_t n = T.n;
+  const int64_t r0 = (int64_t)chunk * row_step;
+  const int64_t r1 = r0 + row_step < T.nrow ? r0 + row_step : T.nrow;
   double acc = 0.0;
-  int64_t r = r0;
-  for (; r + 8 <= r1; r += 8) {
-    double v[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = ld(r + k);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) acc = acc + v[k] * v[k];
+  if constexpr (F16) {
+    const GU16 x = (GU16)T.x;
+    chain_rows<32, uint16_t>(r0, r1, [&](int64_t r) { return (x + r * n)[c]; },
+                             [&](uint16_t h) {
+                               const double v = (double)half_value(h);
+                               acc = acc + v * v;
+                             });
+  } else {
+    const GF32 x = (GF32)T.x;
+    chain_rows<32, float>(r0, r1, [&](int64_t r) { return (x + r * n)[c]; },
+                          [&](float f) {
+                            const double v = (double)f;
+                            acc = acc + v * v;
+                          });
   }
-  for (; r < r1; ++r) {
-    const double v = ld(r);
-    acc = acc + v * v;
-  }
-  part[(int64_t)blockIdx.y * n + c] = acc;
+  T.part[(int64_t)chunk * n + c] = acc;
 }
 
-__global__ void col_combine_kernel(const double* __restrict__ part, int64_t nchunk, int n,
-                                   int64_t nrow, int log_rms, double* __restrict__ out) {
+__global__ void col_combine_kernel(const ColDev* __restrict__ tab, int log_rms) {
+  const ColDev& T = tab[blockIdx.y];
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= n) return;
+  if (c >= T.n) return;
   double acc = 0.0;
-  for (int64_t k = 0; k < nchunk; ++k) acc = acc + part[k * n + c];
-  out[c] = log_rms ? log(sqrt(acc / (double)nrow) + 1e-12) : acc;
+  for (int k = 0; k < T.nchunk; ++k) acc = acc + T.part[(int64_t)k * T.n + c];
+  T.out[c] = log_rms ? log(sqrt(acc / (double)T.nrow) + 1e-12) : acc;
 }
 
 // --------------------------------------------------------------- host side
@@ -326,9 +370,12 @@ struct ErrGroup {
   int64_t max_w;  // weights of the largest gathered tensor
 };
 
+// Optional per-phase timing (cp_err_profile / cp_err_phase_ms): gather, encode,
+// decode, column sums, total.
+static thread_local PhaseClock g_err_clock;
+
 template <int TT>
-static void launch_err_codec(const ErrDev* tab, const ErrGroup& g, hipStream_t st) {
-  const dim3 grid_dec((unsigned)((g.max_w / 4 + 255) / 256), (unsigned)g.count);
+static void launch_err_encode(const ErrDev* tab, const ErrGroup& g, hipStream_t st) {
   int64_t blocks;
   if constexpr (TT == CP_Q8_0) {
     blocks = (g.max_w / 32 + 8 * kWavesPerBlock - 1) / (8 * kWavesPerBlock);
@@ -336,19 +383,42 @@ static void launch_err_codec(const ErrDev* tab, const ErrGroup& g, hipStream_t s
     constexpr int S = 64 / Kq<TT>::G;
     blocks = ((g.max_w / 256 + S - 1) / S + kWavesPerBlock - 1) / kWavesPerBlock;
   }
-  const dim3 grid_enc((unsigned)blocks, (unsigned)g.count);
+  const dim3 grid((unsigned)blocks, (unsigned)g.count);
   if constexpr (TT == CP_Q8_0)  // no weighted path
-    err_encode_kernel<TT, false><<<grid_enc, 256, 0, st>>>(tab + g.first);
+    err_encode_kernel<TT, false><<<grid, 256, 0, st>>>(tab + g.first);
   else if (g.imat)
-    err_encode_kernel<TT, true><<<grid_enc, 256, 0, st>>>(tab + g.first);
+    err_encode_kernel<TT, true><<<grid, 256, 0, st>>>(tab + g.first);
   else
-    err_encode_kernel<TT, false><<<grid_enc, 256, 0, st>>>(tab + g.first);
-  if constexpr (TT == CP_Q8_0)
-    err_decode_kernel<TT><<<grid_dec, 256, 0, st>>>(tab + g.first);
-  else
-    err_decode_kernel<TT><<<dim3((unsigned)((g.max_w / 256 * 16 + 255) / 256), (unsigned)g.count),
-                            256, 0, st>>>(tab + g.first);
+    err_encode_kernel<TT, false><<<grid, 256, 0, st>>>(tab + g.first);
 }
+
+template <int TT>
+static void launch_err_decode(const ErrDev* tab, const ErrGroup& g, hipStream_t st) {
+  // Q8_0: one thread per 4 weights; k-quants: 16 threads per superblock
+  const int64_t threads = TT == CP_Q8_0 ? g.max_w / 4 : g.max_w / 256 * 16;
+  err_decode_kernel<TT><<<dim3((unsigned)((threads + 255) / 256), (unsigned)g.count), 256, 0, st>>>(
+      tab + g.first);
+}
+
+template <template <int> class L>
+static void for_group_type(const ErrDev* tab, const ErrGroup& g, hipStream_t st) {
+  switch (g.ttype) {
+    case CP_Q8_0: L<CP_Q8_0>::run(tab, g, st); break;
+    case CP_Q2_K: L<CP_Q2_K>::run(tab, g, st); break;
+    case CP_Q3_K: L<CP_Q3_K>::run(tab, g, st); break;
+    case CP_Q4_K: L<CP_Q4_K>::run(tab, g, st); break;
+    case CP_Q5_K: L<CP_Q5_K>::run(tab, g, st); break;
+    default: L<CP_Q6_K>::run(tab, g, st); break;
+  }
+}
+template <int TT>
+struct EncodeL {
+  static void run(const ErrDev* t, const ErrGroup& g, hipStream_t st) { launch_err_encode<TT>(t, g, st); }
+};
+template <int TT>
+struct DecodeL {
+  static void run(const ErrDev* t, const ErrGroup& g, hipStream_t st) { launch_err_decode<TT>(t, g, st); }
+};
 
 int err_batch(const cp_err_tensor* ts, int count, void* ws, size_t ws_bytes, double* out,
               hipStream_t st) {
@@ -419,47 +489,99 @@ int err_batch(const cp_err_tensor* ts, int count, void* ws, size_t ws_bytes, dou
     for (int i = 0; i < cn; ++i) b.t[i] = sorted[c0 + i];
     err_store_kernel<<<1, 256, 0, st>>>(b, cn, dtab + c0);
   }
+  CP_PHASE_MARK(g_err_clock, -1);
   err_clear_kernel<<<(count + 255) / 256, 256, 0, st>>>(bad, count);
   err_gather_kernel<<<dim3((unsigned)((max_w / 4 + 255) / 256), (unsigned)count), 256, 0, st>>>(dtab);
   CP_LAUNCHED("objective gather");
-  for (const ErrGroup& g : groups) {
-    switch (g.ttype) {
-      case CP_Q8_0: launch_err_codec<CP_Q8_0>(dtab, g, st); break;
-      case CP_Q2_K: launch_err_codec<CP_Q2_K>(dtab, g, st); break;
-      case CP_Q3_K: launch_err_codec<CP_Q3_K>(dtab, g, st); break;
-      case CP_Q4_K: launch_err_codec<CP_Q4_K>(dtab, g, st); break;
-      case CP_Q5_K: launch_err_codec<CP_Q5_K>(dtab, g, st); break;
-      default: launch_err_codec<CP_Q6_K>(dtab, g, st); break;
-    }
-  }
-  CP_LAUNCHED("objective codec");
+  CP_PHASE_MARK(g_err_clock, 0);
+  for (const ErrGroup& g : groups) for_group_type<EncodeL>(dtab, g, st);
+  CP_LAUNCHED("objective encode");
+  CP_PHASE_MARK(g_err_clock, 1);
+  for (const ErrGroup& g : groups) for_group_type<DecodeL>(dtab, g, st);
+  CP_LAUNCHED("objective decode");
+  CP_PHASE_MARK(g_err_clock, 2);
   err_colsum_kernel<<<dim3((unsigned)((max_n + 63) / 64), (unsigned)count), 64, 0, st>>>(dtab);
+  CP_LAUNCHED("objective column sums");
+  CP_PHASE_MARK(g_err_clock, 3);
   err_final_kernel<<<count, 64, 0, st>>>(dtab, out);
-  CP_LAUNCHED("objective reduce");
+  CP_LAUNCHED("objective total");
+  CP_PHASE_MARK(g_err_clock, 4);
   return CP_OK;
 }
 
-int col_sums(const void* x, int x_dtype, int64_t nrow, int64_t n, int64_t row_step, int log_rms,
-             double* out, void* ws, size_t ws_bytes, hipStream_t st) {
-  if (!x || !out) return set_error(CP_ERR_ARG, "null x/out");
-  if (x_dtype != 0 && x_dtype != 1) return set_error(CP_ERR_ARG, "x_dtype must be 0 or 1");
-  if (nrow <= 0 || n <= 0 || n > (1 << 24) || row_step <= 0)
-    return set_error(CP_ERR_SHAPE, "x is [%lld, %lld], row_step %lld", (long long)nrow,
-                     (long long)n, (long long)row_step);
-  const int64_t nchunk = (nrow + row_step - 1) / row_step;
-  if (nchunk > 65535) return set_error(CP_ERR_SHAPE, "more than 65535 row chunks");
-  if (!ws || ws_bytes < (size_t)nchunk * n * 8)
-    return set_error(CP_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, (size_t)nchunk * n * 8);
-  if (!aligned(x, x_dtype ? 2 : 4) || !aligned(ws, 8) || !aligned(out, 8))
-    return set_error(CP_ERR_ALIGN, "misaligned buffer");
-  double* part = (double*)ws;
-  const dim3 grid((unsigned)((n + 63) / 64), (unsigned)nchunk);
-  if (x_dtype)
-    col_chunk_kernel<true><<<grid, 64, 0, st>>>(x, nrow, (int)n, row_step, part);
-  else
-    col_chunk_kernel<false><<<grid, 64, 0, st>>>(x, nrow, (int)n, row_step, part);
-  col_combine_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(part, nchunk, (int)n, nrow,
-                                                                   log_rms, out);
+constexpr int kColPerStore = 64;
+struct ColBatch {
+  ColDev t[kColPerStore];
+};
+static_assert(sizeof(ColBatch) <= 4000, "kernel argument block");
+static_assert(sizeof(ColDev) % 8 == 0, "table rows are whole 8-byte words");
+__global__ void col_store_kernel(ColBatch b, int cn, ColDev* __restrict__ dst) {
+  const int words = cn * (int)(sizeof(ColDev) / 8);
+  const uint64_t* s = reinterpret_cast<const uint64_t*>(b.t);
+  uint64_t* d = reinterpret_cast<uint64_t*>(dst);
+  for (int w = threadIdx.x; w < words; w += blockDim.x) d[w] = s[w];
+}
+
+size_t col_ws_bytes(const cp_col_tensor* ts, int count, int64_t row_step) {
+  size_t o = a256((size_t)count * sizeof(ColDev));
+  for (int i = 0; i < count; ++i)
+    o += a256((size_t)((ts[i].nrow + row_step - 1) / row_step) * (size_t)ts[i].n * 8);
+  return o;
+}
+
+int col_sums_batch(const cp_col_tensor* ts, int count, int64_t row_step, int log_rms, void* ws,
+                   size_t ws_bytes, hipStream_t st) {
+  if (!ts || count <= 0) return set_error(CP_ERR_ARG, "no tensors");
+  if (count > 65535) return set_error(CP_ERR_ARG, "at most 65535 tensors per call (got %d)", count);
+  if (row_step <= 0) return set_error(CP_ERR_SHAPE, "row_step %lld", (long long)row_step);
+  int64_t max_blocks = 0;
+  int max_n = 0;
+  for (int i = 0; i < count; ++i) {
+    const cp_col_tensor& t = ts[i];
+    if (!t.x || !t.out) return set_error(CP_ERR_ARG, "tensor %d: null x/out", i);
+    if (t.x_dtype != 0 && t.x_dtype != 1) return set_error(CP_ERR_ARG, "tensor %d: x_dtype must be 0 or 1", i);
+    if (t.nrow <= 0 || t.n <= 0 || t.n > (1 << 24))
+      return set_error(CP_ERR_SHAPE, "tensor %d: x is [%lld, %lld]", i, (long long)t.nrow, (long long)t.n);
+    const int64_t nchunk = (t.nrow + row_step - 1) / row_step;
+    const int64_t blocks = nchunk * ((t.n + 63) / 64);
+    if (nchunk > 0x7FFFFFFF || blocks > 0x7FFFFFFF) return set_error(CP_ERR_SHAPE, "tensor %d: too many row chunks", i);
+    if (!aligned(t.x, t.x_dtype ? 2 : 4) || !aligned(t.out, 8))
+      return set_error(CP_ERR_ALIGN, "tensor %d: misaligned buffer", i);
+    max_blocks = blocks > max_blocks ? blocks : max_blocks;
+    max_n = (int)t.n > max_n ? (int)t.n : max_n;
+  }
+  if (!ws || ws_bytes < col_ws_bytes(ts, count, row_step))
+    return set_error(CP_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, col_ws_bytes(ts, count, row_step));
+  if (!aligned(ws, 256)) return set_error(CP_ERR_ALIGN, "workspace needs 256-byte alignment");
+  char* base = (char*)ws;
+  ColDev* dtab = (ColDev*)base;
+  size_t o = a256((size_t)count * sizeof(ColDev));
+  std::vector<ColDev> devs(count);
+  bool any16 = false, any32 = false;
+  for (int i = 0; i < count; ++i) {
+    const cp_col_tensor& t = ts[i];
+    const int nchunk = (int)((t.nrow + row_step - 1) / row_step);
+    devs[i] = ColDev{t.x, (double*)(base + o), t.out, t.nrow, (int)t.n, t.x_dtype, nchunk,
+                     (int)((t.n + 63) / 64)};
+    o += a256((size_t)nchunk * (size_t)t.n * 8);
+    (t.x_dtype ? any16 : any32) = true;
+  }
+  // one table per input dtype: f16 rows first, then f32
+  std::stable_partition(devs.begin(), devs.end(), [](const ColDev& d) { return d.x_f16 != 0; });
+  int n16 = 0;
+  for (const ColDev& d : devs) n16 += d.x_f16 != 0;
+  for (int c0 = 0; c0 < count; c0 += kColPerStore) {
+    const int cn = count - c0 < kColPerStore ? count - c0 : kColPerStore;
+    ColBatch b;
+    for (int i = 0; i < cn; ++i) b.t[i] = devs[c0 + i];
+    col_store_kernel<<<1, 256, 0, st>>>(b, cn, dtab + c0);
+  }
+  if (any16)
+    col_chunk_kernel<true><<<dim3((unsigned)max_blocks, (unsigned)n16), 64, 0, st>>>(dtab, row_step);
+  if (any32)
+    col_chunk_kernel<false><<<dim3((unsigned)max_blocks, (unsigned)(count - n16)), 64, 0, st>>>(
+        dtab + n16, row_step);
+  col_combine_kernel<<<dim3((unsigned)((max_n + 255) / 256), (unsigned)count), 256, 0, st>>>(dtab, log_rms);
   CP_LAUNCHED("column sums");
   return CP_OK;
 }
@@ -483,21 +605,46 @@ int cp_tensor_err_batch(const cp_err_tensor* tensors, int count, void* ws, size_
   return cp::err_batch(tensors, count, ws, ws_bytes, out, (hipStream_t)stream);
 }
 
+void cp_err_profile(int enable) { cp::g_err_clock.on = enable != 0; }
+
+int cp_err_phase_ms(float* out, int nphase) {
+  cp::clear_error();
+  if (!out || nphase <= 0) return cp::set_error(CP_ERR_ARG, "bad phase buffer");
+  hipError_t r = cp::g_err_clock.read(out, nphase);
+  if (r != hipSuccess) return cp::hip_fail(r, "phase events");
+  return nphase < 5 ? nphase : 5;
+}
+
 size_t cp_col_sums_ws_bytes(int64_t nrow, int64_t n, int64_t row_step) {
   if (nrow <= 0 || n <= 0 || row_step <= 0) return 0;
-  return (size_t)((nrow + row_step - 1) / row_step) * (size_t)n * 8;
+  const cp_col_tensor t{nullptr, 0, nrow, n, nullptr};
+  return cp::col_ws_bytes(&t, 1, row_step);
 }
 
 int cp_col_sq_sums(const void* x, int x_dtype, int64_t nrow, int64_t n, int64_t row_step,
                    double* acc, void* ws, size_t ws_bytes, void* stream) {
   cp::clear_error();
-  return cp::col_sums(x, x_dtype, nrow, n, row_step, 0, acc, ws, ws_bytes, (hipStream_t)stream);
+  const cp_col_tensor t{x, x_dtype, nrow, n, acc};
+  return cp::col_sums_batch(&t, 1, row_step, 0, ws, ws_bytes, (hipStream_t)stream);
 }
 
 int cp_col_log_rms(const void* x, int x_dtype, int64_t nrow, int64_t n, int64_t row_step,
                    double* out, void* ws, size_t ws_bytes, void* stream) {
   cp::clear_error();
-  return cp::col_sums(x, x_dtype, nrow, n, row_step, 1, out, ws, ws_bytes, (hipStream_t)stream);
+  const cp_col_tensor t{x, x_dtype, nrow, n, out};
+  return cp::col_sums_batch(&t, 1, row_step, 1, ws, ws_bytes, (hipStream_t)stream);
+}
+
+size_t cp_col_sums_batch_ws_bytes(const cp_col_tensor* tensors, int count, int64_t row_step) {
+  if (!tensors || count <= 0 || row_step <= 0) return 0;
+  return cp::col_ws_bytes(tensors, count, row_step);
+}
+
+int cp_col_sq_sums_batch(const cp_col_tensor* tensors, int count, int64_t row_step, int log_rms,
+                         void* ws, size_t ws_bytes, void* stream) {
+  cp::clear_error();
+  return cp::col_sums_batch(tensors, count, row_step, log_rms != 0, ws, ws_bytes,
+                            (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -31,6 +31,23 @@ def sample_rows(nrow, rows_sample, seed=0):
     return None
 
 
+_SAMPLES = {}
+
+
+def _sample_dev(nrow, rows_sample, seed, device):
+    """Device int32 copy of sample_rows (drawn once per (nrow, rows_sample, seed))."""
+    if not (rows_sample and nrow > rows_sample):
+        return None
+    key = (int(nrow), int(rows_sample), int(seed), str(device))
+    t = _SAMPLES.get(key)
+    if t is None:
+        if len(_SAMPLES) > 64:
+            _SAMPLES.clear()
+        idx = sample_rows(nrow, rows_sample, seed)
+        t = _SAMPLES[key] = torch.from_numpy(idx.astype(np.int32)).to(device)
+    return t
+
+
 def weights_dev(x):
     """(contiguous device tensor of float16 or float32, x_dtype code 1 / 0)."""
     if isinstance(x, torch.Tensor):
@@ -44,19 +61,24 @@ def weights_dev(x):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda(), 1 if a.dtype == np.float16 else 0
 
 
-def _index_dev(p, n, what):
+def index_dev(p, n, what="perm"):
+    """A column index as a device int32 tensor. Host arrays are range-checked here
+    (IndexError, as numpy's fancy indexing raises); device tensors are checked by the
+    kernels, which never dereference an index out of range and report it (the
+    result comes back NaN and tensor_err_many raises IndexError). Negative indices
+    count from the end in both cases."""
     if isinstance(p, torch.Tensor):
-        t = p.to(device="cuda", dtype=torch.int32).reshape(-1)
-        lo, hi = (int(v) for v in torch.aminmax(t)) if t.numel() else (0, 0)
+        t = p.reshape(-1)
+        if not (t.is_cuda and t.dtype == torch.int32):
+            t = t.to(device="cuda", dtype=torch.int32)
     else:
         a = np.asarray(p).reshape(-1)
-        lo, hi = (int(a.min()), int(a.max())) if a.size else (0, 0)
+        if a.size and (int(a.min()) < -n or int(a.max()) >= n):
+            raise IndexError(f"{what} index out of range for {n} columns")
         t = torch.from_numpy(a.astype(np.int32)).cuda()
     if t.numel() != n:
         raise ValueError(f"{what} has {t.numel()} entries for {n} columns")
-    if lo < -n or hi >= n:
-        raise IndexError(f"{what} index out of range for {n} columns")
-    return torch.where(t < 0, t + n, t)  # numpy's negative indices
+    return t.contiguous()
 
 
 def _vec_dev(v, n, dtype, what):
@@ -89,9 +111,8 @@ def tensor_err_many(items):
         if n % bw:
             exc = AssertionError if tt == "Q2_K" else ValueError
             raise exc(f"row length {n} is not a multiple of {bw}")
-        idx = sample_rows(nrow, it.get("rows_sample"), it.get("seed", 0))
-        rows = torch.from_numpy(idx.astype(np.int32)).cuda() if idx is not None else None
-        perm = _index_dev(it["perm"], n, "perm") if it.get("perm") is not None else None
+        rows = _sample_dev(nrow, it.get("rows_sample"), it.get("seed", 0), xd.device)
+        perm = index_dev(it["perm"], n, "perm") if it.get("perm") is not None else None
         qw = it.get("qw")
         # Q8_0's codec ignores qw; the error is still weighted by it (objective.py:37-38)
         qd = _vec_dev(qw, n, torch.float32, "qw") if qw is not None else None
@@ -106,7 +127,7 @@ def tensor_err_many(items):
                                       perm.data_ptr() if perm is not None else None,
                                       wd.data_ptr() if wd is not None else None,
                                       rows.data_ptr() if rows is not None else None,
-                                      len(idx) if idx is not None else 0))
+                                      rows.numel() if rows is not None else 0))
         slots.append(k)
     if not structs:
         return out_vals
@@ -132,17 +153,37 @@ def tensor_err(x, ttype, qw, perm=None, wvec=None, rows_sample=None, seed=0):
                                  rows_sample=rows_sample, seed=seed)])[0]
 
 
-def col_sq_sums(x, row_step=32768):
-    """Device float64 [n]: per-column sums of squares in row chunks of row_step
-    (objective.py:44-48), bit-identical to the reference's accumulator."""
+def col_sq_sums_many(xs, row_step=32768):
+    """Device float64 [n] per tensor: per-column sums of squares in row chunks of
+    row_step (objective.py:44-48), bit-identical to the reference's accumulator,
+    all tensors in one pass."""
     lib = _lib.load()
-    xd, code = weights_dev(x)
-    nrow, n = xd.shape
-    ws = _lib.workspace(lib.cp_col_sums_ws_bytes(nrow, n, row_step), xd.device)
-    acc = torch.empty(n, dtype=torch.float64, device=xd.device)
-    _lib.check(lib.cp_col_sq_sums(_lib.ptr(xd), code, nrow, n, row_step, _lib.ptr(acc),
-                                  _lib.ptr(ws), ws.numel(), _lib.stream_ptr()))
-    return acc
+    devs = [weights_dev(x) for x in xs]
+    outs = [torch.empty(xd.shape[1], dtype=torch.float64, device=xd.device) for xd, _ in devs]
+    structs = [_lib.ColTensor(xd.data_ptr(), code, xd.shape[0], xd.shape[1], o.data_ptr())
+               for (xd, code), o in zip(devs, outs)]
+    arr = (_lib.ColTensor * len(structs))(*structs)
+    ws = _lib.workspace(lib.cp_col_sums_batch_ws_bytes(arr, len(structs), row_step),
+                        devs[0][0].device)
+    _lib.check(lib.cp_col_sq_sums_batch(arr, len(structs), row_step, 0, _lib.ptr(ws), ws.numel(),
+                                        _lib.stream_ptr()))
+    return outs
+
+
+def col_sq_sums(x, row_step=32768):
+    return col_sq_sums_many([x], row_step)[0]
+
+
+def col_log_rms_many(xs, row_step=32768):
+    """col_log_rms of every tensor, the sums in one GPU pass (numpy arrays out)."""
+    accs = col_sq_sums_many(xs, row_step)
+    flat = torch.cat(accs).cpu().numpy()
+    out, o = [], 0
+    for x, a in zip(xs, accs):
+        acc = flat[o:o + a.numel()]
+        o += a.numel()
+        out.append(np.log(np.sqrt(acc / x.shape[0]) + 1e-12))
+    return out
 
 
 def col_log_rms(x, row_step=32768):
@@ -150,6 +191,4 @@ def col_log_rms(x, row_step=32768):
     array. The O(nrow x n) sums run on the GPU; the final n-element
     log(sqrt(acc / nrow) + 1e-12) is the host libm's, as in the reference, so the
     profile (a sort key) is bit-identical."""
-    nrow = x.shape[0]
-    acc = col_sq_sums(x, row_step).cpu().numpy()
-    return np.log(np.sqrt(acc / nrow) + 1e-12)
+    return col_log_rms_many([x], row_step)[0]

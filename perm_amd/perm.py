@@ -185,19 +185,22 @@ def optimize(weights, ttypes, qws, dims, rows_sample=16384, log=print):
     Returns (perms, report) with the reference's keys (report adds "key", the chosen
     residual candidate)."""
     import time
-    from .objective import col_log_rms, tensor_err_many, weights_dev
+    from .objective import col_log_rms_many, index_dev, tensor_err_many, weights_dev
     t0 = time.time()
     dev = {n: weights_dev(w)[0] for n, w in weights.items()}
+    qdev = {n: torch.from_numpy(np.ascontiguousarray(q, dtype=np.float32)).cuda()
+            if str(getattr(q, "dtype", "")) == "float32" else q for n, q in qws.items()}
     res_names = res_space_tensors(dev, dims)
 
     def res_obj(perm):
+        pd = index_dev(perm, dims["d_model"]) if perm is not None else None
         return _ordered_sum(tensor_err_many(
-            [dict(x=dev[n], ttype=ttypes[n], qw=qws.get(n), perm=perm, rows_sample=rows_sample)
+            [dict(x=dev[n], ttype=ttypes[n], qw=qdev.get(n), perm=pd, rows_sample=rows_sample)
              for n in res_names]))
 
     base = res_obj(None)
     res_perm, res_val, res_name = np.arange(dims["d_model"]), base, "identity"
-    profiles = {n: col_log_rms(dev[n]) for n in res_names}
+    profiles = dict(zip(res_names, col_log_rms_many([dev[n] for n in res_names])))
     for kname, key in build_res_keys(dev, dims, profiles).items():
         perm = np.argsort(key, kind="stable")
         val = res_obj(perm)
@@ -211,10 +214,10 @@ def optimize(weights, ttypes, qws, dims, rows_sample=16384, log=print):
     group = nh // nkv
     fns = [f"blk.{l}.ffn_down.weight" for l in range(L)]
     ons = [f"blk.{l}.attn_output.weight" for l in range(L)]
-    fcand = [np.argsort(col_log_rms(dev[fn]), kind="stable") for fn in fns]
+    profs = col_log_rms_many([dev[fn] for fn in fns] + [dev[on] for on in ons])
+    fcand = [np.argsort(p, kind="stable") for p in profs[:L]]
     heads_all, ocand = [], []
-    for on in ons:
-        prof = col_log_rms(dev[on])  # column sums are per column: slices share them
+    for on, prof in zip(ons, profs[L:]):  # column sums are per column: slices share them
         heads = []
         for h in range(nkv):
             key = np.zeros(hd)
@@ -227,10 +230,10 @@ def optimize(weights, ttypes, qws, dims, rows_sample=16384, log=print):
         heads_all.append(heads)
         ocand.append(full)
     errs = tensor_err_many(
-        [dict(x=dev[fn], ttype=ttypes[fn], qw=qws.get(fn)) for fn in fns]
-        + [dict(x=dev[fn], ttype=ttypes[fn], qw=qws.get(fn), perm=p) for fn, p in zip(fns, fcand)]
-        + [dict(x=dev[on], ttype=ttypes[on], qw=qws.get(on)) for on in ons]
-        + [dict(x=dev[on], ttype=ttypes[on], qw=qws.get(on), perm=p) for on, p in zip(ons, ocand)])
+        [dict(x=dev[fn], ttype=ttypes[fn], qw=qdev.get(fn)) for fn in fns]
+        + [dict(x=dev[fn], ttype=ttypes[fn], qw=qdev.get(fn), perm=p) for fn, p in zip(fns, fcand)]
+        + [dict(x=dev[on], ttype=ttypes[on], qw=qdev.get(on)) for on in ons]
+        + [dict(x=dev[on], ttype=ttypes[on], qw=qdev.get(on), perm=p) for on, p in zip(ons, ocand)])
     fb_all, fv_all = errs[0:L], errs[L:2 * L]
     ob_all, ov_all = errs[2 * L:3 * L], errs[3 * L:4 * L]
     ffn_perms, ffn_val, ffn_base = [], 0.0, 0.0

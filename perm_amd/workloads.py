@@ -67,3 +67,57 @@ def qwen3_layer_weights(layer, seed=0, device="cuda"):
     g.manual_seed(seed * 1000 + layer)
     return {name: torch.randn((rows, n), generator=g, device=device) * 0.02
             for name, rows, n, _fam in QWEN3_06B_LAYER}
+
+
+QWEN3_06B_DIMS = {"d_model": 1024, "d_ffn": 3072, "n_layers": 28, "n_heads": 16, "n_kv": 8,
+                  "head_dim": 128}
+QWEN3_06B_VOCAB = 151936
+
+
+def qwen3_gguf_weights(layers=QWEN3_06B_LAYERS, seed=0, device="cuda"):
+    """Random-init float16 weights of the Qwen3-0.6B linear set under their GGUF names
+    (token_embd [151936, 1024] plus 7 tensors per layer, [out, in]), for the PERM
+    search. Entries are N(0, 0.02^2) times a per-input-channel log-normal(sigma 0.5)
+    scale shared by every tensor reading the same space (the residual stream, each
+    layer's FFN intermediate and attention value space), so the channel profiles the
+    search sorts by are not flat."""
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+
+    def scale(n):
+        return torch.exp(0.5 * torch.randn((n,), generator=g, device=device))
+
+    def mat(rows, n, s):
+        return (torch.randn((rows, n), generator=g, device=device) * 0.02 * s).to(torch.float16)
+
+    res = scale(1024)
+    w = {"token_embd.weight": mat(QWEN3_06B_VOCAB, 1024, res)}
+    for l in range(layers):
+        ffn, vo = scale(3072), scale(2048)
+        for name, rows, n, fam in QWEN3_06B_LAYER:
+            s = {"qkv_in": res, "gateup_in": res, "down_in": ffn, "o_in": vo}[fam]
+            w[f"blk.{l}.{name}.weight"] = mat(rows, n, s)
+    return w
+
+
+def qwen3_mixed_typemap(names):
+    """The mixed container of the tied-output workload: Q6_K for the token
+    embedding / output matrix, Q3_K for attention, Q2_K elsewhere."""
+    out = {}
+    for n in names:
+        if n in ("token_embd.weight", "output.weight"):
+            out[n] = "Q6_K"
+        elif ".attn_" in n:
+            out[n] = "Q3_K"
+        else:
+            out[n] = "Q2_K"
+    return out
+
+
+def imatrix_means(weights, seed=0):
+    """imatrix-style importance vectors (positive per-input-channel means) for every
+    tensor except the token embedding / output, which llama.cpp quantizes unweighted."""
+    rng = np.random.default_rng(seed)
+    return {n: (np.abs(rng.standard_normal(w.shape[1])) + 0.1).astype(F32)
+            for n, w in weights.items() if n not in ("token_embd.weight", "output.weight")}
