@@ -156,6 +156,23 @@ int cp_ef_phase_ms(float* out, int nphase);
  * not fixed (split-K partials are added with float32 atomics). */
 int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, float* H, void* stream);
 
+/* ---- Hessian storage (coldpress/hessians.py:163-243) ---- */
+
+/* Pack a float32 [n, n] Hessian for storage: diag32 = diag(H) (float32, exact);
+ * hscale[0] = max|H| / 32768 when max|H| > 32768, else 1; H16 = float16(H / hscale)
+ * rounded to nearest even. Output pointers are device pointers; ws holds 4 bytes.
+ * Replaces the arithmetic of hessians.save_hessians (coldpress/hessians.py:180-194);
+ * the npz write stays with the caller. Bit-exact. */
+int cp_h2_pack(const float* H, int64_t n, uint16_t* H16, float* diag32, float* hscale,
+               void* ws, size_t ws_bytes, void* stream);
+
+/* Expand a stored Hessian to float64: H = double(Hs) * hscale, then the diagonal
+ * overwritten with diag32 when given. Hs is float16 (in_dtype 1) or float32 (0, the
+ * older format). Replaces the arithmetic of hessians.load_hessian
+ * (coldpress/hessians.py:225-243). Bit-exact. */
+int cp_h2_expand(const void* Hs, int in_dtype, int64_t n, double hscale, const float* diag32,
+                 double* H, void* stream);
+
 /* ---- PERM channel permutations (coldpress/perm/spacemaps/qwen3.py, ef.py:289-290) ---- */
 
 /* dst[r][c] = src[row_perm[r]][col_perm[c]] for a row-major [rows, cols] matrix of

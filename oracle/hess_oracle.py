@@ -5,6 +5,12 @@ coldpress/hessians.py:137-154 accumulates, per hooked Linear and per batch,
 oracle is the float64 closed form of the same sum (the parity gate is 1e-5
 relative Frobenius, which float32 accumulation of any order meets by a wide
 margin at the batch sizes used here).
+
+h2_pack / h2_expand restate the storage arithmetic of hessians.py:163-243. Pins: the
+expectations of the reference's own storage tests (test_hessian_fp16.py: exact diagonal,
+off-diagonal equal to float16(float32(H)) when unscaled and within float16 epsilon, finite
+storage of a Hessian far above the float16 range, the float32-only format unchanged), which
+tests/test_oracle_gguf.py restates.
 """
 import numpy as np
 
@@ -31,3 +37,30 @@ def rel_fro(A, B):
     A = np.asarray(A, dtype=np.float64)
     B = np.asarray(B, dtype=np.float64)
     return float(np.linalg.norm(A - B) / np.linalg.norm(B))
+
+
+# ------------------------------------------------------------------ H2 storage
+# hessians.py:163-243: float16 off-diagonal over a per-matrix scale, exact float32 diagonal.
+
+FP16_SAFE_MAX = 32768.0
+
+
+def h2_pack(H):
+    """(H16, diag32, hscale) of the stored form (hessians.py:180-194)."""
+    H = np.asarray(H, dtype=np.float32)
+    diag32 = np.ascontiguousarray(np.diag(H)).astype(np.float32)
+    amax = float(np.max(np.abs(H))) if H.size else 0.0
+    hscale = amax / FP16_SAFE_MAX if amax > FP16_SAFE_MAX else 1.0
+    H16 = (H / np.float32(hscale)).astype(np.float16)
+    return H16, diag32, np.float32(hscale)
+
+
+def h2_expand(H16, hscale=None, diag32=None):
+    """float64 H from the stored form (hessians.py:234-241); hscale / diag32 None for the
+    older formats."""
+    H = np.asarray(H16).astype(np.float64)
+    if hscale is not None:
+        H *= float(hscale)
+    if diag32 is not None:
+        np.fill_diagonal(H, np.asarray(diag32).astype(np.float64))
+    return H

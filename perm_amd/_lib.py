@@ -74,6 +74,8 @@ SIGNATURES = {
     "cp_ef_profile": (None, [_i32]),
     "cp_ef_phase_ms": (_i32, [_vp, _i32]),
     "cp_permute_gather": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
+    "cp_h2_pack": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "cp_h2_expand": (_i32, [_vp, _i32, _i64, _f64, _vp, _vp, _vp]),
     "cp_tensor_err_ws_bytes": (_sz, [_err_p, _i32]),
     "cp_tensor_err_batch": (_i32, [_err_p, _i32, _vp, _sz, _vp, _vp]),
     "cp_err_profile": (None, [_i32]),

@@ -1,0 +1,116 @@
+// Hessian storage format on gfx950 (coldpress/hessians.py:163-243): H is kept as
+// float16 off-diagonal values over a per-matrix scale, with the diagonal exact in
+// float32.
+//
+// pack    amax = max |H| (order-free, exact); hscale = amax / 32768 when amax > 32768,
+//         else 1 -- 32768 is a power of two, so amax * 2^-15 is exact in float32;
+//         H16 = f16(H / hscale) with a correctly rounded float32 division and
+//         round-to-nearest-even to f16 (numpy's astype); diag32 = diag(H).
+// expand  H = double(H16) * double(hscale) (exact: 11 + 24 significant bits), then the
+//         float32 diagonal written over it; a float32 H (the older format) is widened.
+// Both are HBM-bound elementwise passes (pack: 4 B in, 2 B out per entry; expand:
+// 2 or 4 B in, 8 B out).
+#include <hip/hip_runtime.h>
+
+#include "cp_device.h"
+#include "cp_host.h"
+
+namespace cp {
+
+constexpr float kFp16SafeMax = 32768.0f;
+
+// max |x| over the matrix: non-negative floats order like their bit patterns, so an
+// unsigned atomic max on the bits is exact and order-free. amax_bits starts at 0.
+__global__ __launch_bounds__(256) void h2_absmax_kernel(const float* __restrict__ H, int64_t count,
+                                                        unsigned* __restrict__ amax_bits) {
+  unsigned m = 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * 256) {
+    const unsigned b = __float_as_uint(H[i]) & 0x7FFFFFFFu;
+    m = b > m ? b : m;
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    const unsigned v = __shfl_xor(m, o);
+    m = v > m ? v : m;
+  }
+  if ((threadIdx.x & 63) == 0) atomicMax(amax_bits, m);
+}
+
+__global__ void h2_clear_kernel(unsigned* __restrict__ p) { *p = 0u; }
+
+__global__ __launch_bounds__(256) void h2_pack_kernel(const float* __restrict__ H, int64_t n,
+                                                      const unsigned* __restrict__ amax_bits,
+                                                      uint16_t* __restrict__ H16,
+                                                      float* __restrict__ diag32,
+                                                      float* __restrict__ hscale_out) {
+  const float amax = __uint_as_float(*amax_bits);
+  const float hs = amax > kFp16SafeMax ? amax * (1.0f / kFp16SafeMax) : 1.0f;
+  const int64_t count = n * n;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i == 0) *hscale_out = hs;
+  if (i >= count) return;
+  const float v = H[i];
+  H16[i] = half_bits(v / hs);
+  const int64_t r = i / n;
+  if (i == r * n + r) diag32[r] = v;
+}
+
+template <bool F16>
+__global__ __launch_bounds__(256) void h2_expand_kernel(const void* __restrict__ Hs, int64_t n,
+                                                        double hscale,
+                                                        const float* __restrict__ diag32,
+                                                        double* __restrict__ H) {
+  const int64_t count = n * n;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  double v = F16 ? (double)half_value(reinterpret_cast<const uint16_t*>(Hs)[i])
+                 : (double)reinterpret_cast<const float*>(Hs)[i];
+  v = v * hscale;
+  const int64_t r = i / n;
+  if (diag32 && i == r * n + r) v = (double)diag32[r];
+  H[i] = v;
+}
+
+}  // namespace cp
+
+extern "C" {
+
+int cp_h2_pack(const float* H, int64_t n, uint16_t* H16, float* diag32, float* hscale,
+               void* ws, size_t ws_bytes, void* stream) {
+  cp::clear_error();
+  if (!H || !H16 || !diag32 || !hscale) return cp::set_error(CP_ERR_ARG, "null pointer");
+  if (n <= 0 || n > (1 << 19)) return cp::set_error(CP_ERR_SHAPE, "bad size %lld", (long long)n);
+  if (!ws || ws_bytes < 4) return cp::set_error(CP_ERR_WORKSPACE, "workspace %zu < 4 bytes", ws_bytes);
+  if (!cp::aligned(H, 4) || !cp::aligned(H16, 2) || !cp::aligned(diag32, 4) ||
+      !cp::aligned(hscale, 4) || !cp::aligned(ws, 4))
+    return cp::set_error(CP_ERR_ALIGN, "misaligned buffer");
+  hipStream_t st = (hipStream_t)stream;
+  unsigned* amax = (unsigned*)ws;
+  const int64_t count = n * n;
+  cp::h2_clear_kernel<<<1, 1, 0, st>>>(amax);
+  const int64_t blocks = (count + 255) / 256;
+  cp::h2_absmax_kernel<<<(unsigned)(blocks < 4096 ? blocks : 4096), 256, 0, st>>>(H, count, amax);
+  cp::h2_pack_kernel<<<(unsigned)blocks, 256, 0, st>>>(H, n, amax, H16, diag32, hscale);
+  CP_LAUNCHED("Hessian pack");
+  return CP_OK;
+}
+
+int cp_h2_expand(const void* Hs, int in_dtype, int64_t n, double hscale, const float* diag32,
+                 double* H, void* stream) {
+  cp::clear_error();
+  if (!Hs || !H) return cp::set_error(CP_ERR_ARG, "null pointer");
+  if (in_dtype != 0 && in_dtype != 1) return cp::set_error(CP_ERR_ARG, "in_dtype must be 0 or 1");
+  if (n <= 0 || n > (1 << 19)) return cp::set_error(CP_ERR_SHAPE, "bad size %lld", (long long)n);
+  if (!cp::aligned(Hs, in_dtype ? 2 : 4) || !cp::aligned(H, 8) || (diag32 && !cp::aligned(diag32, 4)))
+    return cp::set_error(CP_ERR_ALIGN, "misaligned buffer");
+  hipStream_t st = (hipStream_t)stream;
+  const unsigned blocks = (unsigned)((n * n + 255) / 256);
+  if (in_dtype)
+    cp::h2_expand_kernel<true><<<blocks, 256, 0, st>>>(Hs, n, hscale, diag32, H);
+  else
+    cp::h2_expand_kernel<false><<<blocks, 256, 0, st>>>(Hs, n, hscale, diag32, H);
+  CP_LAUNCHED("Hessian expand");
+  return CP_OK;
+}
+
+}  // extern "C"

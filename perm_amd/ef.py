@@ -250,3 +250,171 @@ def ef_encode_many(tensors, n_iter=2, damp=0.01, act_order=True, mode="exact"):
         for t, o in zip(mine, r):
             out[t["name"]] = o
     return {t["name"]: out[t["name"]] for t in tensors}
+
+
+# ---------------------------------------------------------------- GGUF driver
+
+def _weights_f32(t):
+    """A GGUF tensor's data [rows, ne0] as a float32 CUDA tensor (F32 / F16 / BF16)."""
+    a = np.array(t.data)  # a private host copy of the mapped file's bytes
+    name = t.tensor_type.name
+    if name == "F32":
+        return torch.from_numpy(a).cuda()
+    if name == "F16":
+        return torch.from_numpy(a).cuda().to(torch.float32)
+    if name == "BF16":  # uint16 bit patterns: the float32 with those high 16 bits
+        b = torch.from_numpy(a.astype(np.int32)).cuda()
+        return (b << 16).view(torch.float32)
+    raise ValueError(f"{t.name}: source weights of type {name} are not float")
+
+
+def _stat_err(recon, x, w):
+    """float((((recon - x) ** 2) * w).sum()) of coldpress/ef.py:299-300: the float32
+    terms, summed in float64 (diagnostic; within ~1e-6 relative of the reference's float32
+    pairwise total)."""
+    d = recon - x
+    return float(((d * d) * w).to(torch.float64).sum().item())
+
+
+def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, perms=None,
+                spacemap=None, dims=None, acknowledge_unreviewed=False, only="all", n_iter=2,
+                unsafe_storage_order=False, device="cuda", log=print, layers_per_pass=4):
+    """EF-encode every quantized tensor of ``target_path`` (a stock quant artifact) from the
+    float weights of ``f16_path`` and the Hessians in ``hessdir``, and write a byte-map
+    clone of the target to ``out_path`` (coldpress/ef.py:223-317).
+
+    Per tensor, as the reference: token_embd takes weighted RTN with the layer-0 attention
+    input diagonal (diag(H)/n) as column weights; a tensor with a stored Hessian takes EF
+    (act order unless ``unsafe_storage_order``); any other takes weighted RTN with its
+    imatrix means. With ``perms`` and a ``spacemap`` (an object with the reference's
+    ``input_perm(name, perms, dims, ...)``, or "qwen3" for perm_amd.perm), the imatrix
+    vectors and Hessians (stored in the original order) are permuted to the already
+    permuted weights. Every codec, factorization and sweep runs on the GPU; EF tensors go
+    through ef_encode_many ``layers_per_pass`` blocks at a time, and tensors whose stored
+    Hessians are identical (q/k/v, gate/up) share one factorization. Writes the per-tensor
+    statistics to ``out_path + ".efstats.json"`` and returns them."""
+    import hashlib
+    import json
+    import time
+    from . import hessians as hess
+    from . import kquant as gkq
+    from .ggufio import GGUFReader, load_imatrix_means, reemit
+
+    if device not in ("cuda", "gpu") and not str(device).startswith("cuda"):
+        raise ValueError(f"device {device!r}: this backend runs on the GPU only")
+    if spacemap == "qwen3":
+        from . import perm as spacemap
+    imat = load_imatrix_means(imatrix_path) if imatrix_path else {}
+    f16 = {t.name: t for t in GGUFReader(f16_path).tensors}
+    tr = GGUFReader(target_path)
+    targets = [(t.name, t.tensor_type.name, t) for t in tr.tensors
+               if t.tensor_type.name in gkq.QUANTIZE]
+    unsupported = [(t.name, t.tensor_type.name) for t in tr.tensors
+                   if t.tensor_type.name not in gkq.QUANTIZE
+                   and t.tensor_type.name not in ("F16", "F32", "BF16")]
+    if unsupported:
+        raise ValueError(f"target has types we cannot encode: {unsupported}")
+    ack = {"acknowledge_unreviewed": acknowledge_unreviewed} if acknowledge_unreviewed else {}
+
+    def input_perm(name):
+        if perms is None or spacemap is None:
+            return None
+        p = spacemap.input_perm(name, perms, dims, **ack)
+        return None if p is None else np.asarray(p)
+
+    H_cache = {}
+
+    def hessian(name):
+        """Device float64 H of a tensor, shared between tensors with identical files."""
+        path = hess.hessian_path(hessdir, name)
+        with np.load(path) as z:
+            digest = hashlib.sha1()
+            for k in sorted(z.files):
+                if k != "name":
+                    digest.update(k.encode())
+                    digest.update(np.ascontiguousarray(z[k]).tobytes())
+        key = digest.hexdigest()
+        if key not in H_cache:
+            H_cache[key] = hess.load_hessian(hessdir, name, device="cuda")
+        return H_cache[key]
+
+    selected = []
+    for name, tt, t in targets:
+        is_embdout = name in ("token_embd.weight", "output.weight")
+        if (only == "blk" and is_embdout) or (only == "embdout" and not is_embdout):
+            continue
+        if name not in f16:
+            raise KeyError(f"{name}: absent from {f16_path}")
+        if list(f16[name].shape) != list(t.shape):
+            raise ValueError(f"{name}: f16 shape {f16[name].shape} != target {t.shape}")
+        selected.append((name, tt))
+
+    def block_of(name):
+        return int(name.split(".")[1]) if name.startswith("blk.") else -1
+
+    replace, stats = {}, {}
+    t_start = time.time()
+    groups = {}
+    for name, tt in selected:
+        groups.setdefault(max(block_of(name), 0) // max(layers_per_pass, 1), []).append((name, tt))
+    done = 0
+    for gkey in sorted(groups):
+        t0 = time.time()
+        ef_items, work = [], []
+        for name, tt in groups[gkey]:
+            x = _weights_f32(f16[name])
+            qw = imat.get(name)
+            p = input_perm(name)
+            if qw is not None and p is not None:
+                qw = qw[p]  # imatrix stats in original order; x is already permuted
+            qd = torch.from_numpy(np.ascontiguousarray(qw, dtype=np.float32)).cuda() \
+                if qw is not None else None
+            if name == "token_embd.weight":
+                H0, n0 = hess.load_hessian(hessdir, "blk.0.attn_q.weight", device="cuda")
+                w_embd = (torch.diagonal(H0) / max(n0, 1)).to(torch.float32)
+                if p is not None:
+                    w_embd = w_embd[torch.from_numpy(p).cuda()]
+                w_embd = w_embd.contiguous()
+                raw = gkq.quantize_dev(tt, x, w_embd)
+                work.append((name, tt, x, qd, raw, gkq.dequantize_dev(tt, raw, x.shape[1]),
+                             "wRTN(attn0-diag)"))
+            elif hess.has_hessian(hessdir, name):
+                H, _n = hessian(name)
+                if p is not None:
+                    from .perm import permute_hessian
+                    key = ("perm", id(H), p.tobytes())
+                    if key not in H_cache:
+                        H_cache[key] = (permute_hessian(H, p), _n)
+                    H = H_cache[key][0]
+                ef_items.append({"name": name, "ttype": tt, "x": x, "qw": qd, "H": H})
+                work.append((name, tt, x, qd, None, None,
+                             "EF" if not unsafe_storage_order else "EF(storage-order)"))
+            else:
+                raw = gkq.quantize_dev(tt, x, qd)
+                work.append((name, tt, x, qd, raw, gkq.dequantize_dev(tt, raw, x.shape[1]), "wRTN"))
+        res = ef_encode_many(ef_items, n_iter=n_iter, act_order=not unsafe_storage_order) \
+            if ef_items else {}
+        sec = (time.time() - t0) / max(len(work), 1)
+        for name, tt, x, qd, raw, recon, mode in work:
+            if raw is None:
+                raw, recon = res[name]
+            base = gkq.dequantize_dev(tt, gkq.quantize_dev(tt, x, qd), x.shape[1])
+            w = qd if qd is not None else torch.ones(x.shape[1], dtype=torch.float32,
+                                                      device=x.device)
+            e_base, e_ours = _stat_err(base, x, w), _stat_err(recon, x, w)
+            stats[name] = {"type": tt, "mode": mode,
+                           "rel_err_vs_stock": e_ours / e_base - 1 if e_base else 0.0,
+                           "sec": sec}
+            replace[name] = raw.reshape(-1).cpu().numpy()
+            done += 1
+            if done % 20 == 0 or name in ("token_embd.weight", "output.weight"):
+                log(f"[{done}/{len(selected)}] {name} {tt} {mode} "
+                    f"err-vs-stock {stats[name]['rel_err_vs_stock'] * 100:+.1f}%")
+        H_cache.clear()  # a layer group's Hessians are not read by later groups
+    reemit(target_path, out_path, replace=replace, log=log)
+    if stats:
+        med = float(np.median([s["rel_err_vs_stock"] for s in stats.values()]))
+        log(f"median err-vs-stock: {med * 100:+.2f}%; total {(time.time() - t_start) / 60:.1f} min")
+    with open(out_path + ".efstats.json", "w") as f:
+        json.dump(stats, f, indent=1)
+    return stats

@@ -9,10 +9,25 @@ accumulation -- no upcast copy, no device-to-host copy per batch.
 
 Module -> GGUF tensor naming (the reference uses gguf's TensorNameMap, a package
 not present here) is supplied by the caller as ``name_map``.
+
+Storage (coldpress/hessians.py:163-243): ``save_hessians`` writes the reference's npz
+format (float16 H over a per-matrix ``hscale``, exact float32 ``diag32``, ``n``, ``name``),
+with the packing arithmetic on the GPU (cp_h2_pack); ``load_hessian`` reads the same files
+(and the older float32-only ones) and rebuilds the float64 matrix on the GPU (cp_h2_expand).
 """
+import os
+
+import numpy as np
 import torch
 
 from . import _lib
+
+FP16_SAFE_MAX = 32768.0
+
+# old family-keyed file layout (hessians.py:39-44, 209-222)
+_FAMILY_FALLBACK = {"attn_q": "qkv_in", "attn_k": "qkv_in", "attn_v": "qkv_in",
+                    "attn_output": "o_in", "ffn_gate": "gateup_in", "ffn_up": "gateup_in",
+                    "ffn_down": "down_in"}
 
 
 def xtx_accumulate(X, H=None):
@@ -75,21 +90,39 @@ def collect_hessians(model, batches, name_map, gguf_ne0=None, progress_every=16,
         raise ValueError(f"{len(mismatched)} module(s) map to a GGUF tensor with a different "
                          f"ne[0]; refusing to mis-key a Hessian")
     acc = {}
+    # input identity of the current forward pass -> (its accumulator, the input). Holding
+    # the input keeps its memory from being reused by a later input of the same pass, so
+    # the address identifies one tensor until the pass ends.
+    seen = {}
 
     def make_hook(g):
         def fn(mod, inp, out):
             x = inp[0]
             if not torch.is_floating_point(x):
                 return
-            if g not in acc:
-                acc[g] = HessianAccumulator(x.shape[-1], x.device)
-            acc[g].add(x.detach())
+            # q/k/v (and gate/up) read one and the same input tensor: accumulate it once and
+            # share the accumulator (the reference forms the identical X^T X per module)
+            key = (x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.dtype)
+            hit = seen.get(key)
+            if hit is None:
+                a = acc.get(g)
+                if a is None:
+                    a = HessianAccumulator(x.shape[-1], x.device)
+                a.add(x.detach())
+                seen[key] = (a, x)
+            else:
+                a = hit[0]
+            if g in acc and acc[g] is not a:
+                raise RuntimeError(f"{g}: shares its input with another module in one batch "
+                                   f"but not in another")
+            acc[g] = a
         return fn
 
     handles = [mod.register_forward_hook(make_hook(g)) for mod, g in plan]
     try:
         with torch.inference_mode():
             for c, ids in enumerate(batches):
+                seen.clear()
                 model(ids)
                 if progress_every and (c + 1) % progress_every == 0:
                     log(f"  chunk {c + 1}")
@@ -97,3 +130,93 @@ def collect_hessians(model, batches, name_map, gguf_ne0=None, progress_every=16,
         for h in handles:
             h.remove()
     return {g: {"H": a.H, "n": a.n} for g, a in acc.items()}, unmapped
+
+
+# ---------------------------------------------------------------- storage
+
+def _path(outdir, gguf_name):
+    return os.path.join(outdir, gguf_name.replace(".", "_") + ".npz")
+
+
+def pack_hessian(H):
+    """(H16 float16 [d, d], diag32 float32 [d], hscale float32) of a float32 Hessian, the
+    stored form of save_hessians, computed on the GPU. H: numpy or torch [d, d]."""
+    lib = _lib.load()
+    Hd = H if isinstance(H, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(H))
+    Hd = Hd.to(device="cuda", dtype=torch.float32).contiguous()
+    d = Hd.shape[0]
+    if Hd.shape != (d, d):
+        raise ValueError("H must be square")
+    H16 = torch.empty((d, d), dtype=torch.float16, device=Hd.device)
+    diag = torch.empty(d, dtype=torch.float32, device=Hd.device)
+    hs = torch.empty(1, dtype=torch.float32, device=Hd.device)
+    ws = _lib.workspace(256, Hd.device)
+    _lib.check(lib.cp_h2_pack(_lib.ptr(Hd), d, _lib.ptr(H16), _lib.ptr(diag), _lib.ptr(hs),
+                              _lib.ptr(ws), ws.numel(), _lib.stream_ptr()))
+    return H16, diag, hs
+
+
+def save_hessians(hessians, outdir):
+    """Write each {gguf_name: {"H": [d, d], "n": rows}} as the reference's npz
+    (hessians.py:166-194): H float16 over hscale, diag32, hscale, n, name."""
+    os.makedirs(outdir, exist_ok=True)
+    for gname, h in hessians.items():
+        H16, diag, hs = pack_hessian(h["H"])
+        np.savez_compressed(_path(outdir, gname), H=H16.cpu().numpy(), diag32=diag.cpu().numpy(),
+                            hscale=np.float32(hs.item()), n=h["n"], name=gname)
+
+
+def _fallback_key(gguf_name):
+    """Old family key: blk.3.attn_q.weight -> blk.3.qkv_in, output.weight -> lmhead_in."""
+    if gguf_name == "output.weight":
+        return "lmhead_in"
+    if not gguf_name.startswith("blk."):
+        return None
+    parts = gguf_name.split(".")
+    if len(parts) < 3:
+        return None
+    fam = _FAMILY_FALLBACK.get(parts[2])
+    return f"blk.{parts[1]}.{fam}" if fam else None
+
+
+def hessian_path(hessdir, gguf_name):
+    """The file load_hessian reads for this tensor (per-tensor first, then the family
+    file), or None."""
+    cand = [_path(hessdir, gguf_name)]
+    fk = _fallback_key(gguf_name)
+    if fk is not None:
+        cand.append(_path(hessdir, fk))
+    for p in cand:
+        if os.path.exists(p):
+            return p
+    return None
+
+
+def has_hessian(hessdir, gguf_name):
+    return hessian_path(hessdir, gguf_name) is not None
+
+
+def load_hessian(hessdir, gguf_name, device=None):
+    """(H float64 [d, d], n) for a GGUF tensor name (hessians.py:225-243): float16 H times
+    hscale with the float32 diagonal written back, or an older float32 H widened. The
+    matrix is rebuilt on the GPU; it is returned there when ``device`` is given, as numpy
+    otherwise. Raises FileNotFoundError when neither file exists."""
+    path = hessian_path(hessdir, gguf_name)
+    if path is None:
+        raise FileNotFoundError(f"no Hessian for {gguf_name} in {hessdir}")
+    lib = _lib.load()
+    with np.load(path) as z:  # plain arrays only: no pickled objects are read
+        Hs = np.ascontiguousarray(z["H"])
+        hscale = float(z["hscale"]) if "hscale" in z.files else 1.0
+        diag = np.ascontiguousarray(z["diag32"], dtype=np.float32) if "diag32" in z.files else None
+        n = int(z["n"])
+    if Hs.dtype not in (np.float16, np.float32):
+        Hs = Hs.astype(np.float32)
+    dev = torch.device(device) if device is not None else torch.device("cuda")
+    Hd = torch.from_numpy(Hs).to(dev)
+    dd = torch.from_numpy(diag).to(dev) if diag is not None else None
+    d = Hs.shape[0]
+    out = torch.empty((d, d), dtype=torch.float64, device=dev)
+    _lib.check(lib.cp_h2_expand(_lib.ptr(Hd), 1 if Hs.dtype == np.float16 else 0, d, hscale,
+                                _lib.ptr(dd), _lib.ptr(out), _lib.stream_ptr()))
+    return (out if device is not None else out.cpu().numpy()), n
