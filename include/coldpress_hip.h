@@ -173,6 +173,32 @@ int cp_h2_pack(const float* H, int64_t n, uint16_t* H16, float* diag32, float* h
 int cp_h2_expand(const void* Hs, int in_dtype, int64_t n, double hscale, const float* diag32,
                  double* H, void* stream);
 
+/* ---- linear form of a k-quant tensor (coldpress/scale_tune.py) ---- */
+
+/* W = d (x) A - dmin (x) B with the codes fixed: d, dmin [nrow, n/256] float32 (the fp16
+ * fields), A, B [nrow, n] integer products as int16 (ab_dtype 0) or float32 (1). dmin and
+ * B are written for Q2_K / Q4_K / Q5_K only (may be NULL otherwise). Replaces
+ * scale_tune.extract_linear -- coldpress/scale_tune.py:67-159. Bit-exact. */
+int cp_lin_extract(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, float* d, float* dmin,
+                   void* A, void* B, int ab_dtype, void* stream);
+
+/* W[r][c] = d[r][c/256] * A[r][c] - dmin[r][c/256] * B[r][c] in float32 (dmin and B NULL
+ * for the types without a min). Equal to the container's decode bit for bit. Replaces
+ * scale_tune.reconstruct / reconstruct_np -- coldpress/scale_tune.py:162-173, 245-269. */
+int cp_lin_reconstruct(int64_t nrow, int64_t n, const float* d, const float* dmin,
+                       const int16_t* A, const int16_t* B, float* W, void* stream);
+
+/* The gradient of that form: gd[r][s] = sum over the superblock of gW * A, gdmin = -sum
+ * of gW * B (float32, summed in a fixed order). The backward of scale_tune.reconstruct. */
+int cp_lin_reconstruct_grad(int64_t nrow, int64_t n, const float* gW, const int16_t* A,
+                            const int16_t* B, float* gd, float* gdmin, void* stream);
+
+/* out = raw with only the fp16 d / dmin fields replaced by float16(d), float16(dmin)
+ * (round to nearest even); in place when out == raw. Replaces scale_tune.write_back --
+ * coldpress/scale_tune.py:176-203. */
+int cp_lin_write_back(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, const float* d,
+                      const float* dmin, uint8_t* out, void* stream);
+
 /* ---- PERM channel permutations (coldpress/perm/spacemaps/qwen3.py, ef.py:289-290) ---- */
 
 /* dst[r][c] = src[row_perm[r]][col_perm[c]] for a row-major [rows, cols] matrix of

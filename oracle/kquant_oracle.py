@@ -12,7 +12,9 @@ arithmetic step for step:
 * no fused multiply-add; division and sqrt are correctly rounded (numpy).
 
 Pinned by the golden byte vectors in tests/golden/kquant_golden.npz, written by
-tests/golden/make_golden.py from the reference encoder itself.
+tests/golden/make_golden.py from the reference encoder itself. The linear form of
+scale_tune.py (linear_parts / linear_reconstruct) is pinned by its exact identity with
+those golden-pinned decoders (tests/test_oracle_kquant.py).
 """
 import numpy as np
 
@@ -665,3 +667,41 @@ DEQUANTIZE = {"Q2_K": decode_q2k, "Q3_K": decode_q3k, "Q4_K": decode_q4k,
 
 def roundtrip(x, ttype, qw=None):
     return DEQUANTIZE[ttype](QUANTIZE[ttype](x, qw), x.shape[1])
+
+
+# ------------------------------------------------------------------ linear form
+# coldpress/scale_tune.py:67-173: with the codes fixed, W = d (x) A - dmin (x) B.
+
+_LIN_LAYOUT = {"Q2_K": (80, 82, 16), "Q3_K": (108, None, 16), "Q4_K": (0, 2, 32),
+               "Q5_K": (0, 2, 32), "Q6_K": (208, None, 16)}
+
+
+def linear_parts(raw, tt, n):
+    """(d [nrow, n/256], dmin or None, A [nrow, n], B or None) as float32: A the integer
+    sub-block scale times the signed code, B the integer sub-block min."""
+    d_off, m_off, sub = _LIN_LAYOUT[tt]
+    nrow = raw.shape[0]
+    b = raw.reshape(-1, BYTES_PER_SB[tt])
+    d = _half_field(b, d_off)
+    dmin = _half_field(b, m_off) if m_off is not None else None
+    q = stored_codes(tt, raw).astype(np.int64)          # signed codes
+    if tt == "Q2_K":
+        sc, mn = (b[:, 0:16] & 0xF).astype(np.int64), (b[:, 0:16] >> 4).astype(np.int64)
+    elif tt == "Q3_K":
+        sc, mn = unpack_scales_q3(b[:, 96:108]).astype(np.int64) - 32, None
+    elif tt in ("Q4_K", "Q5_K"):
+        sc, mn = (v.astype(np.int64) for v in unpack_scales_k4(b[:, 4:16]))
+    else:
+        sc, mn = b[:, 192:208].copy().view(np.int8).astype(np.int64), None
+    A = (np.repeat(sc, sub, 1) * q).astype(F32).reshape(nrow, n)
+    B = np.repeat(mn, sub, 1).astype(F32).reshape(nrow, n) if mn is not None else None
+    ns = n // QK_K
+    return (d.reshape(nrow, ns), dmin.reshape(nrow, ns) if dmin is not None else None, A, B)
+
+
+def linear_reconstruct(d, dmin, A, B):
+    """fl(fl(d*A) - fl(dmin*B)) in float32 (scale_tune.py:162-173)."""
+    W = np.repeat(d, QK_K, 1).astype(F32) * A
+    if dmin is not None:
+        W = W - np.repeat(dmin, QK_K, 1).astype(F32) * B
+    return W.astype(F32)

@@ -74,6 +74,10 @@ SIGNATURES = {
     "cp_ef_profile": (None, [_i32]),
     "cp_ef_phase_ms": (_i32, [_vp, _i32]),
     "cp_permute_gather": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
+    "cp_lin_extract": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp]),
+    "cp_lin_reconstruct": (_i32, [_i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "cp_lin_reconstruct_grad": (_i32, [_i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "cp_lin_write_back": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "cp_h2_pack": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "cp_h2_expand": (_i32, [_vp, _i32, _i64, _f64, _vp, _vp, _vp]),
     "cp_tensor_err_ws_bytes": (_sz, [_err_p, _i32]),

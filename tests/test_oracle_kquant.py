@@ -109,3 +109,30 @@ def test_roundtrip_error_is_small(tt):
     rec = K.roundtrip(x, tt)
     rel = np.linalg.norm(rec - x) / np.linalg.norm(x)
     assert rel < {"Q2_K": 0.6, "Q3_K": 0.35, "Q4_K": 0.2, "Q5_K": 0.1, "Q6_K": 0.05}[tt]
+
+
+@pytest.mark.parametrize("tt", ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"])
+def test_linear_form_reproduces_the_decoder(golden, tt):
+    """scale_tune.py's guarantee (:81-83): d (x) A - dmin (x) B in float32 equals the
+    decoder's values, here on every golden container of the type; A and B are
+    integers within the int16-exact ranges the reference stores them in."""
+    for key in golden.files:
+        if not key.startswith("raw/") or not key.endswith("/" + tt):
+            continue
+        raw = golden[key]
+        n = golden[f"x/{key.split('/')[1]}"].shape[1]
+        d, dmin, A, B = K.linear_parts(raw, tt, n)
+        with np.errstate(all="ignore"):
+            W = K.linear_reconstruct(d, dmin, A, B)
+            ref = K.DEQUANTIZE[tt](raw, n)
+        # equal as values (the reference states it with np.array_equal); bit patterns differ
+        # only in the sign of zeros: d*(sc*q) takes d's sign where q = 0, (d*sc)*q d*sc's
+        # (the edge block whose fp16 scale overflows gives NaN = inf * 0 in both forms)
+        with np.errstate(all="ignore"):
+            assert np.array_equal(W, ref, equal_nan=True), key
+        diff = W.view(np.uint32) != ref.view(np.uint32)
+        assert np.all(W[diff] == 0), key
+        assert np.array_equal(A, np.round(A)) and np.abs(A).max() <= 4096
+        assert (B is None) == (tt in ("Q3_K", "Q6_K"))
+        if B is not None:
+            assert np.array_equal(B, np.round(B)) and B.min() >= 0 and B.max() <= 63
