@@ -63,13 +63,17 @@ def build_workload(layers, device):
 
 
 def hessian_phase(X, H, slot):
-    from perm_amd.hessians import xtx_accumulate
+    """Every layer's Hessians, one batched accumulation per matrix size."""
+    from perm_amd.hessians import xtx_accumulate_many
     for Hb in H.values():
         Hb.zero_()
+    xs, hs = [], []
     for l, fams in enumerate(X):
         for fam, Xf in fams.items():
             d, i = slot[(l, fam)]
-            xtx_accumulate(Xf, H[d][i])
+            xs.append(Xf)
+            hs.append(H[d][i])
+    xtx_accumulate_many(xs, hs)
 
 
 def ef_phase(W, H, slot, layers, mode, concurrent=True):
@@ -81,14 +85,15 @@ def ef_phase(W, H, slot, layers, mode, concurrent=True):
 
     def builder(d):
         def build(U, order):
+            # qw = diag(H) / N for every Hessian of the class in one kernel
+            qw = (H[d].diagonal(dim1=1, dim2=2) / float(ROWS)).contiguous()
             items = []
             for l in range(layers):
                 for name, _rows, _n, fam in wl.QWEN3_06B_LAYER:
                     dd, i = slot[(l, fam)]
                     if dd != d:
                         continue
-                    qw = H[d][i].diagonal() / float(ROWS)
-                    items.append({"ttype": "Q2_K", "x": W[l][name], "qw": qw.contiguous(),
+                    items.append({"ttype": "Q2_K", "x": W[l][name], "qw": qw[i],
                                   "U": U[i], "order": order[i], "recon": True})
             return items
         return build
@@ -373,7 +378,7 @@ def main():
     hess_tflops = hess_flops / (hess_ms * 1e-3) / 1e12
 
     # dominant kernel: the Hessian MFMA kernel (one launch per Hessian) or the EF sweep
-    hess_launches = 4 * layers
+    hess_launches = len(H)  # one batched launch per Hessian size
     sweep_launches = 2 * len(H)  # sequential pass: two iterations per size class
     if hess_ms >= ph[2]:
         avg_ms = hess_ms / hess_launches

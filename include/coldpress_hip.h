@@ -156,6 +156,13 @@ int cp_ef_phase_ms(float* out, int nphase);
  * not fixed (split-K partials are added with float32 atomics). */
 int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, float* H, void* stream);
 
+/* H[z] += X[z]^T X[z] for ``count`` jobs of one shape (host arrays of device pointers),
+ * bf16 jobs in as few launches as fit (224 per launch): many Hessians share one grid, so
+ * small d needs fewer row splits. The batched form of cp_hess_accum (the hook of
+ * coldpress/hessians.py:137-154 for every hooked module of a forward pass). */
+int cp_hess_accum_batch(const void* const* X, float* const* H, int count, int x_dtype,
+                        int64_t N, int64_t d, void* stream);
+
 /* ---- Hessian storage (coldpress/hessians.py:163-243) ---- */
 
 /* Pack a float32 [n, n] Hessian for storage: diag32 = diag(H) (float32, exact);

@@ -225,16 +225,29 @@ __device__ __forceinline__ void tile_rows(const uint16_t* X, int64_t r0, int64_t
   }
 }
 
-__global__ __launch_bounds__(HNT) void hess_bf16_tri_kernel(const uint16_t* __restrict__ X, int64_t N,
-                                                            int d, int ntiles, int splits,
-                                                            int64_t rows_per_split,
-                                                            float* __restrict__ H) {
+// Up to kHessJobs Hessians of one shape per launch, by value in the kernel arguments.
+constexpr int kHessJobs = 224;
+struct HessJobs {
+  const uint16_t* X[kHessJobs];
+  float* H[kHessJobs];
+};
+static_assert(sizeof(HessJobs) <= 4000, "kernel argument block");
+
+__global__ __launch_bounds__(HNT) void hess_bf16_tri_kernel(const HessJobs jobs, int njobs,
+                                                            int64_t N, int d, int ntiles, int splits,
+                                                            int64_t rows_per_split) {
   __shared__ __align__(16) char lds[NSLOT * 2 * PANEL];
-  const int total = ntiles * splits;
+  // items run job by job, then split by split: the XCD-contiguous hand-out keeps one
+  // XCD on the same rows of one X
+  const int per_job = ntiles * splits;
+  const int total = per_job * njobs;
   const int per = (total + 7) / 8;
   const int item = (blockIdx.x % 8) * per + blockIdx.x / 8;
   if (item >= total) return;
-  const int split = item / ntiles, tile = item - split * ntiles;
+  const int job = item / per_job, rem = item - job * per_job;
+  const int split = rem / ntiles, tile = rem - split * ntiles;
+  const uint16_t* __restrict__ X = jobs.X[job];
+  float* __restrict__ H = jobs.H[job];
   int ti = (int)((sqrtf(8.0f * (float)tile + 1.0f) - 1.0f) * 0.5f);
   while (ti * (ti + 1) / 2 > tile) --ti;
   while ((ti + 1) * (ti + 2) / 2 <= tile) ++ti;
@@ -273,8 +286,9 @@ __global__ __launch_bounds__(HNT) void hess_bf16_tri_kernel(const uint16_t* __re
       }
 }
 
-// H[i][j] = H[j][i] for i < j, through 64 x 64 LDS tiles.
-__global__ __launch_bounds__(256) void hess_mirror_kernel(float* __restrict__ H, int d) {
+// H[i][j] = H[j][i] for i < j, through 64 x 64 LDS tiles; blockIdx.z is the job.
+__global__ __launch_bounds__(256) void hess_mirror_kernel(const HessJobs jobs, int d) {
+  float* __restrict__ H = jobs.H[blockIdx.z];
   __shared__ float tl[64][65];
   const int bi = blockIdx.y, bj = blockIdx.x;  // target tile (upper): rows bi, cols bj
   if (bj < bi) return;
@@ -369,43 +383,84 @@ static int pick_splits(int ntiles, int64_t N, int64_t d) {
 
 }  // namespace cp
 
-extern "C" int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, float* H, void* stream) {
-  cp::clear_error();
-  if (!X || !H) return cp::set_error(CP_ERR_ARG, "null X/H");
-  if (N <= 0 || d <= 0 || d > (1 << 20)) return cp::set_error(CP_ERR_SHAPE, "bad X shape [%lld, %lld]", (long long)N, (long long)d);
-  if (x_dtype != 0 && x_dtype != 1) return cp::set_error(CP_ERR_ARG, "x_dtype must be 0 (f32) or 1 (bf16)");
-  if (!cp::aligned(X, 16) || !cp::aligned(H, 4)) return cp::set_error(CP_ERR_ALIGN, "X needs 16-byte alignment");
-  if (x_dtype == 1 && d % 8) return cp::set_error(CP_ERR_SHAPE, "bf16 X needs d %% 8 == 0 (got %lld)", (long long)d);
-  hipStream_t st = (hipStream_t)stream;
-  if (x_dtype == 1) {
-    const int T = (int)((d + cp::BT - 1) / cp::BT);
-    const int ntiles = T * (T + 1) / 2;
-    const int splits = cp::pick_splits(ntiles, N, d);
-    if (splits == 0 || (int64_t)ntiles * splits * 8 > INT32_MAX)
-      return cp::set_error(CP_ERR_SHAPE, "X [%lld, %lld] too large for one accumulation; pass fewer rows",
-                           (long long)N, (long long)d);
+namespace cp {
+
+// H_z += X_z^T X_z for count jobs of one shape, bf16 X.
+static int hess_bf16_batch(const void* const* X, float* const* H, int count, int64_t N, int64_t d,
+                           hipStream_t st) {
+  const int T = (int)((d + BT - 1) / BT);
+  const int ntiles = T * (T + 1) / 2;
+  for (int c0 = 0; c0 < count; c0 += kHessJobs) {
+    const int cn = count - c0 < kHessJobs ? count - c0 : kHessJobs;
+    HessJobs jobs;
+    for (int i = 0; i < cn; ++i) {
+      if (!X[c0 + i] || !H[c0 + i]) return set_error(CP_ERR_ARG, "job %d: null X/H", c0 + i);
+      if (!aligned(X[c0 + i], 16) || !aligned(H[c0 + i], 4))
+        return set_error(CP_ERR_ALIGN, "job %d: X needs 16-byte alignment", c0 + i);
+      jobs.X[i] = (const uint16_t*)X[c0 + i];
+      jobs.H[i] = H[c0 + i];
+    }
+    const int splits = pick_splits(ntiles * cn, N, d);
+    if (splits == 0 || (int64_t)ntiles * cn * splits * 8 > INT32_MAX)
+      return set_error(CP_ERR_SHAPE, "X [%lld, %lld] too large for one accumulation; pass fewer rows",
+                       (long long)N, (long long)d);
     int64_t rps = (N + splits - 1) / splits;
-    rps = (rps + cp::KS - 1) / cp::KS * cp::KS;
-    const int total = ntiles * splits;
+    rps = (rps + KS - 1) / KS * KS;
+    const int total = ntiles * splits * cn;
     const int per = (total + 7) / 8;
-    cp::hess_bf16_tri_kernel<<<dim3(8 * per), cp::HNT, 0, st>>>((const uint16_t*)X, N, (int)d,
-                                                                ntiles, splits, rps, H);
+    hess_bf16_tri_kernel<<<dim3(8 * per), HNT, 0, st>>>(jobs, cn, N, (int)d, ntiles, splits, rps);
     CP_LAUNCHED("hessian launch");
     const int tb = (int)((d + 63) / 64);
-    cp::hess_mirror_kernel<<<dim3(tb, tb), 256, 0, st>>>(H, (int)d);
+    hess_mirror_kernel<<<dim3(tb, tb, cn), 256, 0, st>>>(jobs, (int)d);
     CP_LAUNCHED("hessian mirror");
-    return CP_OK;
   }
-  const int tiles = (int)((d + cp::HT - 1) / cp::HT);
+  return CP_OK;
+}
+
+static int hess_f32(const float* X, int64_t N, int64_t d, float* H, hipStream_t st) {
+  const int tiles = (int)((d + HT - 1) / HT);
   // enough row splits for ~4 workgroups per CU, each at least 512 rows
   int64_t want = (1024 + (int64_t)tiles * tiles - 1) / ((int64_t)tiles * tiles);
   int64_t splits = want < 1 ? 1 : want;
   int64_t rps = (N + splits - 1) / splits;
   if (rps < 512) rps = 512;
-  rps = (rps + cp::KT - 1) / cp::KT * cp::KT;
+  rps = (rps + KT - 1) / KT * KT;
   splits = (N + rps - 1) / rps;
   dim3 grid(tiles, tiles, (unsigned)splits);
-  cp::hess_f32_kernel<<<grid, 256, 0, st>>>((const float*)X, N, (int)d, rps, H);
+  hess_f32_kernel<<<grid, 256, 0, st>>>(X, N, (int)d, rps, H);
   CP_LAUNCHED("hessian launch");
+  return CP_OK;
+}
+
+static int hess_check(int x_dtype, int64_t N, int64_t d) {
+  if (N <= 0 || d <= 0 || d > (1 << 20)) return set_error(CP_ERR_SHAPE, "bad X shape [%lld, %lld]", (long long)N, (long long)d);
+  if (x_dtype != 0 && x_dtype != 1) return set_error(CP_ERR_ARG, "x_dtype must be 0 (f32) or 1 (bf16)");
+  if (x_dtype == 1 && d % 8) return set_error(CP_ERR_SHAPE, "bf16 X needs d %% 8 == 0 (got %lld)", (long long)d);
+  return CP_OK;
+}
+
+}  // namespace cp
+
+extern "C" int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, float* H, void* stream) {
+  cp::clear_error();
+  if (!X || !H) return cp::set_error(CP_ERR_ARG, "null X/H");
+  if (int s = cp::hess_check(x_dtype, N, d)) return s;
+  if (!cp::aligned(X, 16) || !cp::aligned(H, 4)) return cp::set_error(CP_ERR_ALIGN, "X needs 16-byte alignment");
+  if (x_dtype == 1) return cp::hess_bf16_batch(&X, &H, 1, N, d, (hipStream_t)stream);
+  return cp::hess_f32((const float*)X, N, d, H, (hipStream_t)stream);
+}
+
+extern "C" int cp_hess_accum_batch(const void* const* X, float* const* H, int count, int x_dtype,
+                                   int64_t N, int64_t d, void* stream) {
+  cp::clear_error();
+  if (!X || !H || count <= 0) return cp::set_error(CP_ERR_ARG, "no jobs");
+  if (int s = cp::hess_check(x_dtype, N, d)) return s;
+  hipStream_t st = (hipStream_t)stream;
+  if (x_dtype == 1) return cp::hess_bf16_batch(X, H, count, N, d, st);
+  for (int i = 0; i < count; ++i) {
+    if (!X[i] || !H[i]) return cp::set_error(CP_ERR_ARG, "job %d: null X/H", i);
+    if (!cp::aligned(X[i], 16) || !cp::aligned(H[i], 4)) return cp::set_error(CP_ERR_ALIGN, "job %d: misaligned", i);
+    if (int s = cp::hess_f32((const float*)X[i], N, d, H[i], st)) return s;
+  }
   return CP_OK;
 }

@@ -178,9 +178,10 @@ def encode_size_classes(classes, n_iter=2, mode="exact", damp=0.01, act_order=Tr
     classes: list of (Hb [batch, n, n] CUDA float32/float64, build) where
     build(U, order) returns the ef_encode_dev items of that class (U [batch, n, n],
     order [batch, n]). Every class gets its own stream; from this one host thread
-    the act orders and one factorization attempt of every class are queued first,
-    then every class's EF, so one class's factorization overlaps another's
-    sweep. Then the factorization flags are read (the only wait), and a class
+    the act orders and one factorization attempt of every class are queued first (in
+    the given order: largest first keeps the longest chain in front), then every
+    class's EF, smallest matrices first, so one class's factorization overlaps
+    another's sweep. Then the factorization flags are read (the only wait), and a class
     with a failed matrix is factorized again with escalation and re-encoded.
     The caller's current stream ends up ordered after all of it.
     Returns one ef_encode_dev result list per class."""
@@ -193,11 +194,14 @@ def encode_size_classes(classes, n_iter=2, mode="exact", damp=0.01, act_order=Tr
             order = act_order_dev(Hb, act_order)
             U, flags = factor_dev_async(Hb, order, damp)
         facs.append((order, U, flags))
-    outs = []
-    for (_, build), s, (order, U, _) in zip(classes, streams, facs):
+    # EFs are queued smallest matrices first: their factorizations end first, and the
+    # host time spent queueing the others would otherwise delay them
+    outs = [None] * len(classes)
+    for k in sorted(range(len(classes)), key=lambda k: classes[k][0].shape[-1]):
+        (_, build), s, (order, U, _) = classes[k], streams[k], facs[k]
         with torch.cuda.stream(s):
-            outs.append(ef_encode_dev(build(U, order), n_iter, MODES[mode] if isinstance(mode, str)
-                                      else mode))
+            outs[k] = ef_encode_dev(build(U, order), n_iter, MODES[mode] if isinstance(mode, str)
+                                    else mode)
     for s in streams:
         cur.wait_stream(s)
     for res in outs:

@@ -50,6 +50,32 @@ def xtx_accumulate(X, H=None):
     return H
 
 
+def xtx_accumulate_many(Xs, Hs):
+    """Hs[z] += Xs[z]^T Xs[z] for many (X, H) pairs, batched by (rows, d, dtype) into as
+    few launches as fit. X: [..., d] bf16 or float32 CUDA tensors; H: contiguous float32
+    [d, d] CUDA tensors (updated in place)."""
+    import ctypes
+    lib = _lib.load()
+    groups = {}
+    for X, H in zip(Xs, Hs):
+        d = X.shape[-1]
+        X2 = X.reshape(-1, d)
+        if X2.dtype not in (torch.bfloat16, torch.float32):
+            X2 = X2.float()
+        X2 = X2.contiguous()
+        if H.shape != (d, d) or H.dtype != torch.float32 or not H.is_contiguous():
+            raise ValueError("H must be a contiguous float32 [d, d] tensor")
+        groups.setdefault((X2.shape[0], d, X2.dtype), []).append((X2, H))
+    for (N, d, dt), jobs in groups.items():
+        xs = (ctypes.c_void_p * len(jobs))(*[x.data_ptr() for x, _ in jobs])
+        hs = (ctypes.c_void_p * len(jobs))(*[h.data_ptr() for _, h in jobs])
+        st = lib.cp_hess_accum_batch(ctypes.cast(xs, ctypes.c_void_p), ctypes.cast(hs, ctypes.c_void_p),
+                                     len(jobs), 1 if dt == torch.bfloat16 else 0, N, d,
+                                     _lib.stream_ptr())
+        _lib.check(st)
+    return Hs
+
+
 class HessianAccumulator:
     """Device-resident float32 X^T X accumulator with a row count (the hook state
     of coldpress/hessians.py:148-153)."""

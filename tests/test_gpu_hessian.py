@@ -52,3 +52,25 @@ def test_collect_hessians_hooks(hs):
     assert Ho.rel_fro(res["blk.0.ffn_up.weight"]["H"].cpu().numpy(), Ho.xtx(X0)) < 1e-5
     with pytest.raises(ValueError, match="different"):
         hs.collect_hessians(model, batches, {"0": "x.weight"}, gguf_ne0={"x.weight": 128})
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_batched_accumulation(hs, dtype):
+    """Many (X, H) jobs in one call, mixed shapes (grouped per shape), with H accumulated
+    in place: every H within 1e-5 of its own closed form, and more jobs of one shape than
+    one launch carries (224)."""
+    g = torch.Generator(device="cuda").manual_seed(7)
+    shapes = [(2048, 1024)] * 3 + [(999, 256)] * 2 + [(4096, 520)] + [(64, 136)] * 230
+    Xs, Hs, base = [], [], []
+    for k, (N, d) in enumerate(shapes):
+        Xs.append((torch.randn((N, d), generator=g, device="cuda") *
+                   torch.exp(torch.randn((d,), generator=g, device="cuda"))).to(dtype))
+        H0 = torch.randn((d, d), generator=g, device="cuda")
+        H0 = H0 @ H0.T
+        base.append(H0.cpu().numpy().astype(np.float64))
+        Hs.append(H0.contiguous())
+    print(f"batched {dtype}: {len(shapes)} jobs", flush=True)
+    hs.xtx_accumulate_many(Xs, Hs)
+    for k in list(range(7)) + [100, 235]:
+        ref = base[k] + Ho.xtx(Xs[k].float().cpu().numpy())
+        assert Ho.rel_fro(Hs[k].cpu().numpy(), ref) < 1e-5, k
