@@ -47,8 +47,8 @@ constexpr int NW = 256;  // outer block-column width of the left-looking sweep
 // op(B) = B [K,N] or, with BT, B^T for B stored [N,K]. Batched over blockIdx.z
 // as z = z1 * nz2 + z2 with separate strides per level.
 //
-// Block tile BM x 64 (BM = 64 or 128), K tile 16; the 4 waves are stacked
-// along M, each BM/4 x 64 built from v_mfma_f64_16x16x4f64. The next K tile is
+// Block tile BM x BN (BM = 64 or 128, BN = 64), K tile 16; the 4 waves are stacked
+// along M, each BM/4 x BN built from v_mfma_f64_16x16x4f64. The next K tile is
 // fetched into registers while the current one is multiplied, then stored into
 // the other half of a double-buffered LDS, so one barrier separates K tiles.
 // Within a K tile, lane group g = lane/16 supplies k = 4g + s to MFMA step s
@@ -97,8 +97,6 @@ __device__ __forceinline__ bool gemm_tile(const GemmArgs& g, int& bx, int& by, i
 
 constexpr int GBK = 16;       // K tile
 constexpr int GLD = GBK + 2;  // LDS row of a [rows][K] tile: 144 B, fragment reads conflict-free
-constexpr int GNLD = 64 + 4;  // LDS row of a [K][64] tile: 544 B, lane groups 4 rows apart land
-                              // in opposite halves of the banks
 
 // p[0], p[1] at column indices c, c + 1, zero where the row is out of range
 // (!ok) or the column reaches lim. VEC: p is 16-byte aligned.
@@ -114,12 +112,14 @@ __device__ inline double2 ld_pair(const double* p, bool ok, int c, int lim) {
   return v;
 }
 
-template <bool BT, int BM, bool VEC>
+template <bool BT, int BM, int BN, bool VEC>
 __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
   constexpr int TI = BM / 64;  // 16-row MFMA tiles per wave
+  constexpr int TJ = BN / 16;  // 16-column MFMA tiles per wave
   constexpr int AQ = BM / 32;  // A-tile pairs fetched per thread
-  constexpr int BROWS = BT ? 64 : GBK;
-  constexpr int BLD = BT ? GLD : GNLD;
+  constexpr int BQ = BN / 32;  // B-tile pairs fetched per thread
+  constexpr int BROWS = BT ? BN : GBK;
+  constexpr int BLD = BT ? GLD : BN + 4;  // [K][BN] rows: lane groups 4 rows apart in opposite bank halves
   __shared__ __align__(16) double As[2][BM][GLD];
   __shared__ __align__(16) double Bs[2][BROWS][BLD];
   int bx, by, bz;
@@ -128,26 +128,26 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
   const double* A = g.A + z1 * g.sA1 + z2 * g.sA2;
   const double* B = g.B + z1 * g.sB1 + z2 * g.sB2;
   double* C = g.C + z1 * g.sC1 + z2 * g.sC2;
-  const int bm = by * BM, bn = bx * 64;
+  const int bm = by * BM, bn = bx * BN;
   if ((g.tri & 4) && bn >= bm + BM) return;
   const int t = threadIdx.x, l = t & 63, wm = (t >> 6) * (BM / 4);
   const int lr = l & 15, lg = l >> 4;
   // loader coordinates: [rows][K] tiles as (row t/8 + 32q, k pair t%8),
-  // [K][64] tiles as (k t/32 + 8q, column pair t%32)
+  // [K][BN] tiles as (k t/(BN/2) + (512/BN)q, column pair t%(BN/2))
   const int tr = t >> 3, tk = (t & 7) * 2;
-  const int nr = t >> 5, nc = (t & 31) * 2;
+  const int nr = t / (BN / 2), nc = (t % (BN / 2)) * 2;
 
-  dbl4 acc[TI][4];
+  dbl4 acc[TI][TJ];
 #pragma unroll
   for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = dbl4{0.0, 0.0, 0.0, 0.0};
+    for (int j = 0; j < TJ; ++j) acc[i][j] = dbl4{0.0, 0.0, 0.0, 0.0};
 
   const int kbeg = (g.tri & 2) ? (bn & ~(GBK - 1)) : 0;
   const int kend = (g.tri & 1) ? min(g.K, bm + BM) : g.K;
   const int nt = kend > kbeg ? (kend - kbeg + GBK - 1) / GBK : 0;
 
-  double2 ra[AQ], rb[2];
+  double2 ra[AQ], rb[BQ];
   auto fetch = [&](int k0) {
 #pragma unroll
     for (int q = 0; q < AQ; ++q) {
@@ -155,12 +155,12 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
       ra[q] = ld_pair<VEC>(A + (int64_t)r * g.lda + k0 + tk, r < g.M, k0 + tk, g.K);
     }
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < BQ; ++q) {
       if (BT) {
         const int r = bn + tr + 32 * q;
         rb[q] = ld_pair<VEC>(B + (int64_t)r * g.ldb + k0 + tk, r < g.N, k0 + tk, g.K);
       } else {
-        const int k = k0 + nr + 8 * q;
+        const int k = k0 + nr + (512 / BN) * q;
         rb[q] = ld_pair<VEC>(B + (int64_t)k * g.ldb + bn + nc, k < g.K, bn + nc, g.N);
       }
     }
@@ -169,11 +169,11 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int q = 0; q < AQ; ++q) *reinterpret_cast<double2*>(&As[b][tr + 32 * q][tk]) = ra[q];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < BQ; ++q) {
       if (BT)
         *reinterpret_cast<double2*>(&Bs[b][tr + 32 * q][tk]) = rb[q];
       else
-        *reinterpret_cast<double2*>(&Bs[b][nr + 8 * q][nc]) = rb[q];
+        *reinterpret_cast<double2*>(&Bs[b][nr + (512 / BN) * q][nc]) = rb[q];
     }
   };
 
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
   for (int it = 0; it < nt; ++it) {
     const int b = it & 1;
     if (it + 1 < nt) fetch(kbeg + (it + 1) * GBK);
-    double af[TI][4], bf[4][4];
+    double af[TI][4], bf[TJ][4];
 #pragma unroll
     for (int ti = 0; ti < TI; ++ti) {
       const double2* p = reinterpret_cast<const double2*>(&As[b][wm + 16 * ti + lr][4 * lg]);
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
       af[ti][3] = v.y;
     }
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj) {
+    for (int tj = 0; tj < TJ; ++tj) {
       if (BT) {
         const double2* p = reinterpret_cast<const double2*>(&Bs[b][16 * tj + lr][4 * lg]);
         const double2 u = p[0], v = p[1];
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int ti = 0; ti < TI; ++ti)
 #pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
+        for (int tj = 0; tj < TJ; ++tj)
           acc[ti][tj] = __builtin_amdgcn_mfma_f64_16x16x4f64(af[ti][s], bf[tj][s], acc[ti][tj], 0, 0, 0);
     if (it + 1 < nt) stash(b ^ 1);
     __syncthreads();
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
 #pragma unroll
   for (int ti = 0; ti < TI; ++ti)
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj)
+    for (int tj = 0; tj < TJ; ++tj)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         // v_mfma_f64_16x16x4f64 result: register r of lane l holds row 4r + l/16, column l%16
@@ -236,12 +236,12 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
       }
 }
 
-template <bool BT, int BM>
+template <bool BT, int BM, int BN>
 static void launch_gemm(const GemmArgs& a, dim3 grid, bool vec, hipStream_t st) {
   if (vec)
-    dgemm_kernel<BT, BM, true><<<grid, 256, 0, st>>>(a);
+    dgemm_kernel<BT, BM, BN, true><<<grid, 256, 0, st>>>(a);
   else
-    dgemm_kernel<BT, BM, false><<<grid, 256, 0, st>>>(a);
+    dgemm_kernel<BT, BM, BN, false><<<grid, 256, 0, st>>>(a);
 }
 
 // every (z1, z2) base of the operand is 16-byte aligned and so are its rows
@@ -253,24 +253,24 @@ static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
   if (a0.M <= 0 || a0.N <= 0 || nz1 <= 0) return CP_OK;
   const bool vec = pairs_aligned(a0.A, a0.lda, a0.sA1, a0.sA2) &&
                    pairs_aligned(a0.B, a0.ldb, a0.sB1, a0.sB2);
-  const int nt = (a0.N + 63) / 64;
-  // 128-row tiles when they still give two blocks per CU, 64-row ones otherwise
-  const bool big = (int64_t)nt * ((a0.M + 127) / 128) * nz1 * a0.nz2 >= 512;
-  const int bm = big ? 128 : 64;
+  // 128-row tiles when they still give two blocks per CU, 64-row ones otherwise. (A
+  // 128 x 128 tile needs ~400 VGPRs, one wave per SIMD, and measured slower: nothing
+  // hides its barrier and staging gaps.)
+  const int64_t z = (int64_t)nz1 * a0.nz2;
+  const int bn = 64;
+  const int bm = (a0.M + 127) / 128 * ((a0.N + 63) / 64) * z >= 512 ? 128 : 64;
   GemmArgs a = a0;
-  a.ntx = nt;
+  a.ntx = (a.N + bn - 1) / bn;
   a.nty = (a.M + bm - 1) / bm;
-  a.nzt = nz1 * a0.nz2;
+  a.nzt = (int)z;
   const int64_t total = (int64_t)a.ntx * a.nty * a.nzt;
   if (total > (int64_t)1 << 30) return set_error(CP_ERR_SHAPE, "fp64 GEMM grid too large");
   const dim3 grid((unsigned)(8 * ((total + 7) / 8)));
-  {
-    if (bt)
-      big ? launch_gemm<true, 128>(a, grid, vec, st) : launch_gemm<true, 64>(a, grid, vec, st);
-    else
-      big ? launch_gemm<false, 128>(a, grid, vec, st) : launch_gemm<false, 64>(a, grid, vec, st);
-    CP_LAUNCHED("fp64 GEMM launch");
-  }
+  if (bt)
+    bm == 128 ? launch_gemm<true, 128, 64>(a, grid, vec, st) : launch_gemm<true, 64, 64>(a, grid, vec, st);
+  else
+    bm == 128 ? launch_gemm<false, 128, 64>(a, grid, vec, st) : launch_gemm<false, 64, 64>(a, grid, vec, st);
+  CP_LAUNCHED("fp64 GEMM launch");
   return CP_OK;
 }
 
@@ -322,12 +322,13 @@ __global__ void fact_shift_kernel(const T* H, int n, int64_t sH, const int* orde
   }
 }
 
-// A[i][j] = H[q_i][q_j] (+ shift on the diagonal) for i >= j, with
+// A[i][j] = H[q_i][q_j] (+ shift on the diagonal) for i >= j, 0 above, with
 // q_i = order[n-1-i]: the act_order gather and the index reversal in one pass.
+// Element-wise form, for rows too long to stage.
 template <typename T>
-__global__ void fact_prepare_kernel(const T* H, int n, int64_t sH, const int* order, int64_t sO,
-                                    const double* shift, double* A, int64_t sA,
-                                    const int* active) {
+__global__ void fact_prepare_gather_kernel(const T* H, int n, int64_t sH, const int* order,
+                                           int64_t sO, const double* shift, double* A, int64_t sA,
+                                           const int* active) {
   const int z = blockIdx.z;
   if (active && !active[z]) return;
   const int j = blockIdx.x * 64 + (threadIdx.x & 63);
@@ -344,6 +345,40 @@ __global__ void fact_prepare_kernel(const T* H, int n, int64_t sH, const int* or
   double v = (double)H[z * sH + (int64_t)qi * n + qj];
   if (i == j) v = v + shift[z];
   a[(int64_t)i * n + j] = v;
+}
+
+// The same with rows staged: a block copies rows q_i of R consecutive rows i into LDS
+// (read whole, coalesced), then writes the R rows of A from there.
+template <typename T>
+__global__ __launch_bounds__(256) void fact_prepare_kernel(const T* H, int n, int64_t sH,
+                                                           const int* order, int64_t sO,
+                                                           const double* shift, double* A,
+                                                           int64_t sA, const int* active, int R) {
+  extern __shared__ __align__(16) char prep_lds[];
+  T* rows = reinterpret_cast<T*>(prep_lds);
+  const int z = blockIdx.y;
+  if (active && !active[z]) return;
+  const int i0 = blockIdx.x * R;
+  const int* o = order ? order + z * sO : nullptr;
+  const T* h = H + z * sH;
+  for (int r = 0; r < R && i0 + r < n; ++r) {
+    const int qi = o ? o[n - 1 - (i0 + r)] : n - 1 - (i0 + r);
+    for (int c = threadIdx.x; c < n; c += blockDim.x) rows[(int64_t)r * n + c] = h[(int64_t)qi * n + c];
+  }
+  __syncthreads();
+  double* a = A + z * sA;
+  for (int j = threadIdx.x; j < n; j += blockDim.x) {
+    const int qj = o ? o[n - 1 - j] : n - 1 - j;
+    for (int r = 0; r < R && i0 + r < n; ++r) {
+      const int i = i0 + r;
+      double v = 0.0;
+      if (j <= i) {
+        v = (double)rows[(int64_t)r * n + qj];
+        if (j == i) v = v + shift[z];
+      }
+      a[(int64_t)i * n + j] = v;
+    }
+  }
 }
 
 // ---------------------------------------------------------------- diagonal block
@@ -477,16 +512,25 @@ __global__ void fill_i32_kernel(int* p, int64_t count, int v) {
 
 // ---------------------------------------------------------------- act order
 // order = stable argsort of -diag(H): rank of i = #{j: d_j > d_i} + #{j < i: d_j == d_i}.
-template <typename T>
-__global__ void act_order_kernel(const T* H, int n, int64_t sH, int* order, int64_t sO) {
+// STAGE: the block first copies the diagonal into LDS (n * sizeof(T) bytes, dynamic),
+// so each diagonal entry leaves HBM once per block instead of once per thread.
+template <typename T, bool STAGE>
+__global__ __launch_bounds__(256) void act_order_kernel(const T* H, int n, int64_t sH, int* order,
+                                                        int64_t sO) {
+  extern __shared__ __align__(16) char act_lds[];
+  T* dg = reinterpret_cast<T*>(act_lds);
   const int z = blockIdx.y;
+  const T* h = H + z * sH;
+  if (STAGE) {
+    for (int j = threadIdx.x; j < n; j += blockDim.x) dg[j] = h[(int64_t)j * n + j];
+    __syncthreads();
+  }
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const T* h = H + z * sH;
-  const double di = (double)h[(int64_t)i * n + i];
+  const double di = (double)(STAGE ? dg[i] : h[(int64_t)i * n + i]);
   int rank = 0;
   for (int j = 0; j < n; ++j) {
-    double dj = (double)h[(int64_t)j * n + j];
+    const double dj = (double)(STAGE ? dg[j] : h[(int64_t)j * n + j]);
     rank += (dj > di) || (dj == di && j < i);
   }
   order[z * sO + rank] = i;
@@ -580,8 +624,18 @@ static int fact_attempt(const T* H, int64_t sH, int n, int batch, const int* ord
   fill_kernel<<<1024, 256, 0, st>>>(X, (int64_t)nn * batch, 0.0);
   fact_shift_kernel<T><<<batch, 256, 0, st>>>(H, n, sH, order, sO, w.damp_d, w.diag_tmp, w.shift,
                                                 w.active);
-  fact_prepare_kernel<T><<<dim3((n + 63) / 64, (n + 3) / 4, batch), 256, 0, st>>>(
-      H, n, sH, order, sO, w.shift, A, sA, w.active);
+  // rows of H staged per block: as many as fit in 48 KB, up to 8; rows longer than
+  // 64 KB take the element-wise gather
+  const int64_t row_bytes = (int64_t)n * sizeof(T);
+  if (row_bytes <= 64 * 1024) {
+    int R = (int)((48 * 1024) / row_bytes);
+    R = R < 1 ? 1 : (R > 8 ? 8 : R);
+    fact_prepare_kernel<T><<<dim3((n + R - 1) / R, batch), 256, (size_t)R * row_bytes, st>>>(
+        H, n, sH, order, sO, w.shift, A, sA, w.active, R);
+  } else {
+    fact_prepare_gather_kernel<T><<<dim3((n + 63) / 64, (n + 3) / 4, batch), 256, 0, st>>>(
+        H, n, sH, order, sO, w.shift, A, sA, w.active);
+  }
   CP_LAUNCHED("factor prepare");
   // left-looking in two levels: an NW-wide block column first receives all
   // earlier columns' updates in one large-K GEMM; inside it, each NB-wide
@@ -715,10 +769,19 @@ int cp_act_order(const void* H, int h_dtype, int64_t n, int batch, int32_t* orde
   if (!H || !order || n <= 0 || batch <= 0) return cp::set_error(CP_ERR_ARG, "bad act_order arguments");
   hipStream_t st = (hipStream_t)stream;
   dim3 grid((unsigned)((n + 255) / 256), batch);
-  if (h_dtype == 1)
-    cp::act_order_kernel<double><<<grid, 256, 0, st>>>((const double*)H, (int)n, n * n, order, n);
-  else
-    cp::act_order_kernel<float><<<grid, 256, 0, st>>>((const float*)H, (int)n, n * n, order, n);
+  const size_t lds = (size_t)n * (h_dtype == 1 ? 8 : 4);
+  const bool stage = lds <= 64 * 1024;
+  if (h_dtype == 1) {
+    if (stage)
+      cp::act_order_kernel<double, true><<<grid, 256, lds, st>>>((const double*)H, (int)n, n * n, order, n);
+    else
+      cp::act_order_kernel<double, false><<<grid, 256, 0, st>>>((const double*)H, (int)n, n * n, order, n);
+  } else {
+    if (stage)
+      cp::act_order_kernel<float, true><<<grid, 256, lds, st>>>((const float*)H, (int)n, n * n, order, n);
+    else
+      cp::act_order_kernel<float, false><<<grid, 256, 0, st>>>((const float*)H, (int)n, n * n, order, n);
+  }
   CP_LAUNCHED("act_order launch");
   return CP_OK;
 }
