@@ -554,7 +554,6 @@ struct EfDev {
   float* WcurT;
   float* Wcur;
   uint8_t* LT;
-  uint8_t* Lrow;
   float* dlT;
   float* mlT;
   int* inv;
@@ -585,10 +584,11 @@ __global__ void ef_index_kernel(const EfDev* __restrict__ tab) {
 
 // dst[inv[c]][r] = src[r][c] (row-major storage order -> column-major visiting
 // order) or its inverse, through a 64x64 LDS tile (coalesced on both sides).
-// WHICH: 0 = x -> WpT, 1 = LT -> Lrow, 2 = WcurT -> Wcur.
+// WHICH: 0 = x -> WpT, 2 = WcurT -> Wcur.
 template <int WHICH>
 __global__ __launch_bounds__(256) void ef_transpose_kernel(const EfDev* __restrict__ tab) {
-  typedef typename std::conditional<WHICH == 1, uint8_t, float>::type T;
+  static_assert(WHICH == 0 || WHICH == 2, "float transposes only");
+  typedef float T;
   const EfDev& t = tab[blockIdx.z];
   const int nrow = t.nrow, n = t.n;
   const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
@@ -610,8 +610,8 @@ __global__ __launch_bounds__(256) void ef_transpose_kernel(const EfDev* __restri
       if (r < nrow && (unsigned)v < (unsigned)n) dst[(int64_t)v * nrow + r] = tile[tx][j];
     }
   } else {  // visiting -> storage
-    const T* src = WHICH == 1 ? (const T*)t.LT : (const T*)t.WcurT;
-    T* dst = WHICH == 1 ? (T*)t.Lrow : (T*)t.Wcur;
+    const T* src = (const T*)t.WcurT;
+    T* dst = (T*)t.Wcur;
     for (int j = ty; j < 64; j += 4) {
       const int c = c0 + j, r = r0 + tx;
       const int v = c < n ? inv[c] : -1;
@@ -704,61 +704,100 @@ __global__ void ef_grid_kernel(const EfDev* __restrict__ tab) {
 }
 
 // ---------------------------------------------------------------- repack
-// Rewrite the code bytes of committed superblocks from stored codes Lrow
-// [nrow][n] (row-major storage order), keeping the scale bytes (ef.py:130-176).
-// One thread per code byte of a superblock.
-__global__ void ef_repack_kernel(const EfDev* __restrict__ tab) {
-  const EfDev& T = tab[blockIdx.y];
-  const int ttype = T.ttype;
-  int lo_b, hi_b, bp;
-  switch (ttype) {
-    case CP_Q2_K: lo_b = 16; hi_b = 80; bp = 84; break;
-    case CP_Q3_K: lo_b = 0; hi_b = 96; bp = 110; break;
-    case CP_Q4_K: lo_b = 16; hi_b = 144; bp = 144; break;
-    case CP_Q5_K: lo_b = 16; hi_b = 176; bp = 176; break;
-    default: lo_b = 0; hi_b = 192; bp = 210; break;
-  }
-  const int64_t NB = (int64_t)T.nrow * (T.n / 256);
-  const int span = hi_b - lo_b;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t sb = t / span;
-  if (sb >= NB) return;
-  const int b = lo_b + (int)(t % span);
-  const uint8_t* c = T.Lrow + sb * 256;
-  uint32_t v;
+// Rewrite the code bytes of committed superblocks from the sweep's codes, keeping
+// the scale bytes (ef.py:130-176). The codes come straight from the visiting-order
+// store LT[inv[c]][r]: a workgroup takes 128 rows x one superblock column, stages
+// the 128 x 256 codes in LDS column by column (128 contiguous bytes of LT each), then
+// writes the superblocks' code bytes, two per thread.
+
+// Code byte b of one superblock from its codes c(k) (code of element k).
+template <class C>
+__device__ __forceinline__ uint32_t pack_code_byte(int ttype, const C& c, int b) {
   if (ttype == CP_Q2_K) {
-    int k = b - 16, base = (k >> 5) * 128 + (k & 31);
-    v = c[base] | c[base + 32] << 2 | c[base + 64] << 4 | c[base + 96] << 6;
-  } else if (ttype == CP_Q3_K) {
+    const int k = b - 16, base = (k >> 5) * 128 + (k & 31);
+    return c(base) | c(base + 32) << 2 | c(base + 64) << 4 | c(base + 96) << 6;
+  }
+  if (ttype == CP_Q3_K) {
     if (b < 32) {
-      v = 0;
-      for (int j = 0; j < 8; ++j) v |= ((c[32 * j + b] >> 2) & 1u) << j;
-    } else {
-      int k = b - 32, base = (k >> 5) * 128 + (k & 31);
-      v = (c[base] & 3) | (c[base + 32] & 3) << 2 | (c[base + 64] & 3) << 4 | (c[base + 96] & 3) << 6;
+      uint32_t v = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v |= ((c(32 * j + b) >> 2) & 1u) << j;
+      return v;
     }
-  } else if (ttype == CP_Q4_K) {
-    int k = b - 16, base = (k >> 5) * 64 + (k & 31);
-    v = (c[base] & 0xF) | (c[base + 32] & 0xF) << 4;
-  } else if (ttype == CP_Q5_K) {
+    const int k = b - 32, base = (k >> 5) * 128 + (k & 31);
+    return (c(base) & 3) | (c(base + 32) & 3) << 2 | (c(base + 64) & 3) << 4 | (c(base + 96) & 3) << 6;
+  }
+  if (ttype == CP_Q4_K) {
+    const int k = b - 16, base = (k >> 5) * 64 + (k & 31);
+    return (c(base) & 0xF) | (c(base + 32) & 0xF) << 4;
+  }
+  if (ttype == CP_Q5_K) {
     if (b < 48) {  // qh: bit q of byte j is code (32q + j) >= 16
-      v = 0;
-      for (int q = 0; q < 8; ++q) v |= (uint32_t)(c[32 * q + b - 16] >> 4) << q;
-    } else {
-      int k = b - 48, base = (k >> 5) * 64 + (k & 31);
-      v = (c[base] & 0xF) | (c[base + 32] & 0xF) << 4;
+      uint32_t v = 0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v |= (uint32_t)(c(32 * q + b - 16) >> 4) << q;
+      return v;
     }
-  } else {
-    if (b < 128) {
-      int h = b >> 6, k = b & 63;
-      int base = h * 128 + (k & 31) + (k >= 32 ? 32 : 0);
-      v = (c[base] & 0xF) | (c[base + 64] & 0xF) << 4;
+    const int k = b - 48, base = (k >> 5) * 64 + (k & 31);
+    return (c(base) & 0xF) | (c(base + 32) & 0xF) << 4;
+  }
+  if (b < 128) {  // Q6_K
+    const int h = b >> 6, k = b & 63;
+    const int base = h * 128 + (k & 31) + (k >= 32 ? 32 : 0);
+    return (c(base) & 0xF) | (c(base + 64) & 0xF) << 4;
+  }
+  const int k = b - 128, base = (k >> 5) * 128 + (k & 31);
+  return (c(base) >> 4) | (c(base + 32) >> 4) << 2 | (c(base + 64) >> 4) << 4 | (c(base + 96) >> 4) << 6;
+}
+
+__device__ __forceinline__ void code_span(int ttype, int* lo_b, int* hi_b, int* bp) {
+  switch (ttype) {
+    case CP_Q2_K: *lo_b = 16; *hi_b = 80; *bp = 84; break;
+    case CP_Q3_K: *lo_b = 0; *hi_b = 96; *bp = 110; break;
+    case CP_Q4_K: *lo_b = 16; *hi_b = 144; *bp = 144; break;
+    case CP_Q5_K: *lo_b = 16; *hi_b = 176; *bp = 176; break;
+    default: *lo_b = 0; *hi_b = 192; *bp = 210; break;
+  }
+}
+
+constexpr int kPackRows = 128;   // rows per workgroup: one 128-byte line of each LT column
+constexpr int kPackPitch = 132;  // LDS bytes per staged column: 33 words, so a wave's columns hit distinct banks
+
+__global__ __launch_bounds__(256) void ef_pack_kernel(const EfDev* __restrict__ tab) {
+  const EfDev& T = tab[blockIdx.y];
+  const int nrow = T.nrow, n = T.n, nsb = n / 256;
+  const int row_tiles = (nrow + kPackRows - 1) / kPackRows;
+  if ((int)blockIdx.x >= row_tiles * nsb) return;
+  const int rt = blockIdx.x / nsb, sb = blockIdx.x - rt * nsb;
+  const int r0 = rt * kPackRows, rows = nrow - r0 < kPackRows ? nrow - r0 : kPackRows;
+  __shared__ __align__(16) uint8_t codes[256 * kPackPitch];  // [column][row]
+  const int t = threadIdx.x;
+  {
+    const uint8_t* src = T.LT + (int64_t)T.inv[sb * 256 + t] * nrow + r0;
+    uint8_t* dst = codes + t * kPackPitch;
+    if ((nrow & 15) == 0) {  // 16-byte aligned runs; rows is a multiple of 16
+      for (int q = 0; q < rows / 16; ++q) {
+        const uint4 v = reinterpret_cast<const uint4*>(src)[q];
+        uint32_t* d = reinterpret_cast<uint32_t*>(dst + 16 * q);
+        d[0] = v.x;
+        d[1] = v.y;
+        d[2] = v.z;
+        d[3] = v.w;
+      }
     } else {
-      int k = b - 128, base = (k >> 5) * 128 + (k & 31);
-      v = (c[base] >> 4) | (c[base + 32] >> 4) << 2 | (c[base + 64] >> 4) << 4 | (c[base + 96] >> 4) << 6;
+      for (int i = 0; i < rows; ++i) dst[i] = src[i];
     }
   }
-  T.raw[sb * bp + b] = (uint8_t)v;
+  __syncthreads();
+  int lo_b, hi_b, bp;
+  code_span(T.ttype, &lo_b, &hi_b, &bp);
+  const int half = (hi_b - lo_b) / 2;  // byte pairs per superblock
+  for (int p = t; p < rows * half; p += 256) {
+    const int row = p / half, b = lo_b + 2 * (p - row * half);
+    auto c = [&](int k) -> uint32_t { return codes[k * kPackPitch + row]; };
+    const uint32_t v = pack_code_byte(T.ttype, c, b) | pack_code_byte(T.ttype, c, b + 1) << 8;
+    *reinterpret_cast<uint16_t*>(T.raw + ((int64_t)(r0 + row) * nsb + sb) * bp + b) = (uint16_t)v;
+  }
 }
 
 // ---------------------------------------------------------------- host driver
@@ -766,7 +805,7 @@ __global__ void ef_repack_kernel(const EfDev* __restrict__ tab) {
 static size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct EfLayout {
-  size_t WpT, E, WcurT, Wcur, LT, Lrow, dlT, mlT, inv, sbidx, end;
+  size_t WpT, E, WcurT, Wcur, LT, dlT, mlT, inv, sbidx, end;
 };
 
 static EfLayout ef_layout(int64_t nrow, int64_t n, size_t base) {
@@ -778,7 +817,6 @@ static EfLayout ef_layout(int64_t nrow, int64_t n, size_t base) {
   L.WcurT = o; o += a256(w * 4);
   L.Wcur = o; o += a256(w * 4);
   L.LT = o; o += a256(w);
-  L.Lrow = o; o += a256(w);
   L.dlT = o; o += a256((size_t)nrow * (n / 16) * 4);
   L.mlT = o; o += a256((size_t)nrow * (n / 16) * 4);
   L.inv = o; o += a256((size_t)n * 4);
@@ -882,7 +920,7 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
                          (int)t.nrow, (int)t.n, lo, hi};
     devs[i] = EfDev{t.x, t.qw, t.order, t.raw, t.recon, (float*)(base + L.WpT),
                     (float*)(base + L.WcurT), (float*)(base + L.Wcur), (uint8_t*)(base + L.LT),
-                    (uint8_t*)(base + L.Lrow), (float*)(base + L.dlT), mlT, (int*)(base + L.inv),
+                    (float*)(base + L.dlT), mlT, (int*)(base + L.inv),
                     (int*)(base + L.sbidx), (int)t.nrow, (int)t.n, t.ttype, sub};
     max_n = (int)t.n > max_n ? (int)t.n : max_n;
     max_rows = (int)t.nrow > max_rows ? (int)t.nrow : max_rows;
@@ -953,9 +991,8 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
       ef_sweep_mfma_kernel<BLK><<<dim3((unsigned)((max_rows + 63) / 64), (unsigned)count), 64, 0, st>>>(dtasks);
     CP_LAUNCHED("EF sweep");
     CP_PHASE(2);
-    ef_transpose_kernel<1><<<dim3(col_tiles, row_tiles, (unsigned)count), 256, 0, st>>>(dtab);
-    const int64_t max_nb = (int64_t)max_rows * (max_n / 256);
-    ef_repack_kernel<<<dim3((unsigned)((max_nb * 192 + 255) / 256), (unsigned)count), 256, 0, st>>>(dtab);
+    const int64_t pack_units = (int64_t)((max_rows + kPackRows - 1) / kPackRows) * (max_n / 256);
+    ef_pack_kernel<<<dim3((unsigned)pack_units, (unsigned)count), 256, 0, st>>>(dtab);
     if (it + 1 < n_iter)
       ef_transpose_kernel<2><<<dim3(col_tiles, row_tiles, (unsigned)count), 256, 0, st>>>(dtab);
     CP_LAUNCHED("EF repack");
