@@ -129,9 +129,11 @@ __device__ __forceinline__ void sweep_block(const SweepTask& tk, int i1, int r, 
 // by the columns of its 16-column piece onwards, so row cb (piece p = cb / 16)
 // holds block columns 16 p .. 63 from tile_base(p) + (cb % 16) * (64 - 16 p):
 // 10 KB instead of 16. sg[k][rl] / sm[k][rl] hold the committed grid step and
-// offset of column k of the current half block for the stripe's row rl,
-// staged in LDS so no global load sits on the column-to-column chain.
+// offset of column k of the current quarter block (kGridCols columns) for the
+// stripe's row rl, staged in LDS so no global load sits on the column-to-column
+// chain.
 constexpr int TILE_FLOATS = 16 * (64 + 48 + 32 + 16);
+constexpr int kGridCols = 16;  // block columns per staged part of the grid
 
 __device__ __forceinline__ constexpr int tile_base(int piece) {
   return piece == 0 ? 0 : piece == 1 ? 16 * 64 : piece == 2 ? 16 * (64 + 48) : 16 * (64 + 48 + 32);
@@ -179,7 +181,7 @@ __device__ __forceinline__ float bcast_group(float x, int own) {
 // Columns hb .. hb + 31 (one half block; sg / sm hold its grid). tile is the
 // compact diagonal tile; row cb holds columns 16 * (cb / 16) .. 63.
 template <int RS>
-__device__ __forceinline__ void sweep_half_split(const SweepTask& tk, int i1, int rr, int rl, int g,
+__device__ __forceinline__ void sweep_part_split(const SweepTask& tk, int i1, int rr, int rl, int g,
                                                  float (&tl)[RS], const float* tile,
                                                  const float (*sg)[RS], const float (*sm)[RS],
                                                  int hb) {
@@ -196,7 +198,7 @@ __device__ __forceinline__ void sweep_half_split(const SweepTask& tk, int i1, in
   float* pw = tk.WcurT + o0;
   uint8_t* pl = tk.LT + o0;
 #pragma unroll
-  for (int a = 0; a < 32; ++a) {
+  for (int a = 0; a < kGridCols; ++a) {
     const int cb = hb + a;
     const int own = cb / RS, i = cb % RS, p = cb / 16;
     // row cb of the tile, indexed by block column (entries below 16 p are not
@@ -228,20 +230,20 @@ __device__ __forceinline__ void sweep_half_split(const SweepTask& tk, int i1, in
   }
 }
 
-// The committed grid step / offset of block columns hb .. hb + 31 for the
-// stripe's rows: lane l covers row l % RS and every (64 / RS)-th column.
+// The committed grid step / offset of block columns hb .. hb + kGridCols - 1 for
+// the stripe's rows: lane l covers row l % RS and every (64 / RS)-th column.
 // load_grid issues the loads into registers, store_grid writes them to sg /
 // sm. sbo[k] = (storage sub-block of block column k) * nrow.
 template <int RS>
-struct GridHalf {
-  static constexpr int P = 64 / RS, NC = 32 / P;
+struct GridPart {
+  static constexpr int P = 64 / RS, NC = kGridCols / P;
   float d[NC], m[NC];
 };
 
 template <int RS>
 __device__ __forceinline__ void load_grid(const SweepTask& tk, const int* sbo, int hb, int l, int rr,
-                                          GridHalf<RS>& g) {
-  constexpr int P = GridHalf<RS>::P, NC = GridHalf<RS>::NC;
+                                          GridPart<RS>& g) {
+  constexpr int P = GridPart<RS>::P, NC = GridPart<RS>::NC;
   const int part = l / RS;
 #pragma unroll
   for (int k = 0; k < NC; ++k) g.d[k] = ld_lane(tk.dlT, (int64_t)sbo[hb + part + P * k] + rr);
@@ -255,8 +257,8 @@ __device__ __forceinline__ void load_grid(const SweepTask& tk, const int* sbo, i
 }
 
 template <int RS>
-__device__ __forceinline__ void store_grid(const GridHalf<RS>& g, int l, float (*sg)[RS], float (*sm)[RS]) {
-  constexpr int P = GridHalf<RS>::P, NC = GridHalf<RS>::NC;
+__device__ __forceinline__ void store_grid(const GridPart<RS>& g, int l, float (*sg)[RS], float (*sm)[RS]) {
+  constexpr int P = GridPart<RS>::P, NC = GridPart<RS>::NC;
   const int rl = l % RS, part = l / RS;
 #pragma unroll
   for (int k = 0; k < NC; ++k) {
@@ -352,15 +354,18 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
   // lanes past the last row work on the last row (and store its values again)
   const int rr = row0 + rl < nrow ? row0 + rl : nrow - 1;
   // one LDS buffer: the RS x 64 target transpose, then the compact diagonal
-  // U tile; the grid steps / offsets of half a block. About 18 KB in all for
-  // either stripe height (the grid arrays are sized for 32 rows), so a CU
-  // holds at most eight of these one-wave workgroups: the dispatcher fills
-  // CUs up to what fits, and a ninth or tenth wave on some CUs would leave
-  // others idle while the busy ones set the kernel's time.
+  // U tile; the grid steps / offsets of a quarter block. About 14.5 KB in all,
+  // so eight of these one-wave workgroups leave 44 KB of a CU's LDS free for a
+  // concurrent stream's workgroups (the factorization's GEMM and diagonal-block
+  // kernels need 34-37 KB), instead of the 10 KB a half-block staging left.
+  // At most two waves per SIMD: more on some SIMDs leaves others idle while the
+  // busy ones set the kernel's time. The 32-row variant's registers (over 170)
+  // already allow no more; the 16-row variant reserves a register to get there.
+  if constexpr (RS == 16) asm volatile("" ::: "v175");
   static_assert(RS * (B + 1) <= TILE_FLOATS, "target transpose fits the tile buffer");
   __shared__ __align__(16) float lds[TILE_FLOATS];
   __shared__ int sbo[B];
-  __shared__ float sg_[32][32], sm_[32][32];
+  __shared__ float sg_[kGridCols][32], sm_[kGridCols][32];
   float (*sg)[RS] = reinterpret_cast<float (*)[RS]>(&sg_[0][0]);
   float (*sm)[RS] = reinterpret_cast<float (*)[RS]>(&sm_[0][0]);
   float (*st)[B + 1] = reinterpret_cast<float (*)[B + 1]>(lds);
@@ -442,9 +447,9 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
     // the block's grid steps / offsets (both halves into registers) and the
     // compact diagonal tile share one round trip to memory; lane l fills
     // column 16 p + l of the tile rows of piece p
-    GridHalf<RS> g0, g1;
-    load_grid<RS>(tk, sbo, 0, l, rr, g0);
-    load_grid<RS>(tk, sbo, 32, l, rr, g1);
+    GridPart<RS> gp[64 / kGridCols];
+#pragma unroll
+    for (int q = 0; q < 64 / kGridCols; ++q) load_grid<RS>(tk, sbo, q * kGridCols, l, rr, gp[q]);
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       float u[16];
@@ -457,14 +462,13 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
         for (int a = 0; a < 16; ++a) lds[tile_base(p) + a * (64 - 16 * p) + l] = u[a];
       }
     }
-    store_grid<RS>(g0, l, sg, sm);
-    __syncthreads();
-    sweep_half_split<RS>(tk, i1, rr, rl, part, tl, lds, sg, sm, 0);
-    __syncthreads();
-    store_grid<RS>(g1, l, sg, sm);
-    __syncthreads();
-    sweep_half_split<RS>(tk, i1, rr, rl, part, tl, lds, sg, sm, 32);
-    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 64 / kGridCols; ++q) {
+      store_grid<RS>(gp[q], l, sg, sm);
+      __syncthreads();
+      sweep_part_split<RS>(tk, i1, rr, rl, part, tl, lds, sg, sm, q * kGridCols);
+      __syncthreads();
+    }
   }
 }
 
