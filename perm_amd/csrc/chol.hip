@@ -298,13 +298,58 @@ __device__ double pw_sum_f64(const double* a, int n, int stride) {
   return pw_sum_f64(a, n2, stride) + pw_sum_f64(a + (int64_t)n2 * stride, n - n2, stride);
 }
 
+// Leaves of numpy's pairwise sum over n values, in order: the recursion above
+// splits until a piece has at most 128 values. Returns the leaf count (at most
+// max_leaves written; n <= 128 * max_leaves / 2 keeps them all).
+__device__ int pw_leaves(int n, int max_leaves, int* off, int* len) {
+  int stack_off[32], stack_len[32], sp = 0, k = 0;
+  stack_off[sp] = 0;
+  stack_len[sp++] = n;
+  while (sp > 0) {
+    --sp;
+    const int o = stack_off[sp], m = stack_len[sp];
+    if (m <= 128) {
+      if (k < max_leaves) {
+        off[k] = o;
+        len[k] = m;
+      }
+      ++k;
+      continue;
+    }
+    int m2 = m / 2;
+    m2 -= m2 % 8;
+    stack_off[sp] = o + m2;  // right piece below the left one: leaves come out in order
+    stack_len[sp++] = m - m2;
+    stack_off[sp] = o;
+    stack_len[sp++] = m2;
+  }
+  return k;
+}
+
+// The pairwise tree combined from its leaf sums, in the recursion's order.
+__device__ double pw_combine(int n, const double* leaf, int& k) {
+  if (n <= 128) return leaf[k++];
+  int n2 = n / 2;
+  n2 -= n2 % 8;
+  const double a = pw_combine(n2, leaf, k);
+  return a + pw_combine(n - n2, leaf, k);
+}
+
+constexpr int kShiftLeaves = 1024;  // pairwise leaves summed in parallel (n <= 65536)
+
 // Diagonal of the act-ordered H in visiting order, then the damping shift
 // damp * mean + 1e-8 (mean replaced by 1 when not positive), as ef.py:64-69
-// computes it from np.mean(np.diag(Hp)). One thread per matrix.
+// computes it from np.mean(np.diag(Hp)). One block per matrix: the leaves of
+// the pairwise sum run on separate threads, then one thread combines them in
+// the recursion's order (same additions, same order as the serial sum).
 template <typename T>
-__global__ void fact_shift_kernel(const T* H, int n, int64_t sH, const int* order, int64_t sO,
-                                  const double* damp, double* diag_tmp, double* shift,
-                                  const int* active) {
+__global__ __launch_bounds__(256) void fact_shift_kernel(const T* H, int n, int64_t sH,
+                                                         const int* order, int64_t sO,
+                                                         const double* damp, double* diag_tmp,
+                                                         double* shift, const int* active) {
+  __shared__ int loff[kShiftLeaves], llen[kShiftLeaves];
+  __shared__ double lsum[kShiftLeaves];
+  __shared__ int nleaves;
   const int z = blockIdx.x;
   if (active && !active[z]) return;
   const T* h = H + z * sH;
@@ -314,16 +359,33 @@ __global__ void fact_shift_kernel(const T* H, int n, int64_t sH, const int* orde
     int p = o ? o[i] : i;
     dg[i] = (double)h[(int64_t)p * n + p];
   }
+  if (threadIdx.x == 0) nleaves = pw_leaves(n, kShiftLeaves, loff, llen);
   __syncthreads();
+  const int nl = nleaves;
+  if (nl <= kShiftLeaves) {
+    for (int k = threadIdx.x; k < nl; k += blockDim.x) lsum[k] = pw_sum_f64(dg + loff[k], llen[k], 1);
+    __syncthreads();
+  }
   if (threadIdx.x == 0) {
-    double mean = pw_sum_f64(dg, n, 1) / (double)n;
-    double base = mean > 0.0 ? mean : 1.0;
+    double total;
+    if (nl <= kShiftLeaves) {
+      int k = 0;
+      total = pw_combine(n, lsum, k);
+    } else {
+      total = pw_sum_f64(dg, n, 1);
+    }
+    const double mean = total / (double)n;
+    const double base = mean > 0.0 ? mean : 1.0;
     shift[z] = damp[z] * base + 1e-8;
   }
 }
 
-// A[i][j] = H[q_i][q_j] (+ shift on the diagonal) for i >= j, 0 above, with
+// A[i][j] = H[q_i][q_j] (+ shift on the diagonal) for i >= j, with
 // q_i = order[n-1-i]: the act_order gather and the index reversal in one pass.
+// Entries above the diagonal are not written: every reader of A takes the lower
+// triangle only (the Cholesky GEMMs' operands lie strictly below the diagonal,
+// the diagonal-block kernel loads i <= r and stores its own zeros, and the outer
+// updates already change the upper part of the tiles they straddle).
 // Element-wise form, for rows too long to stage.
 template <typename T>
 __global__ void fact_prepare_gather_kernel(const T* H, int n, int64_t sH, const int* order,
@@ -334,11 +396,8 @@ __global__ void fact_prepare_gather_kernel(const T* H, int n, int64_t sH, const 
   const int j = blockIdx.x * 64 + (threadIdx.x & 63);
   const int i = blockIdx.y * 4 + (threadIdx.x >> 6);
   if (i >= n || j >= n) return;
+  if (j > i) return;
   double* a = A + z * sA;
-  if (j > i) {
-    a[(int64_t)i * n + j] = 0.0;
-    return;
-  }
   const int* o = order ? order + z * sO : nullptr;
   int qi = o ? o[n - 1 - i] : n - 1 - i;
   int qj = o ? o[n - 1 - j] : n - 1 - j;
@@ -367,16 +426,16 @@ __global__ __launch_bounds__(256) void fact_prepare_kernel(const T* H, int n, in
   }
   __syncthreads();
   double* a = A + z * sA;
-  for (int j = threadIdx.x; j < n; j += blockDim.x) {
+  const int jend = min(n, i0 + R);  // columns up to the block's last row
+  for (int j = threadIdx.x; j < jend; j += blockDim.x) {
     const int qj = o ? o[n - 1 - j] : n - 1 - j;
     for (int r = 0; r < R && i0 + r < n; ++r) {
       const int i = i0 + r;
-      double v = 0.0;
       if (j <= i) {
-        v = (double)rows[(int64_t)r * n + qj];
+        double v = (double)rows[(int64_t)r * n + qj];
         if (j == i) v = v + shift[z];
+        a[(int64_t)i * n + j] = v;
       }
-      a[(int64_t)i * n + j] = v;
     }
   }
 }

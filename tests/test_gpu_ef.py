@@ -53,6 +53,28 @@ def test_factor_matches_closed_form(ef, n):
     assert np.abs(U.T @ U @ Hd - np.eye(n)).max() < 1e-9
 
 
+@pytest.mark.parametrize("n", [100, 1000, 3000])
+def test_factor_damping_shift_is_numpys_mean(ef, n):
+    """Diagonal H: U = diag(1 / sqrt(h + shift)) with correctly rounded sqrt and
+    division, so U equals numpy's bit for bit only if the damping shift does,
+    i.e. only if the mean of diag(H) is summed in numpy's pairwise order."""
+    _say(f"damping shift n={n}")
+    rng = np.random.default_rng(n)
+    h = 10.0 ** rng.uniform(-3, 7, n)
+    H = np.diag(h)
+    shift = 0.01 * np.mean(np.diag(H)) + 1e-8
+    seq = 0.0
+    for v in h:  # the plain left-to-right order: a different shift on this data
+        seq += v
+    if n > 128:
+        assert 0.01 * (seq / n) + 1e-8 != shift
+    Hd = torch.from_numpy(H).cuda()
+    U, used = ef.factor_dev(Hd, None, 0.01, out_dtype=torch.float64)
+    U = U.cpu().numpy()
+    assert used == [0.01]
+    assert np.array_equal(U, np.diag(1.0 / np.sqrt(h + shift)))
+
+
 def test_factor_with_order_and_f32_output(ef):
     n = 512
     H = correlated_hessian(n, 2048, seed=3)
