@@ -174,9 +174,13 @@ def build_res_keys(weights, dims, profiles=None):
 def optimize(weights, ttypes, qws, dims, rows_sample=16384, log=print):
     """Choose the res / ffn / vo permutations minimising the container objective
     (coldpress/perm/spacemaps/qwen3.py:284-355), with every objective evaluation on
-    the GPU: one batched pass per residual candidate (all residual-space tensors),
-    one for the ffn_down baselines of every layer, one for their candidates, and the
-    same two for attn_output.
+    the GPU. No candidate depends on another's objective value: the residual keys
+    come from column profiles, and the ffn_down / attn_output candidates act on the
+    unpermuted weights. So the search takes two device round trips: one for the
+    column profiles of every tensor involved, one for every objective item (each
+    residual candidate over all residual-space tensors, the ffn_down and attn_output
+    baselines and their candidates). The choices are then made in the reference's
+    order from those values.
 
     weights : {gguf_name: [nrow, ne0] float16/float32, numpy or torch}; host arrays are
               uploaded once and stay resident for the whole search
@@ -191,30 +195,20 @@ def optimize(weights, ttypes, qws, dims, rows_sample=16384, log=print):
     qdev = {n: torch.from_numpy(np.ascontiguousarray(q, dtype=np.float32)).cuda()
             if str(getattr(q, "dtype", "")) == "float32" else q for n, q in qws.items()}
     res_names = res_space_tensors(dev, dims)
-
-    def res_obj(perm):
-        pd = index_dev(perm, dims["d_model"]) if perm is not None else None
-        return _ordered_sum(tensor_err_many(
-            [dict(x=dev[n], ttype=ttypes[n], qw=qdev.get(n), perm=pd, rows_sample=rows_sample)
-             for n in res_names]))
-
-    base = res_obj(None)
-    res_perm, res_val, res_name = np.arange(dims["d_model"]), base, "identity"
-    profiles = dict(zip(res_names, col_log_rms_many([dev[n] for n in res_names])))
-    for kname, key in build_res_keys(dev, dims, profiles).items():
-        perm = np.argsort(key, kind="stable")
-        val = res_obj(perm)
-        log(f"  res sort[{kname}]: {val:.6g} ({(val / base - 1) * 100:+.2f}%)")
-        if val < res_val:
-            res_perm, res_val, res_name = perm, val, kname
-    log(f"  res -> {res_name} ({(res_val / base - 1) * 100:+.2f}%)")
-
     L = dims["n_layers"]
     hd, nkv, nh = dims["head_dim"], dims["n_kv"], dims["n_heads"]
     group = nh // nkv
     fns = [f"blk.{l}.ffn_down.weight" for l in range(L)]
     ons = [f"blk.{l}.attn_output.weight" for l in range(L)]
-    profs = col_log_rms_many([dev[fn] for fn in fns] + [dev[on] for on in ons])
+
+    # round trip 1: column profiles of the residual-space tensors and of every
+    # ffn_down / attn_output
+    profs = col_log_rms_many([dev[n] for n in res_names] + [dev[fn] for fn in fns]
+                             + [dev[on] for on in ons])
+    profiles = dict(zip(res_names, profs[:len(res_names)]))
+    profs = profs[len(res_names):]
+    keys = build_res_keys(dev, dims, profiles)
+    res_cands = [("identity", None)] + [(k, np.argsort(key, kind="stable")) for k, key in keys.items()]
     fcand = [np.argsort(p, kind="stable") for p in profs[:L]]
     heads_all, ocand = [], []
     for on, prof in zip(ons, profs[L:]):  # column sums are per column: slices share them
@@ -229,11 +223,30 @@ def optimize(weights, ttypes, qws, dims, rows_sample=16384, log=print):
             full[q * hd:(q + 1) * hd] = q * hd + heads[q // group]
         heads_all.append(heads)
         ocand.append(full)
-    errs = tensor_err_many(
-        [dict(x=dev[fn], ttype=ttypes[fn], qw=qdev.get(fn)) for fn in fns]
-        + [dict(x=dev[fn], ttype=ttypes[fn], qw=qdev.get(fn), perm=p) for fn, p in zip(fns, fcand)]
-        + [dict(x=dev[on], ttype=ttypes[on], qw=qdev.get(on)) for on in ons]
-        + [dict(x=dev[on], ttype=ttypes[on], qw=qdev.get(on), perm=p) for on, p in zip(ons, ocand)])
+
+    # round trip 2: every objective item of the search in one batched pass
+    items = []
+    for _, perm in res_cands:
+        pd = index_dev(perm, dims["d_model"]) if perm is not None else None
+        items += [dict(x=dev[n], ttype=ttypes[n], qw=qdev.get(n), perm=pd, rows_sample=rows_sample)
+                  for n in res_names]
+    items += ([dict(x=dev[fn], ttype=ttypes[fn], qw=qdev.get(fn)) for fn in fns]
+              + [dict(x=dev[fn], ttype=ttypes[fn], qw=qdev.get(fn), perm=p) for fn, p in zip(fns, fcand)]
+              + [dict(x=dev[on], ttype=ttypes[on], qw=qdev.get(on)) for on in ons]
+              + [dict(x=dev[on], ttype=ttypes[on], qw=qdev.get(on), perm=p) for on, p in zip(ons, ocand)])
+    errs = tensor_err_many(items)
+    nr = len(res_names)
+    res_vals = [_ordered_sum(errs[k * nr:(k + 1) * nr]) for k in range(len(res_cands))]
+    errs = errs[len(res_cands) * nr:]
+
+    base = res_vals[0]
+    res_perm, res_val, res_name = np.arange(dims["d_model"]), base, "identity"
+    for (kname, perm), val in zip(res_cands[1:], res_vals[1:]):
+        log(f"  res sort[{kname}]: {val:.6g} ({(val / base - 1) * 100:+.2f}%)")
+        if val < res_val:
+            res_perm, res_val, res_name = perm, val, kname
+    log(f"  res -> {res_name} ({(res_val / base - 1) * 100:+.2f}%)")
+
     fb_all, fv_all = errs[0:L], errs[L:2 * L]
     ob_all, ov_all = errs[2 * L:3 * L], errs[3 * L:4 * L]
     ffn_perms, ffn_val, ffn_base = [], 0.0, 0.0
