@@ -43,10 +43,11 @@ struct SweepTask {
   float* WcurT;
   uint8_t* LT;
   int nrow, n, lo, hi;
+  int first;  // index of the task's first stripe in the row-stripe sweep's item list
 };
 
 // Up to kTasksPerLaunch tensors travel by value in the kernel arguments.
-constexpr int kTasksPerLaunch = 48;
+constexpr int kTasksPerLaunch = 44;
 struct SweepBatch {
   SweepTask t[kTasksPerLaunch];
 };
@@ -342,12 +343,45 @@ struct StripeLayout<16> {
   __device__ static int col(int v, int l) { return 16 * (v >> 2) + (l & 15); }
 };
 
+// Items are the stripes of every task, task by task (tasks[k].first is the
+// first item of task k). With xcd_runs set (every task of the call has the same
+// n, so items are equally long), each XCD takes one contiguous run of items:
+// workgroup w runs on XCD w % 8, so item = (w % 8) * per + w / 8. The stripes
+// resident on an XCD then belong to a few tensors -- tensors sharing one H share
+// one U -- and read the same strips of U through that XCD's L2 instead of every
+// XCD's L2 holding strips of every tensor. Otherwise item = w, in the table's
+// longest-first order.
+__device__ __forceinline__ int sweep_item(const SweepTask* tasks, int count, int total, bool xcd_runs,
+                                          int* task) {
+  const int w = (int)blockIdx.x;
+  int item = w;
+  if (xcd_runs) {
+    const int per = (total + 7) / 8;
+    item = (w % 8) * per + w / 8;
+  }
+  if (item >= total) return -1;
+  int lo = 0, hi = count - 1;  // last task with first <= item
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (tasks[mid].first <= item)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  *task = lo;
+  return item - tasks[lo].first;
+}
+
 template <int RS>
-__global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* __restrict__ tasks) {
+__global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* __restrict__ tasks, int count,
+                                                            int total, int xcd_runs) {
   constexpr int B = 64, G = 8, NV = StripeLayout<RS>::NV, CPP = B * RS / 64;
   typedef float fv __attribute__((ext_vector_type(NV)));
-  const SweepTask tk = tasks[blockIdx.y];
-  const int row0 = blockIdx.x * RS;
+  int ti;
+  const int stripe = sweep_item(tasks, count, total, xcd_runs != 0, &ti);
+  if (stripe < 0) return;
+  const SweepTask tk = tasks[ti];
+  const int row0 = stripe * RS;
   if (row0 >= tk.nrow) return;
   const int l = threadIdx.x, rl = l % RS, part = l / RS;
   const int nrow = tk.nrow, n = tk.n;
@@ -950,6 +984,20 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     ++g.count;
     g.max_nb = nb > g.max_nb ? nb : g.max_nb;
   }
+  // row-stripe sweep items: 32-row stripes unless they would leave SIMDs with
+  // fewer than two waves (256 CUs x 4)
+  int64_t stripes32 = 0;
+  for (int i = 0; i < count; ++i) stripes32 += (ts[i].nrow + 31) / 32;
+  const int RS = stripes32 >= 2 * 1024 ? 32 : 16;
+  int64_t total_stripes = 0;
+  bool same_n = true;
+  for (int k = 0; k < count; ++k) {
+    SweepTask& tk = tasks[by_len[k]];
+    tk.first = (int)total_stripes;
+    total_stripes += (tk.nrow + RS - 1) / RS;
+    same_n = same_n && tk.n == tasks[by_len[0]].n;
+  }
+  if (total_stripes > ((int64_t)1 << 30)) return set_error(CP_ERR_SHAPE, "too many row stripes");
   for (int c0 = 0; c0 < count; c0 += kTasksPerLaunch) {
     const int cn = count - c0 < kTasksPerLaunch ? count - c0 : kTasksPerLaunch;
     SweepBatch b;
@@ -962,9 +1010,6 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     for (int i = 0; i < cn; ++i) b.t[i] = devs[by_kind[c0 + i]];
     ef_dev_store_kernel<<<1, 64, 0, st>>>(b, cn, dtab + c0);
   }
-  // 32-row stripes unless they would leave SIMDs with fewer than two waves (256 CUs x 4)
-  int64_t stripes32 = 0;
-  for (int i = 0; i < count; ++i) stripes32 += (ts[i].nrow + 31) / 32;
   const unsigned col_tiles = (unsigned)((max_n + 63) / 64), row_tiles = (unsigned)((max_rows + 63) / 64);
   ef_index_kernel<<<dim3((unsigned)((max_n + 255) / 256), (unsigned)count), 256, 0, st>>>(dtab);
   ef_transpose_kernel<0><<<dim3(col_tiles, row_tiles, (unsigned)count), 256, 0, st>>>(dtab);
@@ -987,10 +1032,12 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     CP_PHASE(1);
     if (mode == CP_EF_EXACT_VALU)
       ef_sweep_exact_kernel<BLK><<<dim3((unsigned)((max_rows + 255) / 256), (unsigned)count), 256, 0, st>>>(dtasks);
-    else if (mode == CP_EF_EXACT && stripes32 >= 2 * 1024)
-      ef_sweep_rows_kernel<32><<<dim3((unsigned)((max_rows + 31) / 32), (unsigned)count), 64, 0, st>>>(dtasks);
+    else if (mode == CP_EF_EXACT && RS == 32)
+      ef_sweep_rows_kernel<32><<<(unsigned)(8 * ((total_stripes + 7) / 8)), 64, 0, st>>>(
+          dtasks, count, (int)total_stripes, same_n ? 1 : 0);
     else if (mode == CP_EF_EXACT)
-      ef_sweep_rows_kernel<16><<<dim3((unsigned)((max_rows + 15) / 16), (unsigned)count), 64, 0, st>>>(dtasks);
+      ef_sweep_rows_kernel<16><<<(unsigned)(8 * ((total_stripes + 7) / 8)), 64, 0, st>>>(
+          dtasks, count, (int)total_stripes, same_n ? 1 : 0);
     else
       ef_sweep_mfma_kernel<BLK><<<dim3((unsigned)((max_rows + 63) / 64), (unsigned)count), 64, 0, st>>>(dtasks);
     CP_LAUNCHED("EF sweep");
