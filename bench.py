@@ -32,6 +32,11 @@ METRIC = "EF k-quant encode Mweights/s (Q2_K) + Hessian X^T·X TFLOP/s, 1 GPU"
 ROWS = 65536
 PEAK_BF16_TFLOPS = 2516.6
 PEAK_FP32_TFLOPS = 157.3
+# HBM bytes per ef_sweep_rows_kernel launch of the 28-layer exact-mode workload (mean of
+# the sequential pass's six launches), from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs,
+# each scaled by what the counter reads for a plain 1 GiB copy (`--workload copy`):
+# FETCH_SIZE x 2.0, WRITE_SIZE x 1.0. Source: profiles/ef_sweep_rows_qwen3-0.6b_q2k_pmc.md.
+SWEEP_TRAFFIC_BYTES = 10.594e9
 
 
 def log(msg):
@@ -282,6 +287,31 @@ def perm_main(args):
     print(json.dumps(result))
 
 
+def copy_main(args):
+    """A plain elementwise device copy of 1 GiB (read 1 GiB, write 1 GiB) per step: the
+    known-size kernel against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters are
+    scaled into HBM bytes."""
+    import torch
+    nbytes = 1 << 30
+    x = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(args.warmup):
+        torch.mul(x, 1.0, out=y)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        torch.mul(x, 1.0, out=y)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    gbs = 2 * nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "device copy GB/s (HBM byte-counter calibration)", "value": gbs, "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic", "config": {"workload": "copy", "kernel": "torch.mul(x, 1.0, out=y)",
+                                        "bytes_read": nbytes, "bytes_written": nbytes}}))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -292,13 +322,14 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ef-mode", choices=["mfma", "exact"], default="exact",
                     help="cross-block error propagation: MFMA GEMM or the reference's exact order")
-    ap.add_argument("--workload", choices=["ef", "perm-search"], default="ef",
+    ap.add_argument("--workload", choices=["ef", "perm-search", "copy"], default="ef",
                     help="ef: the EF encode + Hessians line (default); perm-search: the PERM "
-                         "space-map search on the GPU objective")
+                         "space-map search on the GPU objective; copy: a plain 1 GiB device "
+                         "copy, the calibration run for the HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         msg = (f"bench.py runs on one GPU only (got --gpus {args.gpus}); the encoder path "
-               f"shards by tensor / row stripe with no exchange, see DESIGN.md")
+               f"shards by tensor / row stripe with no exchange between GPUs")
         print(msg, file=sys.stderr)
         print(json.dumps({"metric": METRIC, "error": msg}))
         sys.exit(2)
@@ -310,6 +341,9 @@ def main():
         sys.exit("bench.py needs a GPU")
     if args.workload == "perm-search":
         perm_main(args)
+        return
+    if args.workload == "copy":
+        copy_main(args)
         return
     lib = _lib.load()
     dev = "cuda"
@@ -391,10 +425,12 @@ def main():
         avg_ms = ph[2] / sweep_launches
         flops_per_launch = ef_flops / sweep_launches
         ach = flops_per_launch / (avg_ms * 1e-3) / 1e12
+        exact_full = mode == _lib.CP_EF_EXACT and layers == 28
         roof = {"kernel": ("ef_sweep_mfma_kernel" if mode == _lib.CP_EF_MFMA
                            else "ef_sweep_rows_kernel"), "bound": "mfma", "achieved": ach,
                 "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_FP32_TFLOPS,
-                "traffic": None, "avg_launch_ms": avg_ms, "launches_per_step": sweep_launches}
+                "traffic": SWEEP_TRAFFIC_BYTES if exact_full else None,
+                "avg_launch_ms": avg_ms, "launches_per_step": sweep_launches}
 
     result = {
         "metric": METRIC,
