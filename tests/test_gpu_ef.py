@@ -204,6 +204,41 @@ def test_many_shares_factor_and_matches_single(ef):
         assert torch.equal(out[nm][0], raw1) and torch.equal(out[nm][1], rec1)
 
 
+def _oracle_items(specs):
+    """(W, tt, qw, H, order, U) per spec (nrow, n, tt, seed), with the oracle's own
+    float32 factor and order, so the GPU sweep must reproduce the oracle bit for bit."""
+    out = []
+    for nrow, n, tt, seed in specs:
+        W = heavy_tailed(nrow, n, seed=seed)
+        H = correlated_hessian(n, 4 * n, seed=seed + 100)
+        qw = (np.diag(H) / (4 * n)).astype(F32)
+        order = E.act_order(H, stable=True)
+        U = E.inv_upper_factor(H[np.ix_(order, order)], 0.01).astype(F32)
+        out.append((W, tt, qw, H, order, U))
+    return out
+
+
+@pytest.mark.parametrize("specs", [
+    # one size: the sweep hands each XCD a contiguous run of stripes; uneven row
+    # counts and partial stripes put task boundaries anywhere in those runs
+    [(70, 512, "Q2_K", 1), (200, 512, "Q3_K", 2), (33, 512, "Q2_K", 3), (129, 512, "Q6_K", 4)],
+    # mixed sizes in one call: stripes in the table's longest-first order
+    [(96, 768, "Q2_K", 5), (70, 512, "Q4_K", 6), (40, 1024, "Q5_K", 7), (64, 256, "Q2_K", 8)],
+], ids=["same_n", "mixed_n"])
+def test_batched_sweep_bit_exact_vs_oracle(ef, specs):
+    """Several tensors in one EF call: every tensor's bytes equal the oracle's."""
+    _say(f"batched sweep {[s[:3] for s in specs]}")
+    data = _oracle_items(specs)
+    items = [{"ttype": tt, "x": torch.from_numpy(W).cuda(), "qw": torch.from_numpy(qw).cuda(),
+              "U": torch.from_numpy(U).cuda(), "order": torch.from_numpy(order.astype(np.int32)).cuda()}
+             for W, tt, qw, _, order, U in data]
+    got = ef.ef_encode_dev(items, 2, ef.MODES["exact"])
+    for (W, tt, qw, H, _, U), (raw, rec) in zip(data, got):
+        want_raw, want_rec = E.ef_encode(W, tt, qw, H, n_iter=2, U=U, stable_order=True)
+        assert np.array_equal(raw.cpu().numpy(), want_raw), tt
+        assert np.array_equal(rec.cpu().numpy(), want_rec), tt
+
+
 def test_factor_async_equals_blocking(ef):
     Hs = [correlated_hessian(320, 1280, seed=s) for s in range(3)]
     Hb = torch.from_numpy(np.stack(Hs)).cuda()
