@@ -287,6 +287,269 @@ def perm_main(args):
     print(json.dumps(result))
 
 
+FORMAT_TYPES = ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0"]
+
+
+def formats_cpu_baseline(W0, qws0, Hs):
+    """The numpy oracle (a port of kquant.py / scale_tune.py / hessians.py) on samples:
+    64 rows of layer 0's ffn_up per container (encode + decode), one 1024 x 1024 Hessian
+    (pack + expand); extrapolated per weight / per entry."""
+    import numpy as np
+    from oracle import hess_oracle as Ho
+    from oracle import kquant_oracle as Ko
+    x = W0["ffn_up"][:64].cpu().numpy()
+    qw = qws0[x.shape[1]].cpu().numpy()
+    per_w = {}
+    spent = 0.0
+    for tt in FORMAT_TYPES:
+        t0 = time.perf_counter()
+        raw = Ko.QUANTIZE[tt](x, None if tt == "Q8_0" else qw)
+        Ko.DEQUANTIZE[tt](raw, x.shape[1])
+        dt = time.perf_counter() - t0
+        spent += dt
+        per_w[tt] = dt / x.size
+    H = Hs[1024][0].cpu().numpy()
+    t0 = time.perf_counter()
+    H16, dg, hs = Ho.h2_pack(H)
+    Ho.h2_expand(H16, hs, dg)
+    h2_dt = time.perf_counter() - t0
+    spent += h2_dt
+    return per_w, h2_dt / H.size, spent
+
+
+def formats_main(args):
+    """Data-format rows on the Qwen3-0.6B-shaped layer set (28 layers, 196 tensors,
+    440,401,920 weights, imatrix-style qw): encode and decode of all six containers, the
+    linear form of the five k-quants (extract A / B / d / dmin, then reconstruct), and the
+    Hessian storage format (pack to float16 + diag32 + hscale, expand to float64) of the
+    112 Hessians' shapes. One step = every format over the whole set."""
+    import numpy as np
+    import torch
+    from perm_amd import _lib, hessians, kquant, scale_tune
+    from perm_amd import workloads as wl
+    layers = args.layers
+    lib = _lib.load()
+    W = [wl.qwen3_layer_weights(l, seed=0, device="cuda") for l in range(layers)]
+    g = torch.Generator(device="cuda").manual_seed(7)
+    qws = {n: torch.rand(n, device="cuda", generator=g) + 0.05 for n in (1024, 2048, 3072)}
+    xs = [(w[name], qws[n]) for w in W for name, _r, n, _f in wl.QWEN3_06B_LAYER]
+    total_w = sum(x.numel() for x, _ in xs)
+    # Hessian-shaped float32 matrices with entries past float16's range (the scaled path)
+    Hs = {1024: torch.randn((2 * layers, 1024, 1024), device="cuda", generator=g) * 4e4,
+          2048: torch.randn((layers, 2048, 2048), device="cuda", generator=g) * 4e4,
+          3072: torch.randn((layers, 3072, 3072), device="cuda", generator=g) * 4e4}
+    h_entries = sum(Hb.numel() for Hb in Hs.values())
+    dec_out = [torch.empty_like(x) for x, _ in xs]
+    h16 = {d: torch.empty(Hb.shape, dtype=torch.float16, device="cuda") for d, Hb in Hs.items()}
+    hdg = {d: torch.empty(Hb.shape[:2], dtype=torch.float32, device="cuda") for d, Hb in Hs.items()}
+    hsc = {d: torch.empty(Hb.shape[0], dtype=torch.float32, device="cuda") for d, Hb in Hs.items()}
+    hexp = torch.empty(3072 * 3072, dtype=torch.float64, device="cuda")
+    hs_host = {}  # the per-matrix scales as a reader holds them (from the file: host values)
+    ws = _lib.workspace(256, torch.device("cuda"))
+    torch.cuda.synchronize()
+
+    def run_type(tt, check=False):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+        ev[0].record()
+        raws = [kquant.quantize_dev(tt, x, None if tt == "Q8_0" else q) for x, q in xs]
+        ev[1].record()
+        for (x, _), raw, out in zip(xs, raws, dec_out):
+            kquant.dequantize_dev(tt, raw, x.shape[1], out=out)
+        ev[2].record()
+        lins = []
+        if tt != "Q8_0":
+            lins = [scale_tune.extract_linear_dev(raw, tt, x.shape[1]) for (x, _), raw in zip(xs, raws)]
+        ev[3].record()
+        recs = [scale_tune._reconstruct_dev(L["d"], L["dmin"], L["A"], L["B"], L["shape"]) for L in lins]
+        ev[4].record()
+        torch.cuda.synchronize()
+        if check:  # the linear form reconstructs exactly what the decoder gives
+            for i in (0, len(xs) - 1):
+                if recs and not torch.equal(torch.nan_to_num(recs[i]), torch.nan_to_num(dec_out[i])):
+                    raise RuntimeError(f"{tt}: linear-form reconstruction differs from the decoder")
+        raw_bytes = sum(r.numel() for r in raws)
+        return [ev[k].elapsed_time(ev[k + 1]) for k in range(4)], raw_bytes
+
+    def run_h2():
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ev[0].record()
+        for d, Hb in Hs.items():
+            for i in range(Hb.shape[0]):
+                _lib.check(lib.cp_h2_pack(_lib.ptr(Hb[i]), d, _lib.ptr(h16[d][i]), _lib.ptr(hdg[d][i]),
+                                          _lib.ptr(hsc[d][i:i + 1]), _lib.ptr(ws), ws.numel(),
+                                          _lib.stream_ptr()))
+        ev[1].record()
+        for d, Hb in Hs.items():
+            out = hexp[:d * d].view(d, d)
+            for i in range(Hb.shape[0]):
+                _lib.check(lib.cp_h2_expand(_lib.ptr(h16[d][i]), 1, d, hs_host[d][i],
+                                            _lib.ptr(hdg[d][i]), _lib.ptr(out), _lib.stream_ptr()))
+        ev[2].record()
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
+
+    for tt in FORMAT_TYPES:
+        run_type(tt, check=True)
+    for d, Hb in Hs.items():
+        hs_host[d] = [1.0] * Hb.shape[0]
+    run_h2()
+    hs_host.update({d: hsc[d].cpu().tolist() for d in Hs})
+    log(f"formats: {len(xs)} tensors, {total_w} weights, {h_entries} Hessian entries")
+    acc = {tt: np.zeros(4) for tt in FORMAT_TYPES}
+    raw_b = {}
+    h2 = np.zeros(2)
+    for _ in range(args.warmup):
+        for tt in FORMAT_TYPES:
+            run_type(tt)
+        run_h2()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        for tt in FORMAT_TYPES:
+            ms, raw_b[tt] = run_type(tt)
+            acc[tt] += ms
+        h2 += np.array(run_h2())
+        log(f"step {k + 1}/{args.steps} done")
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    per = {}
+    enc_dec_ms = 0.0
+    dec_bytes, dec_ms = 0.0, 0.0
+    for tt in FORMAT_TYPES:
+        e, dcd, ex, rc = acc[tt] / args.steps
+        enc_dec_ms += e + dcd
+        dec_bytes += raw_b[tt] + 4.0 * total_w
+        dec_ms += dcd
+        per[tt] = {"encode_ms": e, "decode_ms": dcd, "encode_mweights_per_s": total_w / e / 1e3,
+                   "decode_gb_per_s": (raw_b[tt] + 4.0 * total_w) / (dcd * 1e-3) / 1e9,
+                   "container_bytes": raw_b[tt]}
+        if tt != "Q8_0":
+            nsb = total_w // 256
+            lin_bytes = raw_b[tt] + 4.0 * total_w + 8.0 * nsb  # in: bytes; out: A, B int16, d, dmin
+            per[tt]["linear_extract_ms"] = ex
+            per[tt]["linear_extract_gb_per_s"] = lin_bytes / (ex * 1e-3) / 1e9
+            per[tt]["linear_reconstruct_ms"] = rc
+            per[tt]["linear_reconstruct_gb_per_s"] = (4.0 * total_w + 8.0 * nsb + 4.0 * total_w) / (rc * 1e-3) / 1e9
+    pack_ms, expand_ms = h2 / args.steps
+    h2_res = {"matrices": sum(Hb.shape[0] for Hb in Hs.values()), "entries": h_entries,
+              "pack_ms": pack_ms, "pack_gb_per_s": 6.0 * h_entries / (pack_ms * 1e-3) / 1e9,
+              "expand_ms": expand_ms, "expand_gb_per_s": 10.0 * h_entries / (expand_ms * 1e-3) / 1e9}
+    value = len(FORMAT_TYPES) * total_w / (enc_dec_ms * 1e-3) / 1e6
+    dec_bw = dec_bytes / (dec_ms * 1e-3) / 1e9
+    roof = {"kernel": "kq_decode_kernel (all six containers)", "bound": "hbm", "achieved": dec_bw,
+            "peak": 8000.0, "unit": "GB/s", "frac": dec_bw / 8000.0, "traffic": None,
+            "avg_launch_ms": dec_ms / (len(FORMAT_TYPES) * len(xs)),
+            "launches_per_step": len(FORMAT_TYPES) * len(xs),
+            "note": "algorithmic bytes per decode: the container bytes read + 4 B per weight "
+                    "written; the encodes are VALU-bound (the make_q*_quants candidate searches)"}
+    result = {
+        "metric": "container codec encode+decode Mweights/s (Q2_K..Q6_K, Q8_0), 1 GPU",
+        "value": value, "unit": "Mweights/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": wall_ms, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random-init weights, random positive qw; Hessian-shaped random "
+                "float32 matrices past float16's range; generated on device)",
+        "config": {"workload": "qwen3-0.6b-shaped 28-layer tensor set, every container",
+                   "layers": layers, "tensors": len(xs), "weights": total_w,
+                   "containers": FORMAT_TYPES, "qw": "random positive (none for Q8_0)",
+                   "hessians": h2_res["matrices"]},
+        "formats": per, "hessian_storage": h2_res, "roofline": roof,
+    }
+    if not args.no_cpu_baseline:
+        per_w, h2_per_entry, spent = formats_cpu_baseline(W[0], qws, Hs)
+        cpu_s = sum(per_w.values()) * total_w
+        result["cpu_baseline"] = {
+            "value": len(FORMAT_TYPES) * total_w / cpu_s / 1e6, "unit": "Mweights/s", "cores": 1,
+            "kind": "port",
+            "sample": (f"numpy oracle QUANTIZE + DEQUANTIZE (port of kquant.py) on 64 rows of layer "
+                       f"0's ffn_up per container and the h2 pack + expand of one 1024x1024 matrix "
+                       f"({spent:.1f} s of CPU work), extrapolated per weight to the six containers "
+                       f"over {total_w} weights (est. {cpu_s:.0f} s); single-threaded numpy"),
+            "host_cpus": os.cpu_count()}
+        result["cpu_baseline"]["hessian_storage_entries_per_s"] = 1.0 / h2_per_entry
+        result["gpu_over_cpu"] = value / result["cpu_baseline"]["value"]
+    print(json.dumps(result))
+
+
+def gguf_main(args):
+    """The encode_gguf driver (coldpress/ef.py:223-317) end to end on a synthetic
+    Qwen3-0.6B artifact written to a temporary directory: the f16 GGUF (token_embd
+    151936 x 1024 plus 28 layers x 7 tensors), the stock quant (Q6_K embedding, Q3_K
+    attention, Q2_K elsewhere, encoded on the GPU) and the per-family Hessian files
+    (H = X^T X over 16384 Student-t bf16 rows per family, stored in the float16 format).
+    One step = one encode_gguf call: read the f16 weights and the Hessians, EF every
+    tensor with a Hessian (act order, fp64 factor, two iterations), weighted RTN of the
+    embedding, write the output GGUF."""
+    import shutil
+    import tempfile
+    import numpy as np
+    import torch
+    from perm_amd import ef as gef
+    from perm_amd import gates, hessians, kquant
+    from perm_amd import workloads as wl
+    from perm_amd.gguffile import GGUFWriter, ValueType
+    layers = args.layers
+    tmp = tempfile.mkdtemp(prefix="cp_gguf_bench_")
+    try:
+        f16, stock, hdir, out = (os.path.join(tmp, k) for k in ("f16.gguf", "stock.gguf", "hess", "ef.gguf"))
+        w = wl.qwen3_gguf_weights(layers=layers, device="cuda")
+        typemap = wl.qwen3_mixed_typemap(w.keys())
+        total_w = sum(t.numel() for t in w.values())
+        wr = GGUFWriter(f16, "qwen3")
+        wr.add_kv("qwen3.block_count", layers, ValueType.UINT32)
+        for name, t in w.items():
+            wr.add_tensor(name, t.cpu().numpy())
+        wr.write()
+        wr = GGUFWriter(stock, "qwen3")
+        wr.add_kv("qwen3.block_count", layers, ValueType.UINT32)
+        for name, t in w.items():
+            wr.add_tensor(name, kquant.quantize_dev(typemap[name], t.float().contiguous()).cpu().numpy(),
+                          typemap[name])
+        wr.write()
+        rows = 16384
+        fams = {}
+        for l in range(layers):
+            for i, (fam, d) in enumerate(wl.QWEN3_06B_FAMILIES.items()):
+                X = wl.student_t_activations(rows, d, nu=4.0, seed=1000 * l + i, device="cuda")
+                fams[f"blk.{l}.{fam}"] = {"H": hessians.xtx_accumulate(X), "n": rows}
+        hessians.save_hessians(fams, hdir)
+        del fams, w
+        torch.cuda.synchronize()
+        log(f"artifact: {total_w} weights, {4 * layers} Hessian files in {tmp}")
+        quiet = (lambda *_: None)
+        for _ in range(args.warmup):
+            gef.encode_gguf(f16, stock, hdir, out, log=quiet)
+        t0 = time.perf_counter()
+        for k in range(args.steps):
+            stats = gef.encode_gguf(f16, stock, hdir, out, log=quiet)
+            log(f"step {k + 1}/{args.steps} done")
+        torch.cuda.synchronize()
+        sec = (time.perf_counter() - t0) / args.steps
+        rep = gates.byte_parity(out, stock)
+        modes = {}
+        for st in stats.values():
+            modes[st["mode"]] = modes.get(st["mode"], 0) + 1
+        med = float(np.median([st["rel_err_vs_stock"] for st in stats.values()]))
+        value = total_w / sec / 1e6
+        result = {
+            "metric": "encode_gguf end-to-end Mweights/s (Qwen3-0.6B-shaped artifact), 1 GPU",
+            "value": value, "unit": "Mweights/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": sec * 1e3, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (random-init f16 weights, Student-t bf16 activations for the "
+                    "Hessians; written to a temporary directory)",
+            "config": {"workload": "encode_gguf, qwen3-0.6b-shaped artifact", "layers": layers,
+                       "tensors": len(stats), "weights": total_w,
+                       "containers": "Q6_K token_embd, Q3_K attention, Q2_K elsewhere",
+                       "hessian_files": 4 * layers, "hessian_rows": rows, "n_iter": 2},
+            "modes": modes, "median_rel_err_vs_stock": med,
+            "byte_parity": {"passed": rep["passed"], "total_final": rep["total_final"],
+                            "total_stock": rep["total_stock"]},
+            "roofline": None,
+        }
+        print(json.dumps(result))
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 def copy_main(args):
     """A plain elementwise device copy of 1 GiB (read 1 GiB, write 1 GiB) per step: the
     known-size kernel against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters are
@@ -322,10 +585,13 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ef-mode", choices=["mfma", "exact"], default="exact",
                     help="cross-block error propagation: MFMA GEMM or the reference's exact order")
-    ap.add_argument("--workload", choices=["ef", "perm-search", "copy"], default="ef",
+    ap.add_argument("--workload", choices=["ef", "perm-search", "formats", "gguf", "copy"],
+                    default="ef",
                     help="ef: the EF encode + Hessians line (default); perm-search: the PERM "
-                         "space-map search on the GPU objective; copy: a plain 1 GiB device "
-                         "copy, the calibration run for the HBM byte counters")
+                         "space-map search on the GPU objective; formats: every container's "
+                         "codec, the linear form and the Hessian storage format; gguf: the "
+                         "encode_gguf driver end to end; copy: a plain "
+                         "1 GiB device copy, the calibration run for the HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         msg = (f"bench.py runs on one GPU only (got --gpus {args.gpus}); the encoder path "
@@ -344,6 +610,12 @@ def main():
         return
     if args.workload == "copy":
         copy_main(args)
+        return
+    if args.workload == "formats":
+        formats_main(args)
+        return
+    if args.workload == "gguf":
+        gguf_main(args)
         return
     lib = _lib.load()
     dev = "cuda"

@@ -21,19 +21,30 @@ constexpr float kFp16SafeMax = 32768.0f;
 
 // max |x| over the matrix: non-negative floats order like their bit patterns, so an
 // unsigned atomic max on the bits is exact and order-free. amax_bits starts at 0.
+// One atomic per block (the waves' maxima meet in LDS first): atomics on one address
+// serialize, so their count, not the reads, would otherwise set the time.
+constexpr int kAbsmaxBlocks = 512;
+
 __global__ __launch_bounds__(256) void h2_absmax_kernel(const float* __restrict__ H, int64_t count,
                                                         unsigned* __restrict__ amax_bits) {
+  __shared__ unsigned wmax[4];
   unsigned m = 0;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count;
-       i += (int64_t)gridDim.x * 256) {
-    const unsigned b = __float_as_uint(H[i]) & 0x7FFFFFFFu;
-    m = b > m ? b : m;
+  // 16-byte loads when H is 16-byte aligned (the usual case), 4-byte ones otherwise
+  const int64_t n4 = ((uintptr_t)H & 15) == 0 ? count / 4 : 0;
+  const uint4* H4 = reinterpret_cast<const uint4*>(H);
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+    const uint4 v = H4[i];
+    const unsigned a = max(v.x & 0x7FFFFFFFu, v.y & 0x7FFFFFFFu);
+    const unsigned b = max(v.z & 0x7FFFFFFFu, v.w & 0x7FFFFFFFu);
+    m = max(m, max(a, b));
   }
-  for (int o = 32; o >= 1; o >>= 1) {
-    const unsigned v = __shfl_xor(m, o);
-    m = v > m ? v : m;
-  }
-  if ((threadIdx.x & 63) == 0) atomicMax(amax_bits, m);
+  for (int64_t i = 4 * n4 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * 256)
+    m = max(m, __float_as_uint(H[i]) & 0x7FFFFFFFu);
+  for (int o = 32; o >= 1; o >>= 1) m = max(m, (unsigned)__shfl_xor((int)m, o));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) atomicMax(amax_bits, max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3])));
 }
 
 __global__ void h2_clear_kernel(unsigned* __restrict__ p) { *p = 0u; }
@@ -89,7 +100,9 @@ int cp_h2_pack(const float* H, int64_t n, uint16_t* H16, float* diag32, float* h
   const int64_t count = n * n;
   cp::h2_clear_kernel<<<1, 1, 0, st>>>(amax);
   const int64_t blocks = (count + 255) / 256;
-  cp::h2_absmax_kernel<<<(unsigned)(blocks < 4096 ? blocks : 4096), 256, 0, st>>>(H, count, amax);
+  const int64_t ablocks = (count + 1023) / 1024;
+  cp::h2_absmax_kernel<<<(unsigned)(ablocks < 1 ? 1 : (ablocks < cp::kAbsmaxBlocks ? ablocks : cp::kAbsmaxBlocks)),
+                         256, 0, st>>>(H, count, amax);
   cp::h2_pack_kernel<<<(unsigned)blocks, 256, 0, st>>>(H, n, amax, H16, diag32, hscale);
   CP_LAUNCHED("Hessian pack");
   return CP_OK;

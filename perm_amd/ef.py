@@ -297,7 +297,6 @@ def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, per
     through ef_encode_many ``layers_per_pass`` blocks at a time, and tensors whose stored
     Hessians are identical (q/k/v, gate/up) share one factorization. Writes the per-tensor
     statistics to ``out_path + ".efstats.json"`` and returns them."""
-    import hashlib
     import json
     import time
     from . import hessians as hess
@@ -327,20 +326,26 @@ def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, per
         return None if p is None else np.asarray(p)
 
     H_cache = {}
+    digests = {}  # file path -> content key of its stored bytes
 
-    def hessian(name):
-        """Device float64 H of a tensor, shared between tensors with identical files."""
-        path = hess.hessian_path(hessdir, name)
-        with np.load(path) as z:
-            digest = hashlib.sha1()
-            for k in sorted(z.files):
-                if k != "name":
-                    digest.update(k.encode())
-                    digest.update(np.ascontiguousarray(z[k]).tobytes())
-        key = digest.hexdigest()
-        if key not in H_cache:
-            H_cache[key] = hess.load_hessian(hessdir, name, device="cuda")
-        return H_cache[key]
+    def group_hessians(names):
+        """{name: (device float64 H, n)} for every name with a stored Hessian. Files are
+        shared by content (hessians.stored_digest, no decompression), each distinct file is
+        read once -- on a thread pool, since zlib releases the GIL -- and expanded on the
+        GPU once, from this thread."""
+        from concurrent.futures import ThreadPoolExecutor
+        paths = {nm: hess.hessian_path(hessdir, nm) for nm in names}
+        paths = {nm: p for nm, p in paths.items() if p is not None}
+        for p in set(paths.values()):
+            if p not in digests:
+                digests[p] = hess.stored_digest(p)
+        first = {}
+        for p in paths.values():
+            first.setdefault(digests[p], p)
+        with ThreadPoolExecutor(max_workers=max(1, min(16, len(first)))) as pool:
+            stored = dict(zip(first, pool.map(hess.read_stored, first.values())))
+        dev = {k: hess.expand_stored(v, "cuda") for k, v in stored.items()}
+        return {nm: dev[digests[p]] for nm, p in paths.items()}
 
     selected = []
     for name, tt, t in targets:
@@ -365,6 +370,10 @@ def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, per
     for gkey in sorted(groups):
         t0 = time.time()
         ef_items, work = [], []
+        names = [nm for nm, _ in groups[gkey]]
+        if "token_embd.weight" in names:
+            names.append("blk.0.attn_q.weight")  # the embedding's column weights
+        Hg = group_hessians(names)
         for name, tt in groups[gkey]:
             x = _weights_f32(f16[name])
             qw = imat.get(name)
@@ -374,7 +383,9 @@ def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, per
             qd = torch.from_numpy(np.ascontiguousarray(qw, dtype=np.float32)).cuda() \
                 if qw is not None else None
             if name == "token_embd.weight":
-                H0, n0 = hess.load_hessian(hessdir, "blk.0.attn_q.weight", device="cuda")
+                if "blk.0.attn_q.weight" not in Hg:
+                    raise FileNotFoundError(f"no Hessian for blk.0.attn_q.weight in {hessdir}")
+                H0, n0 = Hg["blk.0.attn_q.weight"]
                 w_embd = (torch.diagonal(H0) / max(n0, 1)).to(torch.float32)
                 if p is not None:
                     w_embd = w_embd[torch.from_numpy(p).cuda()]
@@ -382,8 +393,8 @@ def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, per
                 raw = gkq.quantize_dev(tt, x, w_embd)
                 work.append((name, tt, x, qd, raw, gkq.dequantize_dev(tt, raw, x.shape[1]),
                              "wRTN(attn0-diag)"))
-            elif hess.has_hessian(hessdir, name):
-                H, _n = hessian(name)
+            elif name in Hg:
+                H, _n = Hg[name]
                 if p is not None:
                     from .perm import permute_hessian
                     key = ("perm", id(H), p.tobytes())
@@ -415,6 +426,7 @@ def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, per
                 log(f"[{done}/{len(selected)}] {name} {tt} {mode} "
                     f"err-vs-stock {stats[name]['rel_err_vs_stock'] * 100:+.1f}%")
         H_cache.clear()  # a layer group's Hessians are not read by later groups
+        del Hg
     reemit(target_path, out_path, replace=replace, log=log)
     if stats:
         med = float(np.median([s["rel_err_vs_stock"] for s in stats.values()]))

@@ -222,6 +222,59 @@ def has_hessian(hessdir, gguf_name):
     return hessian_path(hessdir, gguf_name) is not None
 
 
+def read_stored(path):
+    """Host arrays of one stored Hessian file: (H16 or older float32 H, hscale, diag32 or
+    None, n). Plain arrays only: no pickled object is read."""
+    with np.load(path) as z:
+        Hs = np.ascontiguousarray(z["H"])
+        hscale = float(z["hscale"]) if "hscale" in z.files else 1.0
+        diag = np.ascontiguousarray(z["diag32"], dtype=np.float32) if "diag32" in z.files else None
+        n = int(z["n"])
+    if Hs.dtype not in (np.float16, np.float32):
+        Hs = Hs.astype(np.float32)
+    return Hs, hscale, diag, n
+
+
+def expand_stored(stored, device=None):
+    """(float64 H on the device, n) from read_stored's arrays: float16 H times hscale with
+    the float32 diagonal written back, or an older float32 H widened (cp_h2_expand)."""
+    Hs, hscale, diag, n = stored
+    lib = _lib.load()
+    dev = torch.device(device) if device is not None else torch.device("cuda")
+    Hd = torch.from_numpy(Hs).to(dev)
+    dd = torch.from_numpy(diag).to(dev) if diag is not None else None
+    d = Hs.shape[0]
+    out = torch.empty((d, d), dtype=torch.float64, device=dev)
+    _lib.check(lib.cp_h2_expand(_lib.ptr(Hd), 1 if Hs.dtype == np.float16 else 0, d, hscale,
+                                _lib.ptr(dd), _lib.ptr(out), _lib.stream_ptr()))
+    return out, n
+
+
+def stored_digest(path):
+    """Content key of a stored Hessian file, computed without decompressing it: SHA-1 over
+    the stored bytes (and compression method) of every member except the tensor name.
+    Equal keys mean equal stored bytes, hence equal arrays; equal arrays written by
+    different compressors may hash apart, which only forgoes sharing them."""
+    import hashlib
+    import struct
+    import zipfile
+    h = hashlib.sha1()
+    with zipfile.ZipFile(path) as zf, open(path, "rb") as f:
+        for info in sorted(zf.infolist(), key=lambda i: i.filename):
+            if info.filename == "name.npy":
+                continue
+            f.seek(info.header_offset)
+            hdr = f.read(30)  # local file header; name and extra-field lengths at 26 and 28
+            if len(hdr) != 30 or hdr[:4] != b"PK\x03\x04":
+                raise ValueError(f"{path}: damaged member header for {info.filename}")
+            nlen, elen = struct.unpack("<HH", hdr[26:30])
+            f.seek(info.header_offset + 30 + nlen + elen)
+            h.update(info.filename.encode())
+            h.update(struct.pack("<IQ", info.compress_type, info.file_size))
+            h.update(f.read(info.compress_size))
+    return h.hexdigest()
+
+
 def load_hessian(hessdir, gguf_name, device=None):
     """(H float64 [d, d], n) for a GGUF tensor name (hessians.py:225-243): float16 H times
     hscale with the float32 diagonal written back, or an older float32 H widened. The
@@ -230,19 +283,5 @@ def load_hessian(hessdir, gguf_name, device=None):
     path = hessian_path(hessdir, gguf_name)
     if path is None:
         raise FileNotFoundError(f"no Hessian for {gguf_name} in {hessdir}")
-    lib = _lib.load()
-    with np.load(path) as z:  # plain arrays only: no pickled objects are read
-        Hs = np.ascontiguousarray(z["H"])
-        hscale = float(z["hscale"]) if "hscale" in z.files else 1.0
-        diag = np.ascontiguousarray(z["diag32"], dtype=np.float32) if "diag32" in z.files else None
-        n = int(z["n"])
-    if Hs.dtype not in (np.float16, np.float32):
-        Hs = Hs.astype(np.float32)
-    dev = torch.device(device) if device is not None else torch.device("cuda")
-    Hd = torch.from_numpy(Hs).to(dev)
-    dd = torch.from_numpy(diag).to(dev) if diag is not None else None
-    d = Hs.shape[0]
-    out = torch.empty((d, d), dtype=torch.float64, device=dev)
-    _lib.check(lib.cp_h2_expand(_lib.ptr(Hd), 1 if Hs.dtype == np.float16 else 0, d, hscale,
-                                _lib.ptr(dd), _lib.ptr(out), _lib.stream_ptr()))
+    out, n = expand_stored(read_stored(path), device)
     return (out if device is not None else out.cpu().numpy()), n

@@ -230,3 +230,35 @@ def test_h2_oracle_large_hessian_stays_finite():
 def test_h2_oracle_old_float32_format():
     H = _sym_psd(16, 3).astype(np.float32)
     assert np.array_equal(Ho.h2_expand(H), H.astype(np.float64))
+
+
+def test_stored_digest_keys_hessian_files_by_content(tmp_path):
+    """encode_gguf shares one factorization between tensors whose stored Hessian files
+    have the same content; the key comes from the zip members' stored bytes (no
+    decompression) and ignores the tensor name. Equal content with another compression
+    keys apart (a missed share, never a wrong one); any change in H, diag32, hscale or
+    n changes the key; read_stored returns the arrays as written."""
+    from perm_amd import hessians as hs
+    rng = np.random.default_rng(0)
+    H = rng.standard_normal((96, 96)).astype(np.float16)
+    dg = rng.standard_normal(96).astype(np.float32)
+
+    def write(name, H=H, dg=dg, hscale=2.0, n=7, compressed=True):
+        path = str(tmp_path / f"{name}.npz")
+        (np.savez_compressed if compressed else np.savez)(
+            path, H=H, diag32=dg, hscale=np.float32(hscale), n=n, name=name)
+        return path
+
+    base = hs.stored_digest(write("a"))
+    assert hs.stored_digest(write("b")) == base                 # another name, same content
+    assert hs.stored_digest(write("c", compressed=False)) != base
+    H2 = H.copy()
+    H2[5, 7] = np.float16(H2[5, 7] + 1)
+    assert hs.stored_digest(write("d", H=H2)) != base
+    dg2 = dg.copy()
+    dg2[3] += 1
+    assert hs.stored_digest(write("e", dg=dg2)) != base
+    assert hs.stored_digest(write("f", hscale=3.0)) != base
+    assert hs.stored_digest(write("g", n=8)) != base
+    Hs, hscale, diag, n = hs.read_stored(str(tmp_path / "a.npz"))
+    assert np.array_equal(Hs, H) and hscale == 2.0 and np.array_equal(diag, dg) and n == 7

@@ -49,6 +49,28 @@ def test_pack_and_expand_bit_identical(case):
     assert np.array_equal(out.cpu().numpy(), Ho.h2_expand(w16, ws, wd))
 
 
+@pytest.mark.parametrize("offset", [0, 1])
+def test_pack_large_and_misaligned(offset):
+    """max |H| over more entries than the reduction grid covers in one sweep (each block
+    strides), with the extreme planted near the end; the input 16-byte aligned and 4 bytes
+    off (the 4-byte-load path). Same bytes as the storage oracle."""
+    from perm_amd import hessians as hs
+    d = 3000
+    rng = np.random.default_rng(5)
+    H = (rng.standard_normal((d, d)) * 100).astype(F32)
+    H[d - 1, d - 3] = -123456.0
+    _say(f"h2 pack d={d} offset={offset}")
+    buf = torch.empty(d * d + 4, dtype=torch.float32, device="cuda")
+    view = buf[offset:offset + d * d].view(d, d)
+    view.copy_(torch.from_numpy(H))
+    assert (view.data_ptr() % 16 == 0) == (offset == 0)
+    H16, d32, sc = hs.pack_hessian(view)
+    w16, wd, ws = Ho.h2_pack(H)
+    assert float(ws) == 123456.0 / 32768.0 and sc.item() == float(ws)
+    assert np.array_equal(H16.cpu().numpy().view(np.uint16), w16.view(np.uint16))
+    assert np.array_equal(d32.cpu().numpy(), wd)
+
+
 def test_hessian_files(tmp_path):
     from perm_amd import hessians as hs
     H = dict(_cases())["scaled"]
