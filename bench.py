@@ -469,6 +469,47 @@ def formats_main(args):
     print(json.dumps(result))
 
 
+def gguf_cpu_baseline(Wl0, Hl0, emb, rows, layers, n_emb_rows, typemap, total_w):
+    """The numpy oracle (port of ef.py / kquant.py) doing the driver's per-tensor work:
+    for each of layer 0's 7 tensors one factorization (per tensor, as ef.py:189) and the
+    EF at 128 and 512 rows, extrapolated linearly in rows and to every layer; the
+    embedding's weighted Q6_K RTN timed on 256 rows and scaled to its rows. File I/O is
+    not counted."""
+    import numpy as np
+    from oracle import ef_oracle as E
+    from oracle import kquant_oracle as Ko
+    from perm_amd import workloads as wl
+    t_total, spent = 0.0, 0.0
+    for name, nrow, n, fam in wl.QWEN3_06B_LAYER:
+        tt = typemap[f"blk.0.{name}.weight"]
+        Hn = Hl0[fam]
+        t0 = time.perf_counter()
+        order = E.act_order(Hn)
+        U = E.inv_upper_factor(Hn[np.ix_(order, order)], 0.01).astype(np.float32)
+        t_fact = time.perf_counter() - t0
+        ts = {}
+        for r in (128, 512):
+            t0 = time.perf_counter()
+            E.ef_encode(Wl0[name][:r], tt, None, Hn, U=U)
+            ts[r] = time.perf_counter() - t0
+        b = (ts[512] - ts[128]) / 384.0
+        t_total += (t_fact + ts[128] - 128 * b + b * nrow) * layers
+        spent += t_fact + ts[128] + ts[512]
+    w_emb = (np.diag(Hl0["qkv_in"]) / rows).astype(np.float32)
+    t0 = time.perf_counter()
+    Ko.QUANTIZE["Q6_K"](emb, w_emb)
+    dt = time.perf_counter() - t0
+    spent += dt
+    t_total += dt * n_emb_rows / emb.shape[0]
+    return {"value": total_w / t_total / 1e6, "unit": "Mweights/s", "cores": 1, "kind": "port",
+            "sample": (f"numpy oracle (port of ef.py / kquant.py): layer 0's 7 tensors at 128 and "
+                       f"512 rows with one factorization each, and the embedding's weighted Q6_K "
+                       f"RTN on 256 rows ({spent:.1f} s of CPU work), extrapolated to the artifact's "
+                       f"{total_w} weights (est. {t_total:.0f} s; file I/O not counted); the sweep "
+                       f"and codec are single-threaded numpy"),
+            "host_cpus": os.cpu_count()}
+
+
 def gguf_main(args):
     """The encode_gguf driver (coldpress/ef.py:223-317) end to end on a synthetic
     Qwen3-0.6B artifact written to a temporary directory: the f16 GGUF (token_embd
@@ -511,6 +552,14 @@ def gguf_main(args):
                 X = wl.student_t_activations(rows, d, nu=4.0, seed=1000 * l + i, device="cuda")
                 fams[f"blk.{l}.{fam}"] = {"H": hessians.xtx_accumulate(X), "n": rows}
         hessians.save_hessians(fams, hdir)
+        base_in = None
+        if not args.no_cpu_baseline:
+            base_in = ({nm: w[f"blk.0.{nm}.weight"].float().cpu().numpy()
+                        for nm, *_ in wl.QWEN3_06B_LAYER},
+                       {fam: fams[f"blk.0.{fam}"]["H"].double().cpu().numpy()
+                        for fam in wl.QWEN3_06B_FAMILIES},
+                       w["token_embd.weight"][:256].float().cpu().numpy(),
+                       w["token_embd.weight"].shape[0])
         del fams, w
         torch.cuda.synchronize()
         log(f"artifact: {total_w} weights, {4 * layers} Hessian files in {tmp}")
@@ -544,7 +593,15 @@ def gguf_main(args):
             "byte_parity": {"passed": rep["passed"], "total_final": rep["total_final"],
                             "total_stock": rep["total_stock"]},
             "roofline": None,
+            "roofline_note": "end to end: host file I/O (GGUF and Hessian reads, GGUF write) plus "
+                             "the GPU codec / factor / EF; the kernels' rooflines are in the "
+                             "default (ef) and formats lines",
         }
+        if base_in is not None:
+            Wl0, Hl0, emb, n_emb = base_in
+            result["cpu_baseline"] = gguf_cpu_baseline(Wl0, Hl0, emb, rows, layers, n_emb, typemap,
+                                                       total_w)
+            result["gpu_over_cpu"] = value / result["cpu_baseline"]["value"]
         print(json.dumps(result))
     finally:
         shutil.rmtree(tmp, ignore_errors=True)

@@ -280,9 +280,30 @@ def _stat_err(recon, x, w):
     return float(((d * d) * w).to(torch.float64).sum().item())
 
 
+def _auto_layers_per_pass(f16, selected, block_of, frac=0.5):
+    """Layers per EF pass: the largest count whose estimated device footprint fits in
+    ``frac`` of the free device memory. Per weight ~28 B (float32 input and
+    reconstruction, the EF workspace of about 18.5 B, the container bytes); per tensor
+    40 n^2 B for its Hessian (float64 H, the 3 n^2 float64 factor workspace, the float32
+    U), counted per tensor even where tensors share one file, so the estimate errs high."""
+    free, _total = torch.cuda.mem_get_info()
+    per_layer = {}
+    for name, _tt in selected:
+        b = block_of(name)
+        if b < 0:
+            continue
+        shape = [int(x) for x in f16[name].shape]
+        n = shape[0]  # ne0: the input dimension, the Hessian's size
+        nw = int(np.prod(shape))
+        per_layer[b] = per_layer.get(b, 0) + 28 * nw + 40 * n * n
+    if not per_layer:
+        return 1
+    return max(1, int(frac * free // max(per_layer.values())))
+
+
 def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, perms=None,
                 spacemap=None, dims=None, acknowledge_unreviewed=False, only="all", n_iter=2,
-                unsafe_storage_order=False, device="cuda", log=print, layers_per_pass=4):
+                unsafe_storage_order=False, device="cuda", log=print, layers_per_pass=None):
     """EF-encode every quantized tensor of ``target_path`` (a stock quant artifact) from the
     float weights of ``f16_path`` and the Hessians in ``hessdir``, and write a byte-map
     clone of the target to ``out_path`` (coldpress/ef.py:223-317).
@@ -294,8 +315,10 @@ def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, per
     ``input_perm(name, perms, dims, ...)``, or "qwen3" for perm_amd.perm), the imatrix
     vectors and Hessians (stored in the original order) are permuted to the already
     permuted weights. Every codec, factorization and sweep runs on the GPU; EF tensors go
-    through ef_encode_many ``layers_per_pass`` blocks at a time, and tensors whose stored
-    Hessians are identical (q/k/v, gate/up) share one factorization. Writes the per-tensor
+    through ef_encode_many ``layers_per_pass`` blocks at a time (None: as many as fit in
+    half the free device memory, by a conservative estimate of the EF workspace and the
+    fp64 factor buffers per layer), and tensors whose stored Hessians are identical
+    (q/k/v, gate/up) share one factorization. Writes the per-tensor
     statistics to ``out_path + ".efstats.json"`` and returns them."""
     import json
     import time
@@ -361,6 +384,8 @@ def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, per
     def block_of(name):
         return int(name.split(".")[1]) if name.startswith("blk.") else -1
 
+    if layers_per_pass is None:
+        layers_per_pass = _auto_layers_per_pass(f16, selected, block_of)
     replace, stats = {}, {}
     t_start = time.time()
     groups = {}
