@@ -292,12 +292,12 @@ FORMAT_TYPES = ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0"]
 
 def formats_cpu_baseline(W0, qws0, Hs):
     """The numpy oracle (a port of kquant.py / scale_tune.py / hessians.py) on samples:
-    64 rows of layer 0's ffn_up per container (encode + decode), one 1024 x 1024 Hessian
-    (pack + expand); extrapolated per weight / per entry."""
+    layer 0's ffn_up (3072 x 1024) per container (encode + decode), one 3072 x 3072
+    Hessian (pack + expand); extrapolated per weight / per entry."""
     import numpy as np
     from oracle import hess_oracle as Ho
     from oracle import kquant_oracle as Ko
-    x = W0["ffn_up"][:64].cpu().numpy()
+    x = W0["ffn_up"].cpu().numpy()
     qw = qws0[x.shape[1]].cpu().numpy()
     per_w = {}
     spent = 0.0
@@ -308,7 +308,7 @@ def formats_cpu_baseline(W0, qws0, Hs):
         dt = time.perf_counter() - t0
         spent += dt
         per_w[tt] = dt / x.size
-    H = Hs[1024][0].cpu().numpy()
+    H = Hs[3072][0].cpu().numpy()
     t0 = time.perf_counter()
     H16, dg, hs = Ho.h2_pack(H)
     Ho.h2_expand(H16, hs, dg)
@@ -388,8 +388,25 @@ def formats_main(args):
         torch.cuda.synchronize()
         return ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
 
+    # one launch over a large tensor shows the decode kernel's own HBM rate (the
+    # per-tensor calls above carry ~7 us of launch each): every n = 1024 tensor stacked
+    big = torch.cat([x for x, _ in xs if x.shape[1] == 1024])
+    big_out = torch.empty_like(big)
+    big_raw = {tt: kquant.quantize_dev(tt, big, None if tt == "Q8_0" else qws[1024])
+               for tt in FORMAT_TYPES}
+
+    def run_big(tt, reps=5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            kquant.dequantize_dev(tt, big_raw[tt], big.shape[1], out=big_out)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
     for tt in FORMAT_TYPES:
         run_type(tt, check=True)
+        run_big(tt, 1)
     for d, Hb in Hs.items():
         hs_host[d] = [1.0] * Hb.shape[0]
     run_h2()
@@ -428,18 +445,26 @@ def formats_main(args):
             per[tt]["linear_extract_gb_per_s"] = lin_bytes / (ex * 1e-3) / 1e9
             per[tt]["linear_reconstruct_ms"] = rc
             per[tt]["linear_reconstruct_gb_per_s"] = (4.0 * total_w + 8.0 * nsb + 4.0 * total_w) / (rc * 1e-3) / 1e9
+    for tt in FORMAT_TYPES:
+        ms = run_big(tt)
+        per[tt]["decode_large_ms"] = ms
+        per[tt]["decode_large_gb_per_s"] = (big_raw[tt].numel() + 4.0 * big.numel()) / (ms * 1e-3) / 1e9
     pack_ms, expand_ms = h2 / args.steps
     h2_res = {"matrices": sum(Hb.shape[0] for Hb in Hs.values()), "entries": h_entries,
               "pack_ms": pack_ms, "pack_gb_per_s": 6.0 * h_entries / (pack_ms * 1e-3) / 1e9,
               "expand_ms": expand_ms, "expand_gb_per_s": 10.0 * h_entries / (expand_ms * 1e-3) / 1e9}
     value = len(FORMAT_TYPES) * total_w / (enc_dec_ms * 1e-3) / 1e6
-    dec_bw = dec_bytes / (dec_ms * 1e-3) / 1e9
-    roof = {"kernel": "kq_decode_kernel (all six containers)", "bound": "hbm", "achieved": dec_bw,
-            "peak": 8000.0, "unit": "GB/s", "frac": dec_bw / 8000.0, "traffic": None,
-            "avg_launch_ms": dec_ms / (len(FORMAT_TYPES) * len(xs)),
-            "launches_per_step": len(FORMAT_TYPES) * len(xs),
-            "note": "algorithmic bytes per decode: the container bytes read + 4 B per weight "
-                    "written; the encodes are VALU-bound (the make_q*_quants candidate searches)"}
+    big_bytes = sum(big_raw[tt].numel() + 4.0 * big.numel() for tt in FORMAT_TYPES)
+    big_ms = sum(per[tt]["decode_large_ms"] for tt in FORMAT_TYPES)
+    dec_bw = big_bytes / (big_ms * 1e-3) / 1e9
+    roof = {"kernel": "kq_decode_kernel / q8_decode_kernel (six containers)", "bound": "hbm",
+            "achieved": dec_bw, "peak": 8000.0, "unit": "GB/s", "frac": dec_bw / 8000.0,
+            "traffic": None, "avg_launch_ms": big_ms / len(FORMAT_TYPES), "launches_per_step": None,
+            "note": (f"one launch per container over the {big.shape[0]} x {big.shape[1]} stack of every "
+                     f"n = 1024 tensor; algorithmic bytes: the container bytes read + 4 B per weight "
+                     f"written. The per-tensor decodes of the step run at "
+                     f"{dec_bytes / (dec_ms * 1e-3) / 1e9:.0f} GB/s (launch-bound). The encodes are "
+                     f"VALU-bound (the make_q*_quants candidate searches).")}
     result = {
         "metric": "container codec encode+decode Mweights/s (Q2_K..Q6_K, Q8_0), 1 GPU",
         "value": value, "unit": "Mweights/s", "n_gpus": 1, "steps": args.steps,
@@ -459,8 +484,8 @@ def formats_main(args):
         result["cpu_baseline"] = {
             "value": len(FORMAT_TYPES) * total_w / cpu_s / 1e6, "unit": "Mweights/s", "cores": 1,
             "kind": "port",
-            "sample": (f"numpy oracle QUANTIZE + DEQUANTIZE (port of kquant.py) on 64 rows of layer "
-                       f"0's ffn_up per container and the h2 pack + expand of one 1024x1024 matrix "
+            "sample": (f"numpy oracle QUANTIZE + DEQUANTIZE (port of kquant.py) on layer 0's ffn_up "
+                       f"(3072x1024) per container and the h2 pack + expand of one 3072x3072 matrix "
                        f"({spent:.1f} s of CPU work), extrapolated per weight to the six containers "
                        f"over {total_w} weights (est. {cpu_s:.0f} s); single-threaded numpy"),
             "host_cpus": os.cpu_count()}

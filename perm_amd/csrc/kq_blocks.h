@@ -387,16 +387,9 @@ __device__ __forceinline__ void kq_encode_block(const float* __restrict__ x,
 // One thread per 16 consecutive weights of a superblock (16 threads per
 // superblock); y = (d*sc)*q - (dmin*m) in float32 (kquant.py:416-427, :489-503,
 // :596-627, :681-701).
-// Decode 16 weights of one superblock: global thread t covers superblock t / 16.
+// The 16 weights k * 16 .. k * 16 + 15 of the superblock at b (global or LDS bytes).
 template <int TT>
-__device__ __forceinline__ void kq_decode_thread(const uint8_t* __restrict__ raw, int64_t NB,
-                                                 float* __restrict__ y, int64_t t) {
-  constexpr int BP = Kq<TT>::BP;
-  const int64_t sb = t >> 4;
-  if (sb >= NB) return;
-  const int k = (int)(t & 15);
-  const uint8_t* b = raw + sb * BP;
-  float out[16];
+__device__ __forceinline__ void kq_decode16(const uint8_t* __restrict__ b, int k, float (&out)[16]) {
   if constexpr (TT == CP_Q2_K) {
     float d = half_value(b[80] | b[81] << 8), dm = half_value(b[82] | b[83] << 8);
     float dl = d * (float)(b[k] & 0xF), ml = dm * (float)(b[k] >> 4);
@@ -451,9 +444,73 @@ __device__ __forceinline__ void kq_decode_thread(const uint8_t* __restrict__ raw
       out[i] = dl * (float)((low | high << 4) - 32);
     }
   }
+}
+
+// Decode 16 weights of one superblock: global thread t covers superblock t / 16.
+template <int TT>
+__device__ __forceinline__ void kq_decode_thread(const uint8_t* __restrict__ raw, int64_t NB,
+                                                 float* __restrict__ y, int64_t t) {
+  constexpr int BP = Kq<TT>::BP;
+  const int64_t sb = t >> 4;
+  if (sb >= NB) return;
+  const int k = (int)(t & 15);
+  float out[16];
+  kq_decode16<TT>(raw + sb * BP, k, out);
   float4* o = reinterpret_cast<float4*>(y + sb * 256 + 16 * k);
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = make_float4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
+}
+
+// Decode of whole rows by workgroups of 4 waves, each wave 4 superblocks (1024 weights):
+// the wave's container bytes arrive with dword loads (byte loads when the buffer is not
+// 4-byte aligned) into LDS, every lane decodes 16 weights from there (lane = superblock
+// (l / 16), 16-weight group (l % 16)), and the weights leave through LDS so that each
+// store instruction writes 1 KB of consecutive floats. Waves past the end stage and store
+// nothing but take part in both barriers.
+constexpr int kDecSb = 4;  // superblocks per wave
+
+template <int TT>
+struct KqDecodeLds {
+  static constexpr int kBytes = (kDecSb * Kq<TT>::BP + 15) / 16 * 16;
+  uint8_t bytes[4][kBytes];
+  float out[4][kDecSb * 256];
+};
+
+template <int TT>
+__device__ __forceinline__ void kq_decode_block(const uint8_t* __restrict__ raw, int64_t NB,
+                                                float* __restrict__ y, int64_t block, KqDecodeLds<TT>& L) {
+  constexpr int BP = Kq<TT>::BP;
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int64_t sb0 = (block * 4 + w) * kDecSb;
+  const int nsb = sb0 >= NB ? 0 : (int)(NB - sb0 < kDecSb ? NB - sb0 : kDecSb);
+  const int nbytes = nsb * BP;
+  const uint8_t* src = raw + sb0 * BP;
+  uint8_t* dst = L.bytes[w];
+  if ((((uintptr_t)src) & 3) == 0) {
+    const int nd = nbytes >> 2;
+    for (int i = l; i < nd; i += 64)
+      reinterpret_cast<uint32_t*>(dst)[i] = reinterpret_cast<const uint32_t*>(src)[i];
+    for (int i = 4 * nd + l; i < nbytes; i += 64) dst[i] = src[i];
+  } else {
+    for (int i = l; i < nbytes; i += 64) dst[i] = src[i];
+  }
+  __syncthreads();
+  const int s = l >> 4, k = l & 15;
+  if (s < nsb) {
+    float out[16];
+    kq_decode16<TT>(dst + s * BP, k, out);
+    float4* o = reinterpret_cast<float4*>(&L.out[w][s * 256 + 16 * k]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = make_float4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
+  }
+  __syncthreads();
+  const int nw = nsb * 256;
+  float* yo = y + sb0 * 256;
+#pragma unroll
+  for (int i = 0; i < kDecSb; ++i) {
+    const int idx = 256 * i + 4 * l;
+    if (idx < nw) *reinterpret_cast<float4*>(yo + idx) = *reinterpret_cast<const float4*>(&L.out[w][idx]);
+  }
 }
 
 // ---------------------------------------------------------------- Q8_0

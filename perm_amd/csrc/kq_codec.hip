@@ -30,10 +30,12 @@ __global__ __launch_bounds__(256) void kq_encode_kernel(const float* __restrict_
   kq_encode_block<TT, IMAT>(x, qw, NB, nsb, out, blockIdx.x);
 }
 
+// 16 superblocks per workgroup (4 waves x kDecSb): grid ceil(NB / 16).
 template <int TT>
 __global__ __launch_bounds__(256) void kq_decode_kernel(const uint8_t* __restrict__ raw,
                                                         int64_t NB, float* __restrict__ y) {
-  kq_decode_thread<TT>(raw, NB, y, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+  __shared__ __align__(16) KqDecodeLds<TT> lds;
+  kq_decode_block<TT>(raw, NB, y, blockIdx.x, lds);
 }
 
 // ---------------------------------------------------------------- launchers
@@ -100,7 +102,7 @@ int kq_dequantize(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, float*
     return CP_OK;
   }
   const int64_t NB = nrow * (n / 256);
-  const int64_t blocks = (NB * 16 + 255) / 256;
+  const int64_t blocks = (NB + 4 * kDecSb - 1) / (4 * kDecSb);
   switch (ttype) {
     case CP_Q2_K: kq_decode_kernel<CP_Q2_K><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(raw, NB, y); break;
     case CP_Q3_K: kq_decode_kernel<CP_Q3_K><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(raw, NB, y); break;
