@@ -675,12 +675,14 @@ __global__ __launch_bounds__(256) void ef_commit_kernel(const EfDev* __restrict_
   kq_encode_block<TT, IMAT>(from_wcur ? t.Wcur : t.x, t.qw, NB, nsb, t.raw, blockIdx.x);
 }
 
+// 16 superblocks per workgroup (kq_decode_block); a tensor without a reconstruction
+// output skips the whole workgroup.
 template <int TT>
 __global__ __launch_bounds__(256) void ef_decode_kernel(const EfDev* __restrict__ tab) {
+  __shared__ __align__(16) KqDecodeLds<TT> lds;
   const EfDev& t = tab[blockIdx.y];
   if (!t.recon) return;
-  kq_decode_thread<TT>(t.raw, (int64_t)t.nrow * (t.n / 256), t.recon,
-                       (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+  kq_decode_block<TT>(t.raw, (int64_t)t.nrow * (t.n / 256), t.recon, blockIdx.x, lds);
 }
 
 // ---------------------------------------------------------------- committed grid
@@ -909,7 +911,7 @@ static void launch_commit(const EfDev* tab, const EfGroup& g, int from_wcur, hip
 
 template <int TT>
 static void launch_decode(const EfDev* tab, const EfGroup& g, hipStream_t st) {
-  const dim3 grid((unsigned)((g.max_nb * 16 + 255) / 256), (unsigned)g.count);
+  const dim3 grid((unsigned)((g.max_nb + 4 * kDecSb - 1) / (4 * kDecSb)), (unsigned)g.count);
   ef_decode_kernel<TT><<<grid, 256, 0, st>>>(tab + g.first);
 }
 

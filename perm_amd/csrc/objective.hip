@@ -108,15 +108,18 @@ __global__ __launch_bounds__(256) void err_encode_kernel(const ErrDev* __restric
   }
 }
 
+// Q8_0: one thread per 4 weights; k-quants: 16 superblocks per workgroup
+// (kq_decode_block).
 template <int TT>
 __global__ __launch_bounds__(256) void err_decode_kernel(const ErrDev* __restrict__ tab) {
   const ErrDev& T = tab[blockIdx.y];
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t w = (int64_t)T.R * T.n;
-  if constexpr (TT == CP_Q8_0)
-    q8_decode_thread(T.raw, w / 32, T.recon, t);
-  else
-    kq_decode_thread<TT>(T.raw, w / 256, T.recon, t);
+  if constexpr (TT == CP_Q8_0) {
+    q8_decode_thread(T.raw, w / 32, T.recon, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+  } else {
+    __shared__ __align__(16) KqDecodeLds<TT> lds;
+    kq_decode_block<TT>(T.raw, w / 256, T.recon, blockIdx.x, lds);
+  }
 }
 
 // --------------------------------------------------------------- column sums
@@ -394,10 +397,10 @@ static void launch_err_encode(const ErrDev* tab, const ErrGroup& g, hipStream_t 
 
 template <int TT>
 static void launch_err_decode(const ErrDev* tab, const ErrGroup& g, hipStream_t st) {
-  // Q8_0: one thread per 4 weights; k-quants: 16 threads per superblock
-  const int64_t threads = TT == CP_Q8_0 ? g.max_w / 4 : g.max_w / 256 * 16;
-  err_decode_kernel<TT><<<dim3((unsigned)((threads + 255) / 256), (unsigned)g.count), 256, 0, st>>>(
-      tab + g.first);
+  // Q8_0: one thread per 4 weights; k-quants: 16 superblocks per workgroup
+  const int64_t blocks = TT == CP_Q8_0 ? (g.max_w / 4 + 255) / 256
+                                       : (g.max_w / 256 + 4 * kDecSb - 1) / (4 * kDecSb);
+  err_decode_kernel<TT><<<dim3((unsigned)blocks, (unsigned)g.count), 256, 0, st>>>(tab + g.first);
 }
 
 template <template <int> class L>
