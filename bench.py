@@ -765,7 +765,7 @@ def main():
     ef_mw = total_weights / (ef_ms * 1e-3) / 1e6
     hess_tflops = hess_flops / (hess_ms * 1e-3) / 1e12
 
-    # dominant kernel: the Hessian MFMA kernel (one launch per Hessian) or the EF sweep
+    # dominant kernel: the Hessian MFMA kernel (one launch per matrix size) or the EF sweep
     hess_launches = len(H)  # one batched launch per Hessian size
     sweep_launches = 2 * len(H)  # sequential pass: two iterations per size class
     if hess_ms >= ph[2]:

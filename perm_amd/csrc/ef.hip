@@ -179,8 +179,8 @@ __device__ __forceinline__ float bcast_group(float x, int own) {
   }
 }
 
-// Columns hb .. hb + 31 (one half block; sg / sm hold its grid). tile is the
-// compact diagonal tile; row cb holds columns 16 * (cb / 16) .. 63.
+// Columns hb .. hb + kGridCols - 1 (one quarter block; sg / sm hold its grid). tile is
+// the compact diagonal tile; row cb holds columns 16 * (cb / 16) .. 63.
 template <int RS>
 __device__ __forceinline__ void sweep_part_split(const SweepTask& tk, int i1, int rr, int rl, int g,
                                                  float (&tl)[RS], const float* tile,
