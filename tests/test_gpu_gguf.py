@@ -217,6 +217,22 @@ def test_encode_gguf_end_to_end(tmp_path):
         assert set(__import__("json").load(f)) == {s[0] for s in SPEC}
 
 
+def test_encode_gguf_independent_of_layer_grouping(tmp_path):
+    """The driver's output does not depend on how many layers share one EF pass: one
+    layer per pass and the memory-sized default (here every layer in one pass, with the
+    identical q/k Hessian files sharing a factorization) write the same bytes."""
+    from perm_amd import ef
+    _W, f16, stock, hdir = _artifact(tmp_path)
+    outs = []
+    for lpp in (1, None):
+        out = str(tmp_path / f"ef_{lpp}.gguf")
+        _say(f"encode_gguf layers_per_pass={lpp}")
+        ef.encode_gguf(f16, stock, hdir, out, log=lambda *_: None, layers_per_pass=lpp)
+        with open(out, "rb") as f:
+            outs.append(f.read())
+    assert outs[0] == outs[1]
+
+
 def test_encode_gguf_with_perms_and_imatrix(tmp_path):
     """PERM-permuted artifact: the imatrix means and Hessians (original order) are moved by
     the space map's input permutation before EF; the result equals encoding the permuted
