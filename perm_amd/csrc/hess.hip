@@ -136,7 +136,10 @@ __device__ __forceinline__ void read_piece(const char* ra, const char* rb, int h
     f.a[idx] = __builtin_bit_cast(bf16x8, cur);
 }
 
-template <bool DIAG>
+// STAGE_ONLY: the wave stages its share of the panels and meets every barrier but
+// reads no operands and issues no MFMAs -- the wave of a diagonal tile whose 128 x 128
+// block lies wholly above the diagonal, whose sums would be discarded.
+template <bool DIAG, bool STAGE_ONLY = false>
 __device__ __forceinline__ void tile_rows(const uint16_t* X, int64_t r0, int64_t r1, int d, int i0,
                                           int j0, char* lds, f32x16 (&acc)[4][4]) {
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
@@ -170,8 +173,10 @@ __device__ __forceinline__ void tile_rows(const uint16_t* X, int64_t r0, int64_t
   for (int q = 0; q < NQ; ++q) stage_load_one(st, 3, g1, q);
   __syncthreads();
   Operands f0, f1;
+  if constexpr (!STAGE_ONLY) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) read_piece(ra0, rb0, 0, i, f0);
+    for (int i = 0; i < 16; ++i) read_piece(ra0, rb0, 0, i, f0);
+  }
   // Stage s (K = s % 4): store stage s + 2 (fetched two stages ago) into slot
   // K + 2, fetch stage s + 4 into the same registers, and multiply stage s
   // while reading the next operands (its second half, then the first half of
@@ -196,9 +201,11 @@ __device__ __forceinline__ void tile_rows(const uint16_t* X, int64_t r0, int64_t
     constexpr int SE = 32 / NQ;  // MFMAs per store
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0.a[i >> 2], f0.b[i & 3],
-                                                                   acc[i >> 2][i & 3], 0, 0, 0);
-      read_piece(ra, rb, 1, i, f1);
+      if constexpr (!STAGE_ONLY) {
+        acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0.a[i >> 2], f0.b[i & 3],
+                                                                     acc[i >> 2][i & 3], 0, 0, 0);
+        read_piece(ra, rb, 1, i, f1);
+      }
       if (i % SE == 0) {
         *reinterpret_cast<uint4*>(dst + chunk_ofs(i / SE)) = g[i / SE];
         stage_load_one(st, s + 4, g, i / SE);
@@ -207,9 +214,11 @@ __device__ __forceinline__ void tile_rows(const uint16_t* X, int64_t r0, int64_t
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1.a[i >> 2], f1.b[i & 3],
-                                                                   acc[i >> 2][i & 3], 0, 0, 0);
-      read_piece(na, nb, 0, i, f0);
+      if constexpr (!STAGE_ONLY) {
+        acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1.a[i >> 2], f1.b[i & 3],
+                                                                     acc[i >> 2][i & 3], 0, 0, 0);
+        read_piece(na, nb, 0, i, f0);
+      }
       if (i % SE == 0) {
         *reinterpret_cast<uint4*>(dst + chunk_ofs(NQ / 2 + i / SE)) = g[NQ / 2 + i / SE];
         stage_load_one(st, s + 4, g, NQ / 2 + i / SE);
@@ -265,10 +274,12 @@ __global__ __launch_bounds__(HNT) void hess_bf16_tri_kernel(const HessJobs jobs,
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
-  if (ti == tj)
-    tile_rows<true>(X, r0, r1, d, i0, j0, lds, acc);
-  else
+  if (ti != tj)
     tile_rows<false>(X, r0, r1, d, i0, j0, lds, acc);
+  else if (wn > wm)  // wave 1: its block is above the diagonal
+    tile_rows<true, true>(X, r0, r1, d, i0, j0, lds, acc);
+  else
+    tile_rows<true>(X, r0, r1, d, i0, j0, lds, acc);
   // lane l holds, for register v of tile (x, y), row wm + 32x + mfma32_row(v, l)
   // and column wn + 32y + l % 32 of the workgroup tile
   float* Hb = H + (int64_t)(i0 + wm + 4 * (l >> 5)) * d + (j0 + wn + (l & 31));
