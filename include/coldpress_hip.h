@@ -52,13 +52,14 @@ int cp_kq_block_bytes(int ttype);
  * reference does. Replaces kquant.QUANTIZE[tt](x, qw) -- coldpress/kquant.py:732
  * (encoders quantize_q2_K :347, quantize_q3_K :432, quantize_q4_K :588,
  * quantize_q5_K :592, quantize_q6_K :632, quantize_q8_0 :706). Bit-exact with the
- * reference encoder. */
+ * reference encoder. nrow == 0 is a no-op. */
 int cp_kq_quantize(int ttype, const float* x, int64_t nrow, int64_t n, const float* qw,
                    uint8_t* out, void* stream);
 
 /* Container decode of raw [nrow, n/block_weights*block_bytes] into y [nrow, n]
  * float32. Replaces kquant.DEQUANTIZE[tt](raw, n) -- coldpress/kquant.py:734
- * (decoders :416, :489, :596, :610, :681, :721). Bit-exact. */
+ * (decoders :416, :489, :596, :610, :681, :721). Bit-exact. nrow == 0 is a no-op
+ * (an empty container decodes to an empty tensor, as the reference's does). */
 int cp_kq_dequantize(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, float* y,
                      void* stream);
 

@@ -56,9 +56,10 @@ int kq_quantize(int ttype, const float* x, int64_t nrow, int64_t n, const float*
                 uint8_t* out, hipStream_t st) {
   KqGeom geo;
   if (!kq_geom(ttype, &geo)) return set_error(CP_ERR_TTYPE, "unsupported container type %d", ttype);
-  if (nrow <= 0 || n <= 0 || n % geo.block_weights)
+  if (nrow < 0 || n <= 0 || n % geo.block_weights)
     return set_error(CP_ERR_SHAPE, "x is [%lld, %lld]; rows must be positive multiples of %d",
                      (long long)nrow, (long long)n, geo.block_weights);
+  if (nrow == 0) return CP_OK;  // an empty tensor: nothing to encode
   if (!x || !out) return set_error(CP_ERR_ARG, "null x/out");
   if (!aligned(x, 16) || (qw && !aligned(qw, 16)) || !aligned(out, 4))
     return set_error(CP_ERR_ALIGN, "x/qw need 16-byte and out 4-byte alignment");
@@ -87,9 +88,10 @@ int kq_dequantize(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, float*
                   hipStream_t st) {
   KqGeom geo;
   if (!kq_geom(ttype, &geo)) return set_error(CP_ERR_TTYPE, "unsupported container type %d", ttype);
-  if (nrow <= 0 || n <= 0 || n % geo.block_weights)
+  if (nrow < 0 || n <= 0 || n % geo.block_weights)
     return set_error(CP_ERR_SHAPE, "y is [%lld, %lld]; rows must be positive multiples of %d",
                      (long long)nrow, (long long)n, geo.block_weights);
+  if (nrow == 0) return CP_OK;  // an empty container: nothing to decode
   if (!raw || !y) return set_error(CP_ERR_ARG, "null raw/y");
   if (!aligned(y, 16) || !aligned(raw, 2))
     return set_error(CP_ERR_ALIGN, "y needs 16-byte and raw 2-byte alignment");

@@ -57,6 +57,8 @@ def _quantizer(ttype):
         xd, host = _lib.to_device(x, torch.float32)
         if xd.dim() != 2:
             raise ValueError("x must be [nrow, n_per_row]")
+        if xd.shape[0] == 0:  # the reference's out.reshape(nrow, -1) fails on zero rows
+            raise ValueError("cannot encode an empty tensor (zero rows)")
         qd = None
         if qw is not None and ttype != "Q8_0":  # Q8_0 has no weighted path (kquant.py:706)
             qd, _ = _lib.to_device(qw, torch.float32)
@@ -72,7 +74,7 @@ def _quantizer(ttype):
 def _dequantizer(ttype):
     def dequantize(raw, n_per_row):
         rd, host = _lib.to_device(raw, torch.uint8)
-        rd = rd.reshape(rd.shape[0], -1)
+        rd = rd.reshape(rd.shape[0], -1) if rd.numel() else rd.reshape(rd.shape[0], 0)
         y = dequantize_dev(ttype, rd, int(n_per_row))
         return _lib.to_host(y) if host else y
     dequantize.__name__ = f"dequantize_{ttype.lower()}"

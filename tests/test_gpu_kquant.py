@@ -56,6 +56,26 @@ def test_matches_oracle_seeded(kq, tt, weighted):
 
 
 @pytest.mark.parametrize("tt", CODEC_TYPES)
+def test_empty_tensors_behave_like_the_reference(kq, tt):
+    """Zero rows: the reference's encoders fail in their final reshape(nrow, -1) with
+    ValueError (the oracle restates it and fails alike); its decoders return an empty
+    [0, n] float32 array. Numpy and device inputs both."""
+    x = np.zeros((0, 256), np.float32)
+    with pytest.raises(ValueError):
+        K.QUANTIZE[tt](x, None)
+    with pytest.raises(ValueError):
+        kq.QUANTIZE[tt](x, None)
+    with pytest.raises(ValueError):
+        kq.QUANTIZE[tt](torch.zeros((0, 256), device="cuda"), None)
+    raw = np.zeros((0, kq.row_bytes(tt, 256)), np.uint8)
+    want = K.DEQUANTIZE[tt](raw, 256)
+    got = kq.DEQUANTIZE[tt](raw, 256)
+    assert want.shape == got.shape == (0, 256) and got.dtype == want.dtype == np.float32
+    gd = kq.DEQUANTIZE[tt](torch.from_numpy(raw).cuda(), 256)
+    assert gd.is_cuda and tuple(gd.shape) == (0, 256)
+
+
+@pytest.mark.parametrize("tt", CODEC_TYPES)
 def test_ragged_superblock_counts(kq, tt):
     """Superblock counts that leave partial waves (1, 3, 5, 7, 9 superblocks)."""
     for nrow, n in [(1, 256), (3, 256), (1, 1280), (7, 256), (3, 768)]:
