@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256) void lin_write_back_kernel(const uint8_t* raw,
 
 static int lin_check(int ttype, int64_t nrow, int64_t n, LinLayout* L) {
   if (!lin_layout(ttype, L)) return set_error(CP_ERR_TTYPE, "no linear form for container type %d", ttype);
-  if (nrow <= 0 || n <= 0 || n % 256 || nrow * (n / 256) > ((int64_t)1 << 31))
+  if (nrow < 0 || n <= 0 || n % 256 || nrow * (n / 256) > ((int64_t)1 << 31))
     return set_error(CP_ERR_SHAPE, "[%lld, %lld]: rows must be positive multiples of 256",
                      (long long)nrow, (long long)n);
   return CP_OK;
@@ -202,6 +202,7 @@ int cp_lin_extract(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, float
   cp::clear_error();
   cp::LinLayout L;
   if (int s = cp::lin_check(ttype, nrow, n, &L)) return s;
+  if (nrow == 0) return CP_OK;  // an empty tensor
   const bool has_min = L.dmin_off >= 0;
   if (!raw || !d || !A || (has_min && (!dmin || !B)))
     return cp::set_error(CP_ERR_ARG, "null pointer (dmin and B are required for this type)");
@@ -231,7 +232,8 @@ int cp_lin_extract(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, float
 int cp_lin_reconstruct(int64_t nrow, int64_t n, const float* d, const float* dmin,
                        const int16_t* A, const int16_t* B, float* W, void* stream) {
   cp::clear_error();
-  if (nrow <= 0 || n <= 0 || n % 256) return cp::set_error(CP_ERR_SHAPE, "rows must be multiples of 256");
+  if (nrow < 0 || n <= 0 || n % 256) return cp::set_error(CP_ERR_SHAPE, "rows must be multiples of 256");
+  if (nrow == 0) return CP_OK;  // an empty tensor
   if (!d || !A || !W || (!dmin != !B)) return cp::set_error(CP_ERR_ARG, "null pointer (dmin and B go together)");
   if (!cp::aligned(A, 8) || (B && !cp::aligned(B, 8)) || !cp::aligned(W, 16))
     return cp::set_error(CP_ERR_ALIGN, "A/B need 8-byte and W 16-byte alignment");
@@ -245,7 +247,8 @@ int cp_lin_reconstruct(int64_t nrow, int64_t n, const float* d, const float* dmi
 int cp_lin_reconstruct_grad(int64_t nrow, int64_t n, const float* gW, const int16_t* A,
                             const int16_t* B, float* gd, float* gdmin, void* stream) {
   cp::clear_error();
-  if (nrow <= 0 || n <= 0 || n % 256) return cp::set_error(CP_ERR_SHAPE, "rows must be multiples of 256");
+  if (nrow < 0 || n <= 0 || n % 256) return cp::set_error(CP_ERR_SHAPE, "rows must be multiples of 256");
+  if (nrow == 0) return CP_OK;  // an empty tensor
   if (!gW || !A || !gd || (!gdmin != !B)) return cp::set_error(CP_ERR_ARG, "null pointer (gdmin and B go together)");
   if (!cp::aligned(A, 8) || (B && !cp::aligned(B, 8)) || !cp::aligned(gW, 16))
     return cp::set_error(CP_ERR_ALIGN, "A/B need 8-byte and gW 16-byte alignment");
@@ -261,6 +264,7 @@ int cp_lin_write_back(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, co
   cp::clear_error();
   cp::LinLayout L;
   if (int s = cp::lin_check(ttype, nrow, n, &L)) return s;
+  if (nrow == 0) return CP_OK;  // an empty tensor
   if (!raw || !d || !out || (L.dmin_off >= 0 && !dmin))
     return cp::set_error(CP_ERR_ARG, "null pointer (dmin is required for this type)");
   const int64_t nbytes = nrow * (n / 256) * L.bp;

@@ -106,7 +106,8 @@ def write_back(raw_bytes_2d, ttype, d_new_f32, dmin_new_f32=None):
     rd, host = _raw_dev(raw_bytes_2d)
     nrow = rd.shape[0]
     bp = {"Q2_K": 84, "Q3_K": 110, "Q4_K": 144, "Q5_K": 176, "Q6_K": 210}[ttype]
-    n = rd.reshape(nrow, -1).shape[1] // bp * 256
+    row_bytes = rd.shape[1] if rd.dim() == 2 else rd.reshape(nrow, -1).shape[1]
+    n = row_bytes // bp * 256
     d = _as_dev(d_new_f32, torch.float32)
     dmin = _as_dev(dmin_new_f32, torch.float32) if _HAS_MIN[ttype] else None
     if d.numel() != nrow * (n // 256) or (dmin is not None and dmin.numel() != d.numel()):
@@ -114,7 +115,7 @@ def write_back(raw_bytes_2d, ttype, d_new_f32, dmin_new_f32=None):
     out = torch.empty_like(rd)
     _lib.check(lib.cp_lin_write_back(_lib.TTYPE[ttype], _lib.ptr(rd), nrow, n, _lib.ptr(d),
                                      _lib.ptr(dmin), _lib.ptr(out), _lib.stream_ptr()))
-    out = out.reshape(nrow, -1)
+    out = out.reshape(nrow, row_bytes)
     return out.cpu().numpy() if host else out
 
 

@@ -127,3 +127,18 @@ def test_full_size_linear_form(st):
         W = st.reconstruct({**lin, "d": lin["d"], "dmin": lin["dmin"]})
         assert torch.equal(W, kquant.dequantize_dev(tt, raw, 1024))
         assert torch.equal(st.write_back(raw, tt, lin["d"], lin["dmin"]), raw)
+
+
+@pytest.mark.parametrize("tt", TYPES)
+def test_empty_tensor(st, tt):
+    """Zero rows: extract, reconstruct and write_back return empty results, as the
+    reference's numpy code does on an empty container (the oracle's linear_parts)."""
+    raw = np.zeros((0, K.BYTES_PER_SB[tt]), np.uint8)
+    d, dmin, A, B = K.linear_parts(raw, tt, 256)
+    lin = st.extract_linear(raw, tt, 256)
+    assert lin["d"].shape == d.shape == (0, 1) and lin["A"].shape == A.shape == (0, 256)
+    assert (lin["dmin"] is None) == (dmin is None) and (lin["B"] is None) == (B is None)
+    assert st.reconstruct_np(lin).shape == (0, 256)
+    out = st.write_back(raw, tt, np.zeros((0, 1), np.float32),
+                        np.zeros((0, 1), np.float32) if dmin is not None else None)
+    assert out.shape == raw.shape and out.dtype == np.uint8
