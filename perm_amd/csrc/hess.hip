@@ -444,7 +444,7 @@ static int hess_f32(const float* X, int64_t N, int64_t d, float* H, hipStream_t 
 }
 
 static int hess_check(int x_dtype, int64_t N, int64_t d) {
-  if (N <= 0 || d <= 0 || d > (1 << 20)) return set_error(CP_ERR_SHAPE, "bad X shape [%lld, %lld]", (long long)N, (long long)d);
+  if (N < 0 || d <= 0 || d > (1 << 20)) return set_error(CP_ERR_SHAPE, "bad X shape [%lld, %lld]", (long long)N, (long long)d);
   if (x_dtype != 0 && x_dtype != 1) return set_error(CP_ERR_ARG, "x_dtype must be 0 (f32) or 1 (bf16)");
   if (x_dtype == 1 && d % 8) return set_error(CP_ERR_SHAPE, "bf16 X needs d %% 8 == 0 (got %lld)", (long long)d);
   return CP_OK;
@@ -454,8 +454,10 @@ static int hess_check(int x_dtype, int64_t N, int64_t d) {
 
 extern "C" int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, float* H, void* stream) {
   cp::clear_error();
-  if (!X || !H) return cp::set_error(CP_ERR_ARG, "null X/H");
   if (int s = cp::hess_check(x_dtype, N, d)) return s;
+  if (!H) return cp::set_error(CP_ERR_ARG, "null H");
+  if (N == 0) return CP_OK;  // no rows: H += 0
+  if (!X) return cp::set_error(CP_ERR_ARG, "null X");
   if (!cp::aligned(X, 16) || !cp::aligned(H, 4)) return cp::set_error(CP_ERR_ALIGN, "X needs 16-byte alignment");
   if (x_dtype == 1) return cp::hess_bf16_batch(&X, &H, 1, N, d, (hipStream_t)stream);
   return cp::hess_f32((const float*)X, N, d, H, (hipStream_t)stream);
@@ -466,6 +468,7 @@ extern "C" int cp_hess_accum_batch(const void* const* X, float* const* H, int co
   cp::clear_error();
   if (!X || !H || count <= 0) return cp::set_error(CP_ERR_ARG, "no jobs");
   if (int s = cp::hess_check(x_dtype, N, d)) return s;
+  if (N == 0) return CP_OK;  // no rows: every H += 0
   hipStream_t st = (hipStream_t)stream;
   if (x_dtype == 1) return cp::hess_bf16_batch(X, H, count, N, d, st);
   for (int i = 0; i < count; ++i) {

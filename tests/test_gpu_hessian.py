@@ -39,6 +39,21 @@ def test_accumulates_in_place(hs):
     assert Ho.rel_fro(acc.H.cpu().numpy(), ref) < 1e-5
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_zero_row_batch_adds_nothing(hs, dtype):
+    """A batch with no rows leaves H as it was, as the reference's x.T @ x of an empty
+    batch adds zeros (hessians.py:137-154); alone and inside a batched call."""
+    g = torch.Generator(device="cuda").manual_seed(1)
+    H = torch.randn((256, 256), generator=g, device="cuda")
+    before = H.clone()
+    hs.xtx_accumulate(torch.zeros((0, 256), device="cuda", dtype=dtype), H)
+    assert torch.equal(H, before)
+    hs.xtx_accumulate_many([torch.zeros((0, 256), device="cuda", dtype=dtype)] * 2, [H, H.clone()])
+    assert torch.equal(H, before)
+    assert torch.equal(hs.xtx_accumulate(torch.zeros((2, 0, 128), device="cuda", dtype=dtype)),
+                       torch.zeros((128, 128), device="cuda"))
+
+
 def test_collect_hessians_hooks(hs):
     torch.manual_seed(0)
     model = torch.nn.Sequential(torch.nn.Linear(256, 512), torch.nn.GELU(),
