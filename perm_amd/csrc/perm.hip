@@ -31,10 +31,11 @@ extern "C" int cp_permute_gather(const void* src, void* dst, const int32_t* row_
                                  const int32_t* col_perm, int64_t rows, int64_t cols,
                                  int elem_bytes, void* stream) {
   cp::clear_error();
+  if (rows < 0 || cols < 0 || rows > 0x7FFFFFFF)
+    return cp::set_error(CP_ERR_SHAPE, "bad shape [%lld, %lld]", (long long)rows, (long long)cols);
+  if (rows == 0 || cols == 0) return CP_OK;  // an empty tensor, as numpy indexing of one
   if (!src || !dst) return cp::set_error(CP_ERR_ARG, "null src/dst");
   if (src == dst) return cp::set_error(CP_ERR_ARG, "gather cannot run in place");
-  if (rows <= 0 || cols <= 0 || rows > 0x7FFFFFFF)
-    return cp::set_error(CP_ERR_SHAPE, "bad shape [%lld, %lld]", (long long)rows, (long long)cols);
   if (!cp::aligned(src, elem_bytes) || !cp::aligned(dst, elem_bytes))
     return cp::set_error(CP_ERR_ALIGN, "buffers need %d-byte alignment", elem_bytes);
   hipStream_t st = (hipStream_t)stream;

@@ -40,6 +40,15 @@ def test_gather_matches_numpy(gp, dtype):
         assert torch.equal(gp.gather(a, rp, None).cpu(), a.cpu()[torch.from_numpy(rp)])
 
 
+@pytest.mark.parametrize("shape", [(0, 16), (16, 0), (0, 0)])
+def test_gather_empty(gp, shape):
+    """Empty tensors permute to empty tensors, as numpy / torch indexing does."""
+    R, C = shape
+    a = torch.zeros(shape, dtype=torch.float32, device="cuda")
+    out = gp.gather(a, np.arange(R)[::-1].copy(), np.arange(C)[::-1].copy())
+    assert out.is_cuda and tuple(out.shape) == shape
+
+
 def test_layer_permute_roundtrip(gp):
     from perm_amd.workloads import qwen3_layer_weights
     W = qwen3_layer_weights(0, seed=3)
