@@ -272,12 +272,13 @@ def _weights_f32(t):
     raise ValueError(f"{t.name}: source weights of type {name} are not float")
 
 
-def _stat_err(recon, x, w):
-    """float((((recon - x) ** 2) * w).sum()) of coldpress/ef.py:299-300: the float32
-    terms, summed in float64 (diagnostic; within ~1e-6 relative of the reference's float32
-    pairwise total)."""
+def _stat_err_dev(recon, x, w):
+    """(((recon - x) ** 2) * w).sum() of coldpress/ef.py:299-300 as a float64 device
+    scalar: the float32 terms, summed in float64 (diagnostic; within ~1e-6 relative of
+    the reference's float32 pairwise total)."""
     d = recon - x
-    return float(((d * d) * w).to(torch.float64).sum().item())
+    return ((d * d) * w).to(torch.float64).sum()
+
 
 
 def _auto_layers_per_pass(f16, selected, block_of, frac=0.5):
@@ -435,17 +436,26 @@ def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, per
         res = ef_encode_many(ef_items, n_iter=n_iter, act_order=not unsafe_storage_order) \
             if ef_items else {}
         sec = (time.time() - t0) / max(len(work), 1)
+        # the statistics stay on the device until one read-back for the whole group,
+        # and the container bytes come back in one copy
+        errs, raws = [], []
         for name, tt, x, qd, raw, recon, mode in work:
             if raw is None:
                 raw, recon = res[name]
             base = gkq.dequantize_dev(tt, gkq.quantize_dev(tt, x, qd), x.shape[1])
             w = qd if qd is not None else torch.ones(x.shape[1], dtype=torch.float32,
                                                       device=x.device)
-            e_base, e_ours = _stat_err(base, x, w), _stat_err(recon, x, w)
+            errs.append(torch.stack([_stat_err_dev(base, x, w), _stat_err_dev(recon, x, w)]))
+            raws.append(raw.reshape(-1))
+        err_host = torch.stack(errs).cpu().tolist() if errs else []
+        raw_host = torch.cat(raws).cpu().numpy() if raws else None
+        off = 0
+        for (name, tt, _x, _qd, _raw, _rec, mode), (e_base, e_ours), r in zip(work, err_host, raws):
             stats[name] = {"type": tt, "mode": mode,
                            "rel_err_vs_stock": e_ours / e_base - 1 if e_base else 0.0,
                            "sec": sec}
-            replace[name] = raw.reshape(-1).cpu().numpy()
+            replace[name] = raw_host[off:off + r.numel()]
+            off += r.numel()
             done += 1
             if done % 20 == 0 or name in ("token_embd.weight", "output.weight"):
                 log(f"[{done}/{len(selected)}] {name} {tt} {mode} "
