@@ -81,10 +81,11 @@ def hessian_phase(X, H, slot):
     xtx_accumulate_many(xs, hs)
 
 
-def ef_phase(W, H, slot, layers, mode, concurrent=True):
+def ef_phase(W, H, slot, layers, mode, concurrent=True, keep=None):
     """Act order + factor per Hessian size class, then EF of that class's tensors.
     With ``concurrent`` each size class runs on its own stream, so one class's
-    factorization overlaps another's sweep (perm_amd.ef.encode_size_classes)."""
+    factorization overlaps another's sweep (perm_amd.ef.encode_size_classes).
+    ``keep`` (a dict, for parity checks) receives each class's (U, order, qw) by size."""
     from perm_amd import ef as gef
     from perm_amd import workloads as wl
 
@@ -92,6 +93,8 @@ def ef_phase(W, H, slot, layers, mode, concurrent=True):
         def build(U, order):
             # qw = diag(H) / N for every Hessian of the class in one kernel
             qw = (H[d].diagonal(dim1=1, dim2=2) / float(ROWS)).contiguous()
+            if keep is not None:
+                keep[d] = (U, order, qw)
             items = []
             for l in range(layers):
                 for name, _rows, _n, fam in wl.QWEN3_06B_LAYER:
@@ -109,8 +112,8 @@ def ef_phase(W, H, slot, layers, mode, concurrent=True):
     outs = []
     for Hb, build in classes:
         order = gef.act_order_dev(Hb)
-        U, _ = gef.factor_dev(Hb, order, 0.01)
-        outs.append(gef.ef_encode_dev(build(U, order), n_iter=2, mode=mode))
+        U, _ = gef.factor_dev(Hb, order, 0.01, checked=True)
+        outs.append(gef.ef_encode_dev(build(U, order), n_iter=2, mode=mode, checked=True))
     return outs
 
 

@@ -34,7 +34,8 @@ enum cp_status {
   CP_ERR_HIP = -4,       /* a HIP runtime call failed                            */
   CP_ERR_ARG = -5,       /* null pointer / invalid argument                      */
   CP_ERR_ALIGN = -6,     /* pointer alignment requirement violated               */
-  CP_ERR_WORKSPACE = -7  /* workspace too small                                  */
+  CP_ERR_WORKSPACE = -7, /* workspace too small                                  */
+  CP_ERR_INDEX = -8      /* an index argument out of range / not a permutation    */
 };
 
 enum cp_ttype { CP_Q8_0 = 8, CP_Q2_K = 10, CP_Q3_K = 11, CP_Q4_K = 12, CP_Q5_K = 13, CP_Q6_K = 14 };
@@ -67,7 +68,8 @@ int cp_kq_dequantize(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, flo
 
 /* order[z][jj] = column visited jj-th: stable argsort of -diag(H_z) for each of
  * ``batch`` [n, n] matrices (h_dtype 0 = float32, 1 = float64). Replaces
- * ef.py:187 ``np.argsort(-np.diag(H))`` (ties broken by index). */
+ * ef.py:187 ``np.argsort(-np.diag(H))`` (ties broken by index; NaN entries last,
+ * by index, as numpy sorts them). Always a permutation. */
 int cp_act_order(const void* H, int h_dtype, int64_t n, int batch, int32_t* order, void* stream);
 
 /* Workspace bytes cp_chol_inv_upper needs for ``batch`` matrices of size n. */
@@ -80,7 +82,9 @@ size_t cp_chol_ws_bytes(int64_t n, int batch);
  * sweep consumes) or float64 (u_dtype 1). A matrix whose factorization fails is
  * retried with damp x 10, up to max_tries attempts; damp_used (host array of
  * ``batch`` doubles, may be NULL) receives the damp that succeeded.
- * Returns CP_ERR_NOT_PD when a matrix fails every attempt.
+ * Returns CP_ERR_NOT_PD when a matrix fails every attempt, CP_ERR_INDEX when an
+ * order is not a permutation of n (no read ever leaves H: its entries are clamped
+ * before use). A NaN pivot counts as a failed attempt, as LAPACK's does.
  * Replaces ef.cholesky_inv_upper(Hp, damp, _max_tries) -- coldpress/ef.py:46-84
  * -- together with the gather and float32 cast of ef.py:188-189.
  * Synchronizes ``stream`` (it reads the per-matrix failure flags). */
@@ -89,8 +93,9 @@ int cp_chol_inv_upper(const void* H, int h_dtype, int64_t n, int batch, const in
                       void* ws, size_t ws_bytes, void* stream);
 
 /* One attempt of cp_chol_inv_upper at ``damp`` for every matrix, without waiting
- * on the stream: flags[z] (device int32 array of ``batch``) is set to 1 where
- * matrix z met a non-positive pivot, and that U_z is then meaningless. Work
+ * on the stream: flags[z] (device int32 array of ``batch``) has bit 0 set where
+ * matrix z met a non-positive or NaN pivot and bit 1 where its order is not a
+ * permutation; that U_z is then meaningless. Work
  * that consumes U can be queued behind it; a caller that later finds a set flag
  * re-runs cp_chol_inv_upper, whose escalation reproduces the reference's
  * (coldpress/ef.py:60-84). Same workspace as cp_chol_inv_upper. */
@@ -123,7 +128,10 @@ typedef struct cp_ef_tensor {
 size_t cp_ef_ws_bytes(const cp_ef_tensor* tensors, int count);
 
 /* GPTQ error feedback into committed k-quant grids for ``count`` independent
- * tensors in one pass: per iteration, commit the container with the stock
+ * tensors in one pass. Each order must be a permutation of its n (as cp_act_order
+ * gives); one that is not never makes a read or write leave the tensor's buffers,
+ * but its bytes are meaningless (the host wrappers check caller-supplied orders
+ * before the call). Per iteration, commit the container with the stock
  * encoder (cp_kq_quantize) on the current targets, sweep the columns in
  * visiting order quantizing onto the committed grid and propagating the
  * error through U, re-pack the codes; after n_iter iterations decode into
@@ -211,7 +219,8 @@ int cp_lin_write_back(int ttype, const uint8_t* raw, int64_t nrow, int64_t n, co
 
 /* dst[r][c] = src[row_perm[r]][col_perm[c]] for a row-major [rows, cols] matrix of
  * elem_bytes-byte elements (1, 2, 4 or 8); a NULL permutation is the identity.
- * Every index must lie in range (the permutations are validated by the caller).
+ * An index outside [0, rows) / [0, cols) is clamped into it, so no read leaves src
+ * (the host wrapper rejects such indices with IndexError before the call).
  * Replaces the index_select / fancy-index moves of qwen3.apply_perms
  * (coldpress/perm/spacemaps/qwen3.py:141-188) and H[np.ix_(p, p)] (ef.py:289-290).
  * Not in place. */

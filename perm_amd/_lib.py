@@ -14,7 +14,7 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcoldpress_hip.so")
 
 CP_OK, CP_ERR_SHAPE, CP_ERR_TTYPE, CP_ERR_NOT_PD = 0, -1, -2, -3
-CP_ERR_HIP, CP_ERR_ARG, CP_ERR_ALIGN, CP_ERR_WORKSPACE = -4, -5, -6, -7
+CP_ERR_HIP, CP_ERR_ARG, CP_ERR_ALIGN, CP_ERR_WORKSPACE, CP_ERR_INDEX = -4, -5, -6, -7, -8
 
 TTYPE = {"Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
 
@@ -134,7 +134,51 @@ def check(status, exc_for_shape=ValueError):
         raise KeyError(msg)
     if status == CP_ERR_HIP:
         raise HipError(msg)
+    if status == CP_ERR_INDEX:
+        raise IndexError(msg)
     raise ValueError(f"{msg} (status {status})")
+
+
+def check_index(p, size, what="index", permutation=False):
+    """An index array checked on the host before anything is launched with it.
+
+    numpy's rules for an index into an axis of ``size``: every entry lies in
+    [-size, size) and negative entries count from the end (IndexError otherwise, as
+    numpy's fancy indexing raises). With ``permutation`` every position must occur
+    exactly once, as an act order or a channel permutation must (IndexError
+    otherwise). ``p``: a numpy array, a sequence or a torch tensor; a CUDA tensor is
+    checked with device reductions and one synchronization. Returns an int32 array
+    (or tensor, on p's device) with negative entries resolved; the shape is kept."""
+    if isinstance(p, torch.Tensor):
+        t = p.to(torch.int64)
+        if t.numel():
+            lo, hi = (int(v) for v in torch.stack([t.min(), t.max()]).cpu())
+            if lo < -size or hi >= size:
+                raise IndexError(f"{what}: index {lo if lo < -size else hi} is out of bounds "
+                                 f"for axis 0 with size {size}")
+        t = torch.where(t < 0, t + size, t)
+        if permutation and t.numel():
+            rows = t.reshape(-1, t.shape[-1]) if t.dim() else t.reshape(1, 1)
+            ok = rows.shape[-1] == size and bool(
+                torch.equal(torch.sort(rows, dim=-1).values,
+                            torch.arange(size, device=t.device).expand_as(rows)))
+            if not ok:
+                raise IndexError(f"{what} is not a permutation of {size}")
+        return t.to(torch.int32)
+    a = np.asarray(p)
+    if a.dtype.kind not in "iu" and a.size:
+        raise IndexError(f"{what}: indices must be integers, got {a.dtype}")
+    a = a.astype(np.int64)
+    if a.size and (int(a.min()) < -size or int(a.max()) >= size):
+        bad = int(a.min()) if int(a.min()) < -size else int(a.max())
+        raise IndexError(f"{what}: index {bad} is out of bounds for axis 0 with size {size}")
+    a = np.where(a < 0, a + size, a)
+    if permutation and a.size:
+        rows = a.reshape(-1, a.shape[-1]) if a.ndim else a.reshape(1, 1)
+        if rows.shape[-1] != size or not np.array_equal(np.sort(rows, axis=-1),
+                                                        np.broadcast_to(np.arange(size), rows.shape)):
+            raise IndexError(f"{what} is not a permutation of {size}")
+    return a.astype(np.int32)
 
 
 def stream_ptr():

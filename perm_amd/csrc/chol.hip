@@ -275,6 +275,10 @@ static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------- prepare
+// An order entry taken into [0, n): a caller's order that is not a permutation is
+// flagged by fact_shift_kernel and must never address memory outside H.
+__device__ inline int clamp_index(int p, int n) { return p < 0 ? 0 : (p >= n ? n - 1 : p); }
+
 // numpy's pairwise float64 sum of a strided vector (same recursion as the
 // float32 one: 8 accumulators up to 128 elements, halving split above).
 __device__ double pw_sum_f64(const double* a, int n, int stride) {
@@ -298,35 +302,44 @@ __device__ double pw_sum_f64(const double* a, int n, int stride) {
   return pw_sum_f64(a, n2, stride) + pw_sum_f64(a + (int64_t)n2 * stride, n - n2, stride);
 }
 
-// Leaves of numpy's pairwise sum over n values, in order: the recursion above
-// splits until a piece has at most 128 values. Returns the leaf count (at most
-// max_leaves written; n <= 128 * max_leaves / 2 keeps them all).
+// numpy reduces a float64 vector in chunks of 8192 values (its ufunc buffer
+// size): the pairwise recursion runs inside each chunk, and the chunk sums are
+// added left to right onto +0.0. This holds for contiguous and strided inputs
+// alike (np.diag(H) is a strided view).
+constexpr int kNpChunk = 8192;
+
+// Leaves of numpy's pairwise sum over n values, chunk by chunk and in order:
+// inside a chunk the recursion above splits until a piece has at most 128
+// values. Returns the leaf count (at most max_leaves written).
 __device__ int pw_leaves(int n, int max_leaves, int* off, int* len) {
-  int stack_off[32], stack_len[32], sp = 0, k = 0;
-  stack_off[sp] = 0;
-  stack_len[sp++] = n;
-  while (sp > 0) {
-    --sp;
-    const int o = stack_off[sp], m = stack_len[sp];
-    if (m <= 128) {
-      if (k < max_leaves) {
-        off[k] = o;
-        len[k] = m;
+  int k = 0;
+  for (int c0 = 0; c0 < n; c0 += kNpChunk) {
+    int stack_off[32], stack_len[32], sp = 0;
+    stack_off[sp] = c0;
+    stack_len[sp++] = min(kNpChunk, n - c0);
+    while (sp > 0) {
+      --sp;
+      const int o = stack_off[sp], m = stack_len[sp];
+      if (m <= 128) {
+        if (k < max_leaves) {
+          off[k] = o;
+          len[k] = m;
+        }
+        ++k;
+        continue;
       }
-      ++k;
-      continue;
+      int m2 = m / 2;
+      m2 -= m2 % 8;
+      stack_off[sp] = o + m2;  // right piece below the left one: leaves come out in order
+      stack_len[sp++] = m - m2;
+      stack_off[sp] = o;
+      stack_len[sp++] = m2;
     }
-    int m2 = m / 2;
-    m2 -= m2 % 8;
-    stack_off[sp] = o + m2;  // right piece below the left one: leaves come out in order
-    stack_len[sp++] = m - m2;
-    stack_off[sp] = o;
-    stack_len[sp++] = m2;
   }
   return k;
 }
 
-// The pairwise tree combined from its leaf sums, in the recursion's order.
+// One chunk's pairwise tree combined from its leaf sums, in the recursion's order.
 __device__ double pw_combine(int n, const double* leaf, int& k) {
   if (n <= 128) return leaf[k++];
   int n2 = n / 2;
@@ -335,32 +348,67 @@ __device__ double pw_combine(int n, const double* leaf, int& k) {
   return a + pw_combine(n - n2, leaf, k);
 }
 
-constexpr int kShiftLeaves = 1024;  // pairwise leaves summed in parallel (n <= 65536)
+// np.add.reduce of n float64 values from their leaf sums: chunk trees added in order.
+__device__ double np_sum_from_leaves(int n, const double* leaf) {
+  double total = 0.0;
+  int k = 0;
+  for (int c0 = 0; c0 < n; c0 += kNpChunk) total = total + pw_combine(min(kNpChunk, n - c0), leaf, k);
+  return total;
+}
+
+// np.add.reduce of n float64 values, serially.
+__device__ double np_sum_f64(const double* a, int n) {
+  double total = 0.0;
+  for (int c0 = 0; c0 < n; c0 += kNpChunk) total = total + pw_sum_f64(a + c0, min(kNpChunk, n - c0), 1);
+  return total;
+}
+
+constexpr int kShiftLeaves = 1024;  // pairwise leaves summed in parallel (n <= 131072)
 
 // Diagonal of the act-ordered H in visiting order, then the damping shift
 // damp * mean + 1e-8 (mean replaced by 1 when not positive), as ef.py:64-69
 // computes it from np.mean(np.diag(Hp)). One block per matrix: the leaves of
-// the pairwise sum run on separate threads, then one thread combines them in
-// the recursion's order (same additions, same order as the serial sum).
+// the chunked pairwise sum run on separate threads, then one thread combines
+// them in numpy's order (same additions, same order as the serial sum).
+//
+// The order is checked here as well: an entry outside [0, n) or a repeated one sets
+// bit 2 of fail[z] (marks: n ints of scratch per matrix, cleared here). Every
+// kernel of the factorization clamps the order's entries, so a bad order never
+// reads outside H.
 template <typename T>
 __global__ __launch_bounds__(256) void fact_shift_kernel(const T* H, int n, int64_t sH,
                                                          const int* order, int64_t sO,
                                                          const double* damp, double* diag_tmp,
-                                                         double* shift, const int* active) {
+                                                         double* shift, const int* active,
+                                                         int* marks, int64_t sM, int* fail) {
   __shared__ int loff[kShiftLeaves], llen[kShiftLeaves];
   __shared__ double lsum[kShiftLeaves];
-  __shared__ int nleaves;
+  __shared__ int nleaves, bad_order;
   const int z = blockIdx.x;
   if (active && !active[z]) return;
   const T* h = H + z * sH;
   const int* o = order ? order + z * sO : nullptr;
   double* dg = diag_tmp + (int64_t)z * n;
+  if (threadIdx.x == 0) bad_order = 0;
+  if (o) {
+    int* mk = marks + z * sM;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) mk[i] = 0;
+    __syncthreads();
+    int bad = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const int p = o[i];
+      if ((unsigned)p >= (unsigned)n) bad = 1;
+      else if (atomicExch(&mk[p], 1)) bad = 1;
+    }
+    if (bad) atomicOr(&bad_order, 1);
+  }
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    int p = o ? o[i] : i;
+    const int p = o ? clamp_index(o[i], n) : i;
     dg[i] = (double)h[(int64_t)p * n + p];
   }
   if (threadIdx.x == 0) nleaves = pw_leaves(n, kShiftLeaves, loff, llen);
   __syncthreads();
+  if (threadIdx.x == 0 && bad_order) fail[z] |= 2;
   const int nl = nleaves;
   if (nl <= kShiftLeaves) {
     for (int k = threadIdx.x; k < nl; k += blockDim.x) lsum[k] = pw_sum_f64(dg + loff[k], llen[k], 1);
@@ -368,12 +416,10 @@ __global__ __launch_bounds__(256) void fact_shift_kernel(const T* H, int n, int6
   }
   if (threadIdx.x == 0) {
     double total;
-    if (nl <= kShiftLeaves) {
-      int k = 0;
-      total = pw_combine(n, lsum, k);
-    } else {
-      total = pw_sum_f64(dg, n, 1);
-    }
+    if (nl <= kShiftLeaves)
+      total = np_sum_from_leaves(n, lsum);
+    else
+      total = np_sum_f64(dg, n);
     const double mean = total / (double)n;
     const double base = mean > 0.0 ? mean : 1.0;
     shift[z] = damp[z] * base + 1e-8;
@@ -399,8 +445,8 @@ __global__ void fact_prepare_gather_kernel(const T* H, int n, int64_t sH, const 
   if (j > i) return;
   double* a = A + z * sA;
   const int* o = order ? order + z * sO : nullptr;
-  int qi = o ? o[n - 1 - i] : n - 1 - i;
-  int qj = o ? o[n - 1 - j] : n - 1 - j;
+  int qi = o ? clamp_index(o[n - 1 - i], n) : n - 1 - i;
+  int qj = o ? clamp_index(o[n - 1 - j], n) : n - 1 - j;
   double v = (double)H[z * sH + (int64_t)qi * n + qj];
   if (i == j) v = v + shift[z];
   a[(int64_t)i * n + j] = v;
@@ -421,14 +467,14 @@ __global__ __launch_bounds__(256) void fact_prepare_kernel(const T* H, int n, in
   const int* o = order ? order + z * sO : nullptr;
   const T* h = H + z * sH;
   for (int r = 0; r < R && i0 + r < n; ++r) {
-    const int qi = o ? o[n - 1 - (i0 + r)] : n - 1 - (i0 + r);
+    const int qi = o ? clamp_index(o[n - 1 - (i0 + r)], n) : n - 1 - (i0 + r);
     for (int c = threadIdx.x; c < n; c += blockDim.x) rows[(int64_t)r * n + c] = h[(int64_t)qi * n + c];
   }
   __syncthreads();
   double* a = A + z * sA;
   const int jend = min(n, i0 + R);  // columns up to the block's last row
   for (int j = threadIdx.x; j < jend; j += blockDim.x) {
-    const int qj = o ? o[n - 1 - j] : n - 1 - j;
+    const int qj = o ? clamp_index(o[n - 1 - j], n) : n - 1 - j;
     for (int r = 0; r < R && i0 + r < n; ++r) {
       const int i = i0 + r;
       if (j <= i) {
@@ -541,7 +587,7 @@ __global__ __launch_bounds__(256) void fact_diag_kernel(double* A, int64_t sA, d
       Ak[(int64_t)r * n + i] = i <= r ? L[r][i] : 0.0;
     }
   }
-  if (i == 0 && bad) fail[z] = 1;
+  if (i == 0 && bad) atomicOr(&fail[z], 1);
 }
 
 // U[i][j] = X[n-1-i][n-1-j] for i <= j, 0 below the diagonal (OutT = float:
@@ -570,7 +616,9 @@ __global__ void fill_i32_kernel(int* p, int64_t count, int v) {
 }
 
 // ---------------------------------------------------------------- act order
-// order = stable argsort of -diag(H): rank of i = #{j: d_j > d_i} + #{j < i: d_j == d_i}.
+// order = stable argsort of -diag(H): rank of i = #{j: d_j > d_i} + #{j < i: d_j == d_i}
+// among the non-NaN entries; NaN entries come after all of them, by index, where
+// numpy's sort places NaN. The ranks are then a permutation for any input.
 // STAGE: the block first copies the diagonal into LDS (n * sizeof(T) bytes, dynamic),
 // so each diagonal entry leaves HBM once per block instead of once per thread.
 template <typename T, bool STAGE>
@@ -587,10 +635,12 @@ __global__ __launch_bounds__(256) void act_order_kernel(const T* H, int n, int64
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const double di = (double)(STAGE ? dg[i] : h[(int64_t)i * n + i]);
+  const bool nan_i = di != di;
   int rank = 0;
   for (int j = 0; j < n; ++j) {
     const double dj = (double)(STAGE ? dg[j] : h[(int64_t)j * n + j]);
-    rank += (dj > di) || (dj == di && j < i);
+    const bool nan_j = dj != dj;
+    rank += nan_i ? (!nan_j || j < i) : (dj > di || (dj == di && j < i));
   }
   order[z * sO + rank] = i;
 }
@@ -681,8 +731,11 @@ static int fact_attempt(const T* H, int64_t sH, int n, int batch, const int* ord
   double *A = w.A, *X = w.X, *Tm = w.Tm;
   fill_i32_kernel<<<(batch + 255) / 256, 256, 0, st>>>(w.fail, batch, 0);
   fill_kernel<<<1024, 256, 0, st>>>(X, (int64_t)nn * batch, 0.0);
+  // the order check's marks live in the GEMM scratch Tm, which the doubling GEMMs
+  // later overwrite without reading (beta = 0)
   fact_shift_kernel<T><<<batch, 256, 0, st>>>(H, n, sH, order, sO, w.damp_d, w.diag_tmp, w.shift,
-                                                w.active);
+                                                w.active, reinterpret_cast<int*>(Tm),
+                                                (int64_t)(2 * nn), w.fail);
   // rows of H staged per block: as many as fit in 48 KB, up to 8; rows longer than
   // 64 KB take the element-wise gather
   const int64_t row_bytes = (int64_t)n * sizeof(T);
@@ -791,6 +844,9 @@ static int fact_run(const T* H, int64_t sH, int n, int batch, const int* order, 
     if (int e = fact_attempt<T>(H, sH, n, batch, order, sO, U, u_dtype, sU, w, st)) return e;
     CP_HIP(hipMemcpyAsync(fail_h, w.fail, batch * sizeof(int), hipMemcpyDeviceToHost, st));
     CP_HIP(hipStreamSynchronize(st));
+    for (int z = 0; z < batch; ++z)
+      if (act[z] && (fail_h[z] & 2))
+        return set_error(CP_ERR_INDEX, "order of matrix %d is not a permutation of %d", z, n);
     int pending = 0;
     for (int z = 0; z < batch; ++z) {
       if (!act[z]) continue;

@@ -609,13 +609,18 @@ __global__ void ef_dev_store_kernel(const EfDevBatch batch, int count, EfDev* ds
   if ((int)threadIdx.x < count) dst[threadIdx.x] = batch.t[threadIdx.x];
 }
 
-// inv[order[jj]] = jj and sbidx[jj] = order[jj] / sub
+// inv[order[jj]] = jj and sbidx[jj] = order[jj] / sub. An order that is not a
+// permutation writes no entry out of range (sbidx of an out-of-range entry is 0), and
+// the readers of inv take its entries into [0, n), so unwritten ones stay harmless.
 __global__ void ef_index_kernel(const EfDev* __restrict__ tab) {
   const EfDev& t = tab[blockIdx.y];
   const int jj = blockIdx.x * blockDim.x + threadIdx.x;
   if (jj >= t.n) return;
   const int c = t.order[jj];
-  if ((unsigned)c >= (unsigned)t.n) return;  // not a permutation: no write out of range
+  if ((unsigned)c >= (unsigned)t.n) {
+    t.sbidx[jj] = 0;
+    return;
+  }
   t.inv[c] = jj;
   t.sbidx[jj] = c / t.sub;
 }
@@ -813,7 +818,8 @@ __global__ __launch_bounds__(256) void ef_pack_kernel(const EfDev* __restrict__ 
   __shared__ __align__(16) uint8_t codes[256 * kPackPitch];  // [column][row]
   const int t = threadIdx.x;
   {
-    const uint8_t* src = T.LT + (int64_t)T.inv[sb * 256 + t] * nrow + r0;
+    const int v = T.inv[sb * 256 + t];
+    const uint8_t* src = T.LT + (int64_t)((unsigned)v < (unsigned)n ? v : 0) * nrow + r0;
     uint8_t* dst = codes + t * kPackPitch;
     if ((nrow & 15) == 0) {  // 16-byte aligned runs; rows is a multiple of 16
       for (int q = 0; q < rows / 16; ++q) {

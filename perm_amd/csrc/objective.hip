@@ -175,11 +175,13 @@ __global__ __launch_bounds__(64) void err_colsum_kernel(const ErrDev* __restrict
 }
 
 // --------------------------------------------------------------- pairwise sum
-// numpy's pairwise summation of a contiguous float64 array of n values v(i):
-// fewer than 8 sequentially from 0.0; up to 128 with eight strided accumulators,
+// numpy's summation of a float64 array of n values v(i). It reduces in chunks
+// of 8192 values (its ufunc buffer size), adding the chunk sums left to right
+// onto +0.0. Inside a chunk the sum is pairwise: fewer than 8 values
+// sequentially from 0.0; up to 128 with eight strided accumulators,
 // ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)), then the remainder; longer runs split at
 // n/2 rounded down to a multiple of 8, the two halves summed recursively. The
-// recursion runs on an explicit stack (depth <= 32 for n < 2^36).
+// recursion runs on an explicit stack (depth <= 32).
 template <class V>
 __device__ double pw_leaf(const V& v, int64_t lo, int64_t n) {
   if (n < 8) {
@@ -201,7 +203,7 @@ __device__ double pw_leaf(const V& v, int64_t lo, int64_t n) {
 }
 
 template <class V>
-__device__ double pw_sum(const V& v, int64_t n) {
+__device__ double pw_tree(const V& v, int64_t lo0, int64_t n) {
   struct Frame {
     int64_t lo, n;
     double left;
@@ -209,7 +211,7 @@ __device__ double pw_sum(const V& v, int64_t n) {
   };
   Frame st[32];
   int sp = 0;
-  st[0] = Frame{0, n, 0.0, 0};
+  st[0] = Frame{lo0, n, 0.0, 0};
   for (;;) {
     Frame& f = st[sp];
     if (f.n <= 128) {
@@ -238,6 +240,15 @@ __device__ double pw_sum(const V& v, int64_t n) {
   }
 }
 
+constexpr int64_t kNpChunk = 8192;
+
+template <class V>
+__device__ double pw_sum(const V& v, int64_t n) {
+  double s = 0.0;
+  for (int64_t c0 = 0; c0 < n; c0 += kNpChunk) s = s + pw_tree(v, c0, n - c0 < kNpChunk ? n - c0 : kNpChunk);
+  return s;
+}
+
 __global__ __launch_bounds__(64) void err_final_kernel(const ErrDev* __restrict__ tab,
                                                        double* __restrict__ out) {
   if (threadIdx.x != 0) return;
@@ -262,7 +273,7 @@ __global__ __launch_bounds__(64) void err_final_kernel(const ErrDev* __restrict_
   } else {
     s = pw_sum([=](int64_t i) { return ce[i]; }, T.n);
   }
-  out[T.slot] = 0.0 + s;
+  out[T.slot] = s;
 }
 
 __global__ void err_clear_kernel(int* __restrict__ bad, int count) {

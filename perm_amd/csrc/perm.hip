@@ -4,7 +4,9 @@
 // dst[r][c] = src[row_perm[r]][col_perm[c]] (identity where a permutation is
 // NULL), for 1-, 2-, 4- or 8-byte elements. Pure HBM-bound index work: each
 // thread writes one output element of a row, so stores are coalesced and the
-// gathered loads stay inside one source row.
+// gathered loads stay inside one source row. An index outside the axis is
+// clamped into it (the host wrapper rejects such permutations before the call),
+// so no read ever leaves src.
 #include <hip/hip_runtime.h>
 
 #include "cp_host.h"
@@ -17,12 +19,12 @@ __global__ __launch_bounds__(256) void gather_kernel(const T* __restrict__ src, 
                                                      const int* __restrict__ cp_, int64_t rows,
                                                      int64_t cols) {
   const int64_t r = blockIdx.y;
-  const int64_t sr = rp ? rp[r] : r;
+  const int64_t sr = rp ? min(max((int64_t)rp[r], (int64_t)0), rows - 1) : r;
   const T* s = src + sr * cols;
   T* o = dst + r * cols;
   for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < cols;
        c += (int64_t)gridDim.x * blockDim.x)
-    o[c] = s[cp_ ? cp_[c] : c];
+    o[c] = s[cp_ ? min(max((int64_t)cp_[c], (int64_t)0), cols - 1) : c];
 }
 
 }  // namespace cp

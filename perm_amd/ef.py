@@ -44,17 +44,34 @@ def act_order_dev(H, enabled=True):
     return order
 
 
-def factor_dev(H, order=None, damp=0.01, max_tries=6, out_dtype=torch.float32):
+def _order_dev(order, batch, n, device, checked):
+    """The visiting order as a device int32 [batch, n] tensor. A caller's order is
+    checked first (every row a permutation of n; negative entries count from the end,
+    as numpy's): IndexError before anything is launched. ``checked``: the order comes
+    from act_order_dev, which always gives a permutation."""
+    if order is None:
+        return None
+    if not checked:
+        if int(np.prod(np.shape(order))) != batch * n:
+            raise ValueError(f"order has shape {tuple(np.shape(order))}, expected {batch} x {n}")
+        order = _lib.check_index(order, n, "order", permutation=True)
+    if not isinstance(order, torch.Tensor):
+        order = torch.from_numpy(np.ascontiguousarray(order))
+    return order.to(device=device, dtype=torch.int32).reshape(batch, n).contiguous()
+
+
+def factor_dev(H, order=None, damp=0.01, max_tries=6, out_dtype=torch.float32, checked=False):
     """Upper U with U^T U = inv(Hp + lambda I), Hp = H[order][:, order], on the device.
 
-    H: [n, n] or [batch, n, n] CUDA tensor (float32/float64, contiguous).
+    H: [n, n] or [batch, n, n] CUDA tensor (float32/float64, contiguous). ``order``
+    (numpy array or tensor) must be a permutation per matrix: IndexError otherwise,
+    before any launch (``checked`` skips the check for orders from act_order_dev).
     Returns (U [.., n, n] of out_dtype, damp actually used per matrix)."""
-    lib = _lib.load()
     squeeze = H.dim() == 2
     Hb = H.unsqueeze(0) if squeeze else H
     batch, n = Hb.shape[0], Hb.shape[-1]
-    if order is not None:
-        order = order.reshape(batch, n).to(torch.int32).contiguous()
+    order = _order_dev(order, batch, n, H.device, checked)
+    lib = _lib.load()
     U = torch.empty((batch, n, n), dtype=out_dtype, device=H.device)
     ws = _lib.workspace(lib.cp_chol_ws_bytes(n, batch), H.device)
     used = (ctypes.c_double * batch)()
@@ -66,17 +83,16 @@ def factor_dev(H, order=None, damp=0.01, max_tries=6, out_dtype=torch.float32):
     return (U[0] if squeeze else U), list(used)
 
 
-def factor_dev_async(H, order=None, damp=0.01, out_dtype=torch.float32):
+def factor_dev_async(H, order=None, damp=0.01, out_dtype=torch.float32, checked=False):
     """One attempt of ``factor_dev`` at ``damp``, queued on the current stream
     without waiting on it. Returns (U, flags): flags is an int32 device tensor
     [batch] whose set entries mark matrices that met a non-positive pivot (their
     U is meaningless and ``factor_dev`` must redo them, with escalation)."""
-    lib = _lib.load()
     squeeze = H.dim() == 2
     Hb = H.unsqueeze(0) if squeeze else H
     batch, n = Hb.shape[0], Hb.shape[-1]
-    if order is not None:
-        order = order.reshape(batch, n).to(torch.int32).contiguous()
+    order = _order_dev(order, batch, n, H.device, checked)
+    lib = _lib.load()
     U = torch.empty((batch, n, n), dtype=out_dtype, device=H.device)
     flags = torch.empty(batch, dtype=torch.int32, device=H.device)
     ws = _lib.workspace(lib.cp_chol_ws_bytes(n, batch), H.device)
@@ -104,12 +120,17 @@ def _ws_for(tensors):
     return arr, lib.cp_ef_ws_bytes(arr, len(tensors))
 
 
-def ef_encode_dev(items, n_iter=2, mode=_lib.CP_EF_EXACT):
+def ef_encode_dev(items, n_iter=2, mode=_lib.CP_EF_EXACT, checked=False):
     """Batched EF on device tensors.
 
     items: list of dicts with keys ttype, x [nrow, n] f32, qw [n] f32 or None,
-    U [n, n] f32 (visiting order), order [n] int32, and optional ``recon`` flag.
+    U [n, n] f32 (visiting order), order [n] int32 (a permutation: IndexError
+    otherwise, before any launch; ``checked`` skips that for orders from
+    act_order_dev), and optional ``recon`` flag.
     Returns a list of (raw uint8 [nrow, row_bytes], recon f32 or None)."""
+    if not checked:
+        items = [dict(it, order=_order_dev(it["order"], 1, it["x"].shape[1], it["x"].device,
+                                           False).reshape(-1)) for it in items]
     lib = _lib.load()
     keep, structs, outs = [], [], []
     for it in items:
@@ -153,9 +174,9 @@ def ef_encode(x, ttype, qw, H, n_iter=2, damp=0.01, act_order=True, mode="exact"
                            else torch.float32)
     qd = _lib.to_device(qw, torch.float32)[0].reshape(-1) if qw is not None else None
     order = act_order_dev(Hd, act_order)
-    U, _ = factor_dev(Hd, order, damp)
+    U, _ = factor_dev(Hd, order, damp, checked=True)
     (raw, rec), = ef_encode_dev([{"ttype": ttype, "x": xd, "qw": qd, "U": U, "order": order}],
-                                n_iter, MODES[mode])
+                                n_iter, MODES[mode], checked=True)
     if host:
         return _lib.to_host(raw), _lib.to_host(rec)
     return raw, rec
@@ -192,7 +213,7 @@ def encode_size_classes(classes, n_iter=2, mode="exact", damp=0.01, act_order=Tr
         s.wait_stream(cur)
         with torch.cuda.stream(s):
             order = act_order_dev(Hb, act_order)
-            U, flags = factor_dev_async(Hb, order, damp)
+            U, flags = factor_dev_async(Hb, order, damp, checked=True)
         facs.append((order, U, flags))
     # EFs are queued smallest matrices first: their factorizations end first, and the
     # host time spent queueing the others would otherwise delay them
@@ -201,7 +222,7 @@ def encode_size_classes(classes, n_iter=2, mode="exact", damp=0.01, act_order=Tr
         (_, build), s, (order, U, _) = classes[k], streams[k], facs[k]
         with torch.cuda.stream(s):
             outs[k] = ef_encode_dev(build(U, order), n_iter, MODES[mode] if isinstance(mode, str)
-                                    else mode)
+                                    else mode, checked=True)
     for s in streams:
         cur.wait_stream(s)
     for res in outs:
@@ -214,9 +235,9 @@ def encode_size_classes(classes, n_iter=2, mode="exact", damp=0.01, act_order=Tr
         if bad:
             Hb, build = classes[k]
             order = facs[k][0]
-            U, _ = factor_dev(Hb, order, damp)
+            U, _ = factor_dev(Hb, order, damp, checked=True)
             outs[k] = ef_encode_dev(build(U, order), n_iter, MODES[mode] if isinstance(mode, str)
-                                    else mode)
+                                    else mode, checked=True)
     return outs
 
 

@@ -28,11 +28,13 @@ def identity_perms(dims):
                    for _ in range(dims["n_layers"])]}
 
 
-def _check(p, n):
-    p = np.asarray(p)
-    if p.shape != (n,) or not np.array_equal(np.sort(p), np.arange(n)):
-        raise ValueError(f"not a permutation of {n}")
-    return p
+def _check(p, n, what="permutation"):
+    """p as an int32 permutation of n, checked before any launch: a wrong length raises
+    ValueError, an entry out of range or a repeated one IndexError (numpy's fancy
+    indexing raises IndexError for the first; the second is not a permutation)."""
+    if np.shape(p) != (n,):
+        raise ValueError(f"{what} has shape {np.shape(p)}, expected ({n},)")
+    return _lib.check_index(p, n, what, permutation=True)
 
 
 def v_output_index(perms, layer, dims):
@@ -57,17 +59,19 @@ def o_input_index(perms, layer, dims):
 
 
 def input_perm(gguf_name, perms, dims):
-    """Permutation of a tensor's input axis (GGUF ne[0]) or None (qwen3.py:106-123)."""
+    """Permutation of a tensor's input axis (GGUF ne[0]) or None (qwen3.py:106-123).
+    Each returned permutation is checked (length, range, uniqueness) before it is used
+    to move weights, importance vectors or Hessians."""
     if gguf_name in ("token_embd.weight", "output.weight"):
-        return np.asarray(perms["res"])
+        return _check(perms["res"], dims["d_model"], "res permutation")
     if not gguf_name.startswith("blk."):
         return None
     parts = gguf_name.split(".")
     layer, kind = int(parts[1]), parts[2]
     if kind in RES_INPUT_KINDS:
-        return np.asarray(perms["res"])
+        return _check(perms["res"], dims["d_model"], "res permutation")
     if kind == "ffn_down":
-        return np.asarray(perms["ffn"][layer])
+        return _check(perms["ffn"][layer], dims["d_ffn"], f"ffn permutation of layer {layer}")
     if kind == "attn_output":
         return o_input_index(perms, layer, dims)
     return None
@@ -80,25 +84,30 @@ def inverse(p):
     return inv
 
 
-def _dev_index(p, device):
+def _dev_index(p, size, device, what):
+    """A row or column index checked on the host (numpy's rules, negative entries from
+    the end; IndexError before any launch) as a device int32 tensor."""
     if p is None:
         return None
+    if np.shape(p) != (size,):
+        raise ValueError(f"{what} has shape {tuple(np.shape(p))}, the axis has {size} entries")
+    p = _lib.check_index(p, size, what)
     if isinstance(p, torch.Tensor):
-        return p.to(device=device, dtype=torch.int32).contiguous()
-    return torch.from_numpy(np.ascontiguousarray(np.asarray(p), dtype=np.int32)).to(device)
+        return p.to(device=device).contiguous()
+    return torch.from_numpy(np.ascontiguousarray(p)).to(device)
 
 
 def gather(t, rows=None, cols=None):
-    """t[rows][:, cols] on the device (None = all). t: 2-D CUDA tensor of 1/2/4/8-byte
-    elements. The permutations must be in range."""
-    lib = _lib.load()
+    """t[rows][:, cols] on the device (None = all), as numpy's t[np.ix_(rows, cols)].
+    t: 2-D CUDA tensor of 1/2/4/8-byte elements; rows / cols have one entry per row /
+    column of t. An index out of range raises IndexError before anything is launched."""
     if t.dim() != 2:
         raise ValueError("gather needs a 2-D tensor")
-    t = t.contiguous()
     R, C = t.shape
-    rp, cp = _dev_index(rows, t.device), _dev_index(cols, t.device)
-    if rp is not None and rp.numel() != R or cp is not None and cp.numel() != C:
-        raise ValueError("permutation length does not match the tensor")
+    rp = _dev_index(rows, R, t.device, "row index")
+    cp = _dev_index(cols, C, t.device, "column index")
+    lib = _lib.load()
+    t = t.contiguous()
     out = torch.empty_like(t)
     st = lib.cp_permute_gather(_lib.ptr(t), _lib.ptr(out), _lib.ptr(rp), _lib.ptr(cp), R, C,
                                t.element_size(), _lib.stream_ptr())

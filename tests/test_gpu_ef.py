@@ -53,14 +53,44 @@ def test_factor_matches_closed_form(ef, n):
     assert np.abs(U.T @ U @ Hd - np.eye(n)).max() < 1e-9
 
 
-@pytest.mark.parametrize("n", [100, 1000, 3000])
+def _np_tree(v):
+    """One pairwise tree over all of v (numpy's order only up to 8192 values)."""
+    n = len(v)
+    if n < 8:
+        r = 0.0
+        for a in v:
+            r = r + a
+        return r
+    if n <= 128:
+        r = list(v[:8])
+        i = 8
+        while i + 8 <= n:
+            for j in range(8):
+                r[j] = r[j] + v[i + j]
+            i += 8
+        s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]))
+        for a in v[i:]:
+            s = s + a
+        return s
+    n2 = n // 2
+    n2 -= n2 % 8
+    return _np_tree(v[:n2]) + _np_tree(v[n2:])
+
+
+@pytest.mark.parametrize("n", [100, 1000, 3000, 9000, 14336])
 def test_factor_damping_shift_is_numpys_mean(ef, n):
     """Diagonal H: U = diag(1 / sqrt(h + shift)) with correctly rounded sqrt and
     division, so U equals numpy's bit for bit only if the damping shift does,
-    i.e. only if the mean of diag(H) is summed in numpy's pairwise order."""
+    i.e. only if the mean of diag(H) is summed in numpy's order (pairwise inside
+    chunks of 8192 values, the chunk sums added in order)."""
     _say(f"damping shift n={n}")
     rng = np.random.default_rng(n)
     h = 10.0 ** rng.uniform(-3, 7, n)
+    draw = 0
+    while n > 8192 and _np_tree(list(h)) == np.add.reduce(h):
+        # a draw on which one tree over all n values gives another sum than numpy's
+        draw += 1
+        h = 10.0 ** np.random.default_rng(n + 1000 * draw).uniform(-3, 7, n)
     H = np.diag(h)
     shift = 0.01 * np.mean(np.diag(H)) + 1e-8
     seq = 0.0
@@ -69,10 +99,14 @@ def test_factor_damping_shift_is_numpys_mean(ef, n):
     if n > 128:
         assert 0.01 * (seq / n) + 1e-8 != shift
     Hd = torch.from_numpy(H).cuda()
+    del H
     U, used = ef.factor_dev(Hd, None, 0.01, out_dtype=torch.float64)
-    U = U.cpu().numpy()
+    del Hd
     assert used == [0.01]
-    assert np.array_equal(U, np.diag(1.0 / np.sqrt(h + shift)))
+    diag = torch.diagonal(U).cpu().numpy()
+    assert int(torch.count_nonzero(U)) == n
+    del U
+    assert np.array_equal(diag, 1.0 / np.sqrt(h + shift))
 
 
 def test_factor_with_order_and_f32_output(ef):
@@ -111,6 +145,53 @@ def test_factor_escalates_like_reference(ef, capfd):
     # the oracle escalates to the same damp and lands on the same factor
     U_ref = E.inv_upper_factor(H, 0.01, log=False)
     assert np.abs(U - U_ref).max() / np.abs(U_ref).max() < 1e-9
+
+
+def test_nan_diagonal_orders_last_and_raises_linalg_error(ef):
+    """numpy's argsort puts NaN last, and LAPACK's Cholesky fails on a NaN pivot at every
+    damping, so the reference raises LinAlgError. The GPU order is a permutation with the
+    NaN columns last (by index), and the factor raises the same error."""
+    n = 256
+    H = correlated_hessian(n, 1024, seed=12)
+    H[5, 5] = np.nan
+    H[77, 77] = np.nan
+    Hd = torch.from_numpy(H).cuda()
+    order = ef.act_order_dev(Hd).cpu().numpy()
+    assert np.array_equal(order, np.argsort(-np.diag(H), kind="stable"))
+    assert order[-2:].tolist() == [5, 77]
+    with pytest.raises(np.linalg.LinAlgError):
+        ef.factor_dev(Hd, torch.from_numpy(order).cuda(), 0.01)
+    with pytest.raises(np.linalg.LinAlgError):
+        ef.ef_encode(heavy_tailed(4, n, seed=1), "Q2_K", None, H)
+
+
+def test_factor_flags_an_order_that_is_not_a_permutation(ef):
+    """Called through the C ABI with a bad order (no host check in between), the factor
+    clamps every read of it and reports CP_ERR_INDEX; the async form sets bit 1 of the
+    matrix's flag and leaves the other matrix alone."""
+    from perm_amd import _lib
+    lib = _lib.load()
+    n = 128
+    Hs = np.stack([correlated_hessian(n, 512, seed=s) for s in (1, 2)])
+    Hb = torch.from_numpy(Hs).cuda()
+    order = torch.arange(n, dtype=torch.int32, device="cuda").repeat(2, 1)
+    order[1, 3] = 1000      # out of range
+    order[1, 9] = -4        # out of range
+    ws = _lib.workspace(lib.cp_chol_ws_bytes(n, 2))
+    U = torch.empty(2, n, n, device="cuda")
+    st = lib.cp_chol_inv_upper(_lib.ptr(Hb), 1, n, 2, _lib.ptr(order), 0.01, 6, _lib.ptr(U), 0,
+                               None, _lib.ptr(ws), ws.numel(), _lib.stream_ptr())
+    assert st == _lib.CP_ERR_INDEX
+    with pytest.raises(IndexError):
+        _lib.check(st)
+    order[1, 3], order[1, 9] = 3, 3  # in range, repeated
+    flags = torch.full((2,), 7, dtype=torch.int32, device="cuda")
+    _lib.check(lib.cp_chol_inv_upper_async(_lib.ptr(Hb), 1, n, 2, _lib.ptr(order), 0.01,
+                                           _lib.ptr(U), 0, _lib.ptr(flags), _lib.ptr(ws),
+                                           ws.numel(), _lib.stream_ptr()))
+    assert flags.cpu().tolist() == [0, 2]
+    U0 = E.inv_upper_factor(Hs[0], 0.01).astype(F32)
+    assert np.abs(U[0].cpu().numpy() - U0).max() <= 4 * np.spacing(np.abs(U0).max())
 
 
 def test_factor_gives_up(ef):
@@ -177,6 +258,79 @@ def test_full_gpu_path_within_gates(ef, tt):
     _say(f"  codes agree {agree:.6f}, err rel diff {abs(e_gpu - e_ref) / e_ref:.2e}")
     assert agree >= 0.999
     assert abs(e_gpu - e_ref) / e_ref < 1e-3
+
+
+def test_fp16_stored_rank_deficient_hessian(ef, tmp_path):
+    """The reference's faithful-path case (test_ef_cholesky_robust.py:67-79): a rank-
+    deficient X^T X (128 rows for n = 512, four rows x60) through the fp16 Hessian storage
+    (here the GPU pack / expand of perm_amd.hessians). The GPU factor takes the oracle's
+    damping step, agrees with its factor within 1e-9 relative, and the EF encode on it
+    stays inside the gates."""
+    from perm_amd import hessians as hs
+    n = 512
+    rng = np.random.default_rng(2)
+    A = rng.standard_normal((n // 4, n))
+    A[:4] *= 60.0
+    H = (A.T @ A).astype(np.float32)
+    hs.save_hessians({"blk.0.ffn_down.weight": {"H": H, "n": 4096}}, str(tmp_path))
+    H_rt, _ = hs.load_hessian(str(tmp_path), "blk.0.ffn_down.weight")
+    assert H_rt.dtype == np.float64
+    Hd = torch.from_numpy(H_rt).cuda()
+    U, used = ef.factor_dev(Hd, None, 0.01, out_dtype=torch.float64)
+    U_ref = E.inv_upper_factor(H_rt, 0.01, log=False)
+    assert used == [0.01]
+    U = U.cpu().numpy()
+    assert np.abs(U - U_ref).max() / np.abs(U_ref).max() < 1e-9
+    W = heavy_tailed(96, n, seed=4)
+    qw = (np.diag(H_rt) / 4096).astype(F32)
+    raw, rec = ef.ef_encode(W, "Q2_K", qw, H_rt)
+    want_raw, want_rec = E.ef_encode(W, "Q2_K", qw, H_rt, stable_order=True)
+    agree = (_codes("Q2_K", raw, *W.shape) == _codes("Q2_K", want_raw, *W.shape)).mean()
+    e_gpu, e_ref = E.h_weighted_err(W, rec, H_rt), E.h_weighted_err(W, want_rec, H_rt)
+    _say(f"  rank-deficient fp16 H: codes agree {agree:.6f}, err rel diff "
+         f"{abs(e_gpu - e_ref) / e_ref:.2e}")
+    assert agree >= 0.999 and abs(e_gpu - e_ref) / e_ref < 1e-3
+
+
+def _damped_near_singular(n, rel, seed):
+    """H with eigenvalues linspace(1, 100) except the smallest, placed so that the damped
+    matrix H + (0.01 mean(diag H) + 1e-8) I has smallest eigenvalue rel x the shift
+    (negative rel: not positive definite at the first damping)."""
+    eig = np.linspace(1.0, 100.0, n)
+    S, c = eig[1:].sum(), 0.01 / n
+    eig[0] = -(c * S + 1e-8) * (1 - rel) / (1 + c * (1 - rel))
+    return _spectrum_matrix(n, eig, seed)
+
+
+@pytest.mark.parametrize("rel", [1e-2, 1e-6, 1e-11, -1e-11, -1e-6, -1e-2, -30.0])
+def test_near_singular_damped_hessian_escalates_like_reference(ef, rel):
+    """Damped matrices close to singular on both sides: the GPU takes the reference's
+    escalation step every time (ef.py:60-84: LAPACK inverse, then Cholesky of it; here the
+    Cholesky of the reversed damped H). The two criteria part only where the damped
+    matrix's condition number reaches about 1e16 (smallest eigenvalue within ~1e-14 of
+    the shift), where the reference's own LAPACK inverse is decided by rounding; the
+    cases here stay 1000x clear of that band. Where the factor is well conditioned it
+    agrees with the oracle's within 1e-9 relative."""
+    n = 256
+    H = _damped_near_singular(n, rel, seed=3)
+    U_ref = E.inv_upper_factor(H, 0.01, log=False)
+    d_ref = None
+    for k in range(6):  # the oracle's damping step, read back from its closed form
+        Hd = H + (0.01 * 10 ** k * np.mean(np.diag(H)) + 1e-8) * np.eye(n)
+        try:
+            Hi = np.linalg.inv(Hd)
+            if np.array_equal(np.linalg.cholesky((Hi + Hi.T) / 2).T, U_ref):
+                d_ref = 0.01 * 10 ** k
+                break
+        except np.linalg.LinAlgError:
+            continue
+    assert d_ref is not None
+    U, used = ef.factor_dev(torch.from_numpy(H).cuda(), None, 0.01, out_dtype=torch.float64)
+    assert np.isclose(used[0], d_ref, rtol=1e-12), (used, d_ref)
+    U = U.cpu().numpy()
+    assert np.all(np.isfinite(U)) and np.array_equal(U, np.triu(U))
+    if used[0] > 0.01 or rel >= 1e-2:  # well conditioned after the shift
+        assert np.abs(U - U_ref).max() / np.abs(U_ref).max() < 1e-9
 
 
 def test_ef_beats_rtn_on_gpu(ef):

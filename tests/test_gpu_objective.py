@@ -51,6 +51,44 @@ def test_tensor_err_bit_identical(ob, tt, dtype):
         assert got == want, (k, got, want)
 
 
+def _one_tree(v):
+    """Pairwise sum of v as one tree (numpy's order only up to 8192 values)."""
+    n = len(v)
+    if n <= 128:
+        r = list(v[:8])
+        i = 8
+        while i + 8 <= n:
+            r = [r[j] + v[i + j] for j in range(8)]
+            i += 8
+        s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]))
+        for a in v[i:]:
+            s = s + a
+        return s
+    n2 = n // 2
+    n2 -= n2 % 8
+    return _one_tree(v[:n2]) + _one_tree(v[n2:])
+
+
+@pytest.mark.parametrize("tt", ["Q4_K", "Q8_0"])
+def test_total_over_more_than_8192_columns(ob, tt):
+    """numpy sums the weighted column errors in chunks of 8192 values; with 9216 columns
+    a single pairwise tree gives another total on this data, and the GPU gives numpy's."""
+    from oracle import kquant_oracle as K
+    n = 9216
+    x = heavy_tailed(6, n, seed=8)
+    rng = np.random.default_rng(14)
+    wvec = 10.0 ** rng.uniform(-3, 5, n)
+    qw = (10.0 ** rng.uniform(-2, 3, n)).astype(F32)
+    rec = K.roundtrip(x, tt, None)
+    colerr = ((rec.astype(np.float64) - x.astype(np.float64)) ** 2).sum(0)
+    assert _one_tree(list(colerr * wvec)) != float((colerr * wvec).sum())
+    for k, v in enumerate([dict(wvec=wvec), dict(qw=qw), dict(qw=qw, perm=rng.permutation(n))]):
+        _say(f"tensor_err {tt} n={n} variant {k}")
+        want = Po.tensor_err(x, tt, v.get("qw"), perm=v.get("perm"), wvec=v.get("wvec"))
+        got = ob.tensor_err(x, tt, v.get("qw"), perm=v.get("perm"), wvec=v.get("wvec"))
+        assert got == want, (k, got, want)
+
+
 def test_batch_equals_single_calls(ob):
     """One pass over mixed types, shapes, dtypes and options equals the single calls."""
     rng = np.random.default_rng(3)

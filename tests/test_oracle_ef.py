@@ -118,6 +118,101 @@ def test_sweep_matches_scalar_recurrence(tt):
     assert np.array_equal(got, want)
 
 
+def _row_grid(tt, raw_row, n):
+    """One row's committed grid, read sub-block by sub-block from its container bytes
+    with the golden-pinned field readers: (steps dl[n/sub], offsets ml or None)."""
+    sub = K.SUB_W[tt]
+    bp = K.BYTES_PER_SB[tt]
+    dl, ml = [], []
+    for sb in range(n // 256):
+        b = raw_row[sb * bp:(sb + 1) * bp][None]
+        if tt == "Q2_K":
+            d, m = K._half_field(b, 80)[0], K._half_field(b, 82)[0]
+            sc = [(int(v) & 0xF, int(v) >> 4) for v in b[0, 0:16]]
+        elif tt == "Q3_K":
+            d, m = K._half_field(b, 108)[0], None
+            sc = [(int(v) - 32, 0) for v in K.unpack_scales_q3(b[:, 96:108])[0]]
+        elif tt in ("Q4_K", "Q5_K"):
+            d, m = K._half_field(b, 0)[0], K._half_field(b, 2)[0]
+            s_, m_ = K.unpack_scales_k4(b[:, 4:16])
+            sc = list(zip((int(v) for v in s_[0]), (int(v) for v in m_[0])))
+        else:
+            d, m = K._half_field(b, 208)[0], None
+            sc = [(int(v), 0) for v in b[0, 192:208].view(np.int8)]
+        for s_k, m_k in sc:
+            dl.append(F32(d * F32(s_k)))
+            if m is not None:
+                ml.append(F32(m * F32(m_k)))
+    return dl, (ml if ml else None)
+
+
+def _row_ef(x_row, tt, qw, U, order, n_iter, restart_from="x", commit_on="targets"):
+    """ef_encode (ef.py:179-218) for ONE row, written from the GPTQ recurrence alone:
+    each iteration commits the codec (K.QUANTIZE, golden-pinned) on the current targets,
+    reads the row's grid from those bytes, sweeps the visiting order starting again from
+    the original weights, and scatters the compensated targets back into storage order.
+    Returns (final codes in storage order, the targets the last commit saw).
+    ``restart_from`` / ``commit_on`` select the two planted mistakes a test must catch:
+    sweeping from the current targets instead of x, and committing every pass on x."""
+    n = x_row.size
+    sub = K.SUB_W[tt]
+    lo, hi = E.GRID[tt][1], E.GRID[tt][2]
+    targets = x_row.astype(F32).copy()
+    codes = np.zeros(n, np.int64)
+    committed_on = None
+    for _ in range(n_iter):
+        committed_on = (targets if commit_on == "targets" else x_row).astype(F32).copy()
+        raw = K.QUANTIZE[tt](committed_on[None], qw)[0]
+        dl, ml = _row_grid(tt, raw, n)
+        start = x_row if restart_from == "x" else targets
+        t = np.array([start[order[jj]] for jj in range(n)], F32)  # visiting order
+        for jj in range(n):
+            j = order[jj]
+            d = dl[j // sub]
+            m = ml[j // sub] if ml is not None else F32(0)
+            if d == 0:
+                q, e = 0, F32(0)
+            else:
+                q = int(K.rint_magic(np.array([F32(F32(t[jj] + m) / d)]))[0])
+                q = min(max(q, lo), hi)
+                e = F32(F32(t[jj] - F32(F32(d * F32(q)) - m)) / U[jj, jj])
+            codes[j] = q
+            # fl(t - fl(e * u)) elementwise: numpy float32 arithmetic, no fused terms
+            t[jj + 1:] = t[jj + 1:] - (e * U[jj, jj + 1:]).astype(F32)
+        targets = np.empty(n, F32)
+        for jj in range(n):
+            targets[order[jj]] = t[jj]
+    return codes, committed_on
+
+
+@pytest.mark.parametrize("tt", ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"])
+def test_ef_loop_matches_row_restatement(tt):
+    """The oracle's whole ef_encode loop equals the per-row restatement for n_iter 1-3:
+    the codes (read back with the golden-pinned code readers) and the scale fields (the
+    codec's own bytes on the targets of the last commit). The two planted mistakes give
+    other bytes on the same inputs, so an oracle carrying either one fails this test."""
+    n, nrow = (256, 3) if tt in ("Q3_K", "Q6_K") else (512, 2)
+    W = heavy_tailed(nrow, n, seed=21)
+    H = correlated_hessian(n, 2048, seed=22)
+    qw = (np.diag(H) / 2048).astype(F32) if tt != "Q6_K" else None
+    order = E.act_order(H, stable=True)
+    U = E.inv_upper_factor(H[np.ix_(order, order)]).astype(F32)
+    for n_iter in (1, 2, 3):
+        raw, rec = E.ef_encode(W, tt, qw, H, n_iter=n_iter, U=U, order=order)
+        codes = K.stored_codes(tt, raw).reshape(nrow, n).astype(np.int64)  # signed codes
+        for r in range(nrow):
+            want, seen = _row_ef(W[r], tt, qw, U, order, n_iter)
+            assert np.array_equal(codes[r], want), (n_iter, r)
+            commit = K.QUANTIZE[tt](seen[None], qw)[0]
+            assert np.array_equal(E.write_codes(tt, commit[None], want[None], 1, n)[0], raw[r])
+        assert np.array_equal(rec, K.DEQUANTIZE[tt](raw, n))
+        if n_iter == 1:
+            continue
+        for mistake in ({"restart_from": "targets"}, {"commit_on": "x"}):
+            planted = [_row_ef(W[r], tt, qw, U, order, n_iter, **mistake)[0] for r in range(nrow)]
+            assert not np.array_equal(codes, np.stack(planted)), (n_iter, mistake)
+
+
 @pytest.mark.parametrize("tt", ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"])
 def test_diagonal_hessian_reduces_to_codec(tt):
     """With a diagonal H nothing propagates: every superblock whose sub-block steps are
