@@ -145,6 +145,23 @@ int cp_ef_encode(int ttype, const float* x, int64_t nrow, int64_t n, const float
                  const float* U, const int32_t* order, int n_iter, uint8_t* raw, float* recon,
                  void* ws, size_t ws_bytes, void* stream);
 
+/* cp_ef_encode without a caller workspace and without any device allocation. No
+ * counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The EF workspace is a static device array of cp_ef_noalloc_max_ws_bytes() bytes
+ * (64 MiB: any tensor up to about 3.8 M weights, e.g. every Qwen3-0.6B linear) that
+ * each GPU the library runs on holds until the process ends; a larger tensor returns
+ * CP_ERR_WORKSPACE before anything is launched. The array is looked up once per device
+ * (hipGetSymbolAddress) on that device's first call. Every call on one GPU shares it,
+ * so calls that overlap on one GPU (other streams, other host threads) race: order
+ * them. Same results as cp_ef_encode, byte for byte; phase timing is off inside it. */
+int cp_ef_encode_noalloc(int ttype, const float* x, int64_t nrow, int64_t n, const float* qw,
+                         const float* U, const int32_t* order, int n_iter, uint8_t* raw,
+                         float* recon, void* stream);
+
+/* Bytes of the static workspace behind cp_ef_encode_noalloc. */
+size_t cp_ef_noalloc_max_ws_bytes(void);
+
 /* Per-thread switch for phase timing of EF calls (hipEvents recorded on the
  * call's stream; no synchronization inside the call). No counterpart in the
  * reference, which times whole tensors with time.time() (coldpress/ef.py:277, 304). */

@@ -70,6 +70,9 @@ SIGNATURES = {
     "cp_ef_encode_batch": (_i32, [_ef_p, _i32, _i32, _i32, _vp, _sz, _vp]),
     "cp_ef_encode": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _sz,
                             _vp]),
+    "cp_ef_encode_noalloc": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _vp, _i32, _vp, _vp,
+                                    _vp]),
+    "cp_ef_noalloc_max_ws_bytes": (_sz, []),
     "cp_hess_accum": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp]),
     "cp_hess_accum_batch": (_i32, [_vp, _vp, _i32, _i32, _i64, _i64, _vp]),
     "cp_ef_profile": (None, [_i32]),

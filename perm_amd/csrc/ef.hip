@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -1076,6 +1077,54 @@ int ef_phase_ms(float* out, int nphase) {
   return nphase < 5 ? nphase : 5;
 }
 
+// ---------------------------------------------------------------- allocation-free entry
+// The EF workspace of cp_ef_encode_noalloc: a static device array that every GPU the
+// library runs on holds until the process ends. Its name is a host-side stand-in,
+// never a device address: host code only uses the address hipGetSymbolAddress gives
+// for the current device, looked up once per device on that device's first call.
+// Nothing in the EF workspace has to start at zero (every buffer is written before
+// it is read), so a call may find the previous call's contents there.
+constexpr size_t kNoAllocWsBytes = (size_t)64 << 20;
+static __device__ __align__(256) char scratch[kNoAllocWsBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int scratch_ptr(void** out) {
+  int dev = -1;
+  CP_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(CP_ERR_ARG, "device %d out of range", dev);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(CP_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return CP_OK;
+}
+
+int ef_encode_noalloc(const cp_ef_tensor& t, int n_iter, hipStream_t st) {
+  const size_t need = t.nrow > 0 && t.n > 0 ? ef_ws_bytes(&t, 1) : 0;  // bad shapes: ef_encode_batch's error
+  if (need > kNoAllocWsBytes)
+    return set_error(CP_ERR_WORKSPACE,
+                     "tensor [%lld, %lld] needs %zu bytes of EF workspace; the allocation-free "
+                     "entry point holds %zu (use cp_ef_encode with a caller workspace)",
+                     (long long)t.nrow, (long long)t.n, need, kNoAllocWsBytes);
+  void* ws = nullptr;
+  if (int e = scratch_ptr(&ws)) return e;
+  // phase timing would create events on first use: off for this call
+  const bool timing = g_clock.on;
+  g_clock.on = false;
+  const int r = ef_encode_batch(&t, 1, n_iter, CP_EF_EXACT, ws, kNoAllocWsBytes, st);
+  g_clock.on = timing;
+  return r;
+}
+
 }  // namespace cp
 
 extern "C" {
@@ -1105,6 +1154,16 @@ int cp_ef_encode(int ttype, const float* x, int64_t nrow, int64_t n, const float
   cp::clear_error();
   cp_ef_tensor t{ttype, nrow, n, x, qw, U, order, raw, recon};
   return cp::ef_encode_batch(&t, 1, n_iter, CP_EF_EXACT, ws, ws_bytes, (hipStream_t)stream);
+}
+
+size_t cp_ef_noalloc_max_ws_bytes(void) { return cp::kNoAllocWsBytes; }
+
+int cp_ef_encode_noalloc(int ttype, const float* x, int64_t nrow, int64_t n, const float* qw,
+                         const float* U, const int32_t* order, int n_iter, uint8_t* raw,
+                         float* recon, void* stream) {
+  cp::clear_error();
+  cp_ef_tensor t{ttype, nrow, n, x, qw, U, order, raw, recon};
+  return cp::ef_encode_noalloc(t, n_iter, (hipStream_t)stream);
 }
 
 }  // extern "C"
