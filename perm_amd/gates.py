@@ -1,33 +1,40 @@
-"""The byte-parity gate of coldpress/gates.py:34-58 on this package's GGUF reader."""
+"""The byte-parity gate of the encode stage (coldpress/gates.py:34-58), on this
+package's GGUF reader.
+
+An encoded artifact may replace a stock quant only if a loader sees the same tensors
+with the same container types and payload sizes: the final file must list exactly the
+stock file's tensor names, each with the stock type and byte size, and its tensor bytes
+may not exceed the stock total.
+"""
 from .ggufio import read_typemap
 
 
 class GateError(AssertionError):
-    pass
+    """A hard gate failed."""
+
+
+def _violations(final, stock):
+    """Every way the final type map departs from the stock one, as readable lines."""
+    out = [f"missing from the final artifact: {n}" for n in sorted(set(stock) - set(final))]
+    out += [f"not in the stock artifact: {n}" for n in sorted(set(final) - set(stock))]
+    for name in sorted(set(stock) & set(final)):
+        for key in ("type", "n_bytes"):
+            if final[name][key] != stock[name][key]:
+                out.append(f"{name}: {key} {final[name][key]} (stock {stock[name][key]})")
+    return out
 
 
 def byte_parity(final_gguf, stock_gguf):
-    """The final artifact has the stock quant's per-tensor type map and sizes and no more
-    total tensor bytes. Raises GateError otherwise; returns a report dict."""
-    fm = read_typemap(final_gguf)
-    sm = read_typemap(stock_gguf)
-    if set(fm) != set(sm):
-        only_final = sorted(set(fm) - set(sm))
-        only_stock = sorted(set(sm) - set(fm))
-        raise GateError(f"byte-parity FAIL: tensor-set differs "
-                        f"(+final {only_final[:4]}, +stock {only_stock[:4]})")
-    mismatches = []
-    for name in sm:
-        if fm[name]["type"] != sm[name]["type"]:
-            mismatches.append((name, "type", fm[name]["type"], sm[name]["type"]))
-        if fm[name]["n_bytes"] != sm[name]["n_bytes"]:
-            mismatches.append((name, "n_bytes", fm[name]["n_bytes"], sm[name]["n_bytes"]))
-    total_final = sum(v["n_bytes"] for v in fm.values())
-    total_stock = sum(v["n_bytes"] for v in sm.values())
-    if mismatches:
-        raise GateError(f"byte-parity FAIL: {len(mismatches)} per-tensor mismatches, "
-                        f"e.g. {mismatches[:3]}")
+    """Check final_gguf against stock_gguf. Raises GateError listing what differs;
+    returns {"tensors", "total_final", "total_stock", "passed": True} otherwise."""
+    final, stock = read_typemap(final_gguf), read_typemap(stock_gguf)
+    total_final = sum(v["n_bytes"] for v in final.values())
+    total_stock = sum(v["n_bytes"] for v in stock.values())
+    problems = _violations(final, stock)
     if total_final > total_stock:
-        raise GateError(f"byte-parity FAIL: total {total_final} > stock {total_stock}")
-    return {"tensors": len(sm), "total_final": total_final, "total_stock": total_stock,
+        problems.append(f"tensor bytes {total_final} exceed the stock {total_stock}")
+    if problems:
+        shown = "; ".join(problems[:4]) + ("; ..." if len(problems) > 4 else "")
+        raise GateError(f"byte parity: {len(problems)} violation(s): {shown}")
+    return {"tensors": len(stock), "total_final": total_final, "total_stock": total_stock,
             "passed": True}

@@ -124,6 +124,29 @@ def test_reemit_replace_quant_tensor(tmp_path):
         ggufio.reemit(a, b, replace={"norm.weight": np.zeros(64, np.uint8)}, log=lambda *_: None)
 
 
+def test_reemit_keeps_any_layout_and_touches_only_the_payload(tmp_path):
+    """A file laid out unlike gguf-py's writer (the architecture key after others, 64-byte
+    alignment): re-emission keeps every byte outside the replaced tensor's range, and that
+    range holds the new container bytes."""
+    a, b = str(tmp_path / "a.gguf"), str(tmp_path / "b.gguf")
+    w = GGUFWriter(a)
+    w.add_kv("general.alignment", 64, ValueType.UINT32)
+    w.add_kv("general.name", "odd", ValueType.STRING)
+    w.add_kv("general.architecture", "llama", ValueType.STRING)
+    w.add_tensor("norm.weight", heavy_tailed(1, 48, 3)[0])
+    w.add_tensor("blk.0.ffn_down.weight", K.QUANTIZE["Q4_K"](heavy_tailed(3, 512, 4)), "Q4_K")
+    w.write()
+    new = K.QUANTIZE["Q4_K"](heavy_tailed(3, 512, 5))
+    ggufio.reemit(a, b, replace={"blk.0.ffn_down.weight": new}, log=lambda *_: None)
+    t = [t for t in GGUFReader(a).tensors if t.name == "blk.0.ffn_down.weight"][0]
+    old_bytes, new_bytes = open(a, "rb").read(), open(b, "rb").read()
+    lo, hi = t.data_offset, t.data_offset + t.n_bytes
+    assert len(old_bytes) == len(new_bytes) and t.data_offset % 64 == 0
+    assert old_bytes[:lo] == new_bytes[:lo] and old_bytes[hi:] == new_bytes[hi:]
+    assert new_bytes[lo:hi] == new.tobytes()
+    assert gates.byte_parity(b, a)["passed"]
+
+
 def test_reemit_replace_f32(tmp_path):
     a, b = str(tmp_path / "a.gguf"), str(tmp_path / "b.gguf")
     _build(a)
