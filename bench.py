@@ -660,6 +660,214 @@ def copy_main(args):
                                         "bytes_read": nbytes, "bytes_written": nbytes}}))
 
 
+CONFIG_METRIC = "EF k-quant encode Mweights/s + Hessian X^T·X TFLOP/s, 1 GPU"
+CONFIG_WORKLOADS = ("single-linear", "tied-output", "llama3-8b-layer")
+
+
+def config_cpu_baseline(spec, W, H, slot, rows_of, counts_fn):
+    """The numpy oracle (port of ef.py:46-218 + kquant.py) on one tensor of every distinct
+    (shape, container, importance) class of the spec: the factorization of its Hessian
+    (ef.py:189 runs one per tensor) plus EF at two row counts, fit as a + b * rows and
+    extrapolated to the class's tensors. A tensor of at most 1024 rows is timed whole."""
+    import numpy as np
+    from oracle import ef_oracle as E
+    try:
+        from threadpoolctl import threadpool_info
+        blas_threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:  # threadpoolctl missing or unreadable
+        blas_threads = 1
+    classes = {}
+    for name, rows, n, fam, tt, qwk in spec["tensors"]:
+        classes.setdefault((rows, n, tt, qwk, fam.split(".")[-1]), []).append((name, fam))
+    t_total, spent, fact_cache, notes = 0.0, 0.0, {}, []
+    for (rows, n, tt, qwk, fkind), members in classes.items():
+        name, fam = members[0]
+        d, i = slot[fam]
+        Hn = H[d][i].double().cpu().numpy()
+        qw = (np.diag(Hn) / (1.0 if spec["normalize"] else rows_of[fam])).astype(np.float32) \
+            if qwk == "diag" else None
+        key = (d, i)
+        if key not in fact_cache:
+            t0 = time.perf_counter()
+            order = E.act_order(Hn)
+            U = E.inv_upper_factor(Hn[np.ix_(order, order)], 0.01).astype(np.float32)
+            fact_cache[key] = (order, U, time.perf_counter() - t0)
+            spent += fact_cache[key][2]
+        order, U, t_fact = fact_cache[key]
+        Wn = W[name]
+        if rows <= 1024:
+            t0 = time.perf_counter()
+            E.ef_encode(Wn.cpu().numpy(), tt, qw, Hn, U=U, order=order)
+            t_rows = time.perf_counter() - t0
+            spent += t_rows
+            t_tensor = t_fact + t_rows
+            notes.append(f"{name} whole")
+        else:
+            r1, r2 = (8, 32) if n > 4096 else ((32, 128) if n > 1024 else (128, 512))
+            ts = {}
+            for r in (r1, r2):
+                x = Wn[:r].cpu().numpy()
+                t0 = time.perf_counter()
+                E.ef_encode(x, tt, qw, Hn, U=U, order=order)
+                ts[r] = time.perf_counter() - t0
+                spent += ts[r]
+            b = (ts[r2] - ts[r1]) / (r2 - r1)
+            t_tensor = t_fact + ts[r1] + b * (rows - r1)
+            notes.append(f"{name} at {r1}/{r2} rows")
+        t_total += t_tensor * counts_fn(members)
+        log(f"cpu {name} [{rows}x{n}] {tt}: factor {t_fact:.2f}s -> tensor {t_tensor:.1f}s "
+            f"(x{counts_fn(members)})")
+    total_weights = sum(r * n for _, r, n, *_ in spec["tensors"])
+    return {
+        "value": total_weights / t_total / 1e6, "unit": "Mweights/s", "cores": int(blas_threads),
+        "kind": "port",
+        "sample": (f"numpy oracle (port of ef.py/kquant.py), one tensor per shape/container "
+                   f"class ({'; '.join(notes)}), one factorization per tensor as the reference "
+                   f"does; {spent:.1f} s of CPU work, extrapolated linearly in rows to the "
+                   f"{len(spec['tensors'])} tensors (est. {t_total:.0f} s for the full encode); "
+                   f"sweep and codec single-threaded numpy, factorization on {blas_threads} "
+                   f"BLAS threads"),
+        "host_cpus": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+    }
+
+
+def config_main(args):
+    """One of the reference's other benchmark configurations (perm_amd.workloads.config_spec):
+    per step, every Hessian of the spec (batched by size), then act order, factorization and
+    two-iteration EF of every tensor (size classes on concurrent streams) with the final
+    decode. value = EF Mweights/s; a sequential pass after the timed steps gives the
+    factorization and sweep times the rooflines use."""
+    import ctypes
+    import torch
+    from perm_amd import _lib, hessians
+    from perm_amd import ef as gef
+    from perm_amd import workloads as wl
+    lib = _lib.load()
+    spec = wl.config_spec(args.workload)
+    fams = spec["families"]
+    log(f"{args.workload}: {len(fams)} Hessians, {len(spec['tensors'])} tensors")
+    X = {}
+    for i, (k, (d, rows, kind)) in enumerate(fams.items()):
+        X[k] = wl.family_activations(kind, rows, d, seed=1000 + i)
+    W = wl.spec_weights(spec)
+    sizes = sorted({d for d, _r, _k in fams.values()}, reverse=True)
+    keys = {d: [k for k, (dd, _r, _k) in fams.items() if dd == d] for d in sizes}
+    H = {d: torch.zeros((len(keys[d]), d, d), device="cuda") for d in sizes}
+    slot = {k: (d, i) for d in sizes for i, k in enumerate(keys[d])}
+    rows_of = {k: r for k, (_d, r, _k) in fams.items()}
+    torch.cuda.synchronize()
+    total_weights = sum(r * n for _, r, n, *_ in spec["tensors"])
+    hess_flops = sum(float(r) * d * (d + 1) for d, r, _k in fams.values())
+    ef_flops = 2 * sum(r * n * (n - 1) for _, r, n, *_ in spec["tensors"])
+    fact_flops = sum(2.0 / 3.0 * d ** 3 for d, _r, _k in fams.values())
+
+    def hessian_phase():
+        for Hb in H.values():
+            Hb.zero_()
+        hessians.xtx_accumulate_many([X[k] for k in fams], [H[slot[k][0]][slot[k][1]] for k in fams])
+        if spec["normalize"]:
+            for k in fams:
+                H[slot[k][0]][slot[k][1]].div_(float(rows_of[k]))
+
+    def builder(d):
+        def build(U, order):
+            items = []
+            for name, rows, n, fam, tt, qwk in spec["tensors"]:
+                dd, i = slot[fam]
+                if dd != d:
+                    continue
+                qw = None
+                if qwk == "diag":
+                    scale = 1.0 if spec["normalize"] else float(rows_of[fam])
+                    qw = (torch.diagonal(H[d][i]) / scale).contiguous()
+                items.append({"ttype": tt, "x": W[name], "qw": qw, "U": U[i], "order": order[i],
+                              "recon": True})
+            return items
+        return build
+
+    def ef_phase():
+        return gef.encode_size_classes([(H[d], builder(d)) for d in sizes], n_iter=2,
+                                       mode="exact", damp=0.01)
+
+    def step():
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ev[0].record()
+        hessian_phase()
+        ev[1].record()
+        ef_phase()
+        ev[2].record()
+        return ev
+
+    for i in range(args.warmup):
+        step()
+        torch.cuda.synchronize()
+        log(f"warmup {i + 1}/{args.warmup} done")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    marks = []
+    for i in range(args.steps):
+        marks.append(step())
+        log(f"step {i + 1}/{args.steps} done")
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    hess_ms = sum(a.elapsed_time(b) for a, b, _ in marks) / args.steps
+    ef_ms = sum(b.elapsed_time(c) for _, b, c in marks) / args.steps
+
+    # sequential pass: per size class, the factorization then the EF with phase timing
+    fact_ms, phases = 0.0, []
+    lib.cp_ef_profile(1)
+    for d in sizes:
+        f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        f0.record()
+        order = gef.act_order_dev(H[d])
+        U, _ = gef.factor_dev(H[d], order, 0.01, checked=True)
+        f1.record()
+        gef.ef_encode_dev(builder(d)(U, order), 2, _lib.CP_EF_EXACT, checked=True)
+        buf = (ctypes.c_float * 5)()
+        lib.cp_ef_phase_ms(ctypes.cast(buf, ctypes.c_void_p), 5)
+        torch.cuda.synchronize()
+        fact_ms += f0.elapsed_time(f1)
+        phases.append(list(buf))
+        del U, order
+    lib.cp_ef_profile(0)
+    ph = [sum(p[k] for p in phases) for k in range(5)]
+    sweep_launches = 2 * len(sizes)
+    avg_ms = ph[2] / sweep_launches
+    ach = ef_flops / sweep_launches / (avg_ms * 1e-3) / 1e12
+    ef_mw = total_weights / (ef_ms * 1e-3) / 1e6
+    containers = sorted({tt for *_, tt, _q in spec["tensors"]})
+    result = {
+        "metric": CONFIG_METRIC, "value": ef_mw, "unit": "Mweights/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": wall * 1e3 / args.steps, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random-init weights, synthetic activations; generated on device)",
+        "config": {"workload": args.workload, "tensors": len(spec["tensors"]),
+                   "weights": total_weights, "hessians": len(fams),
+                   "hessian_rows": sorted({r for _d, r, _k in fams.values()}),
+                   "hessian_sizes": sizes, "containers": containers, "n_iter": 2, "damp": 0.01,
+                   "act_order": True, "ef_mode": "exact"},
+        "roofline": {"kernel": "ef_sweep_rows_kernel", "bound": "mfma", "achieved": ach,
+                     "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_FP32_TFLOPS,
+                     "traffic": None, "avg_launch_ms": avg_ms,
+                     "launches_per_step": sweep_launches},
+        "ef": {"ms": ef_ms, "mweights_per_s": ef_mw, "flops_update": ef_flops,
+               "sequential_pass": {"factor_ms": fact_ms, "setup": ph[0], "commit": ph[1],
+                                   "sweep": ph[2], "repack": ph[3], "decode": ph[4]}},
+        "factor": {"ms": fact_ms, "flops": fact_flops,
+                   "tflops": fact_flops / (fact_ms * 1e-3) / 1e12,
+                   "frac_of_fp64_peak": fact_flops / (fact_ms * 1e-3) / 1e12 / 78.6},
+        "hessian": {"ms": hess_ms, "flops": hess_flops,
+                    "tflops": hess_flops / (hess_ms * 1e-3) / 1e12,
+                    "activations": "f32" if spec["normalize"] else "bf16"},
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline (numpy oracle on one tensor per class)")
+        result["cpu_baseline"] = config_cpu_baseline(spec, W, H, slot, rows_of, len)
+        result["gpu_over_cpu"] = ef_mw / result["cpu_baseline"]["value"]
+    print(json.dumps(result))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -670,9 +878,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ef-mode", choices=["mfma", "exact"], default="exact",
                     help="cross-block error propagation: MFMA GEMM or the reference's exact order")
-    ap.add_argument("--workload", choices=["ef", "perm-search", "formats", "gguf", "copy"],
+    ap.add_argument("--workload", choices=["ef", *CONFIG_WORKLOADS, "perm-search", "formats",
+                                           "gguf", "copy"],
                     default="ef",
-                    help="ef: the EF encode + Hessians line (default); perm-search: the PERM "
+                    help="ef: the EF encode + Hessians line (default); single-linear, "
+                         "tied-output, llama3-8b-layer: the other benchmark configurations "
+                         "(perm_amd.workloads.config_spec); perm-search: the PERM "
                          "space-map search on the GPU objective; formats: every container's "
                          "codec, the linear form and the Hessian storage format; gguf: the "
                          "encode_gguf driver end to end; copy: a plain "
@@ -690,6 +901,9 @@ def main():
     from perm_amd import workloads as wl
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a GPU")
+    if args.workload in CONFIG_WORKLOADS:
+        config_main(args)
+        return
     if args.workload == "perm-search":
         perm_main(args)
         return

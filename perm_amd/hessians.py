@@ -7,8 +7,10 @@ stays on the device and each batch is added by one MFMA kernel launch
 (cp_hess_accum), bf16 activations going straight into bf16 MFMA with float32
 accumulation -- no upcast copy, no device-to-host copy per batch.
 
-Module -> GGUF tensor naming (the reference uses gguf's TensorNameMap, a package
-not present here) is supplied by the caller as ``name_map``.
+Module -> GGUF tensor naming: the reference asks gguf's TensorNameMap (pip ``gguf``,
+absent here); ``build_name_map`` carries the map for the HF decoder layout of the dense
+llama-family architectures (llama, mistral, qwen2, qwen3), and ``collect_hessians`` also
+takes a caller's map.
 
 Storage (coldpress/hessians.py:163-243): ``save_hessians`` writes the reference's npz
 format (float16 H over a per-matrix ``hscale``, exact float32 ``diag32``, ``n``, ``name``),
@@ -30,10 +32,18 @@ _FAMILY_FALLBACK = {"attn_q": "qkv_in", "attn_k": "qkv_in", "attn_v": "qkv_in",
                     "ffn_down": "down_in"}
 
 
+def _on_device(X, H):
+    """Both operands must live on one CUDA device: their addresses go to a kernel."""
+    if not X.is_cuda or (H is not None and (not H.is_cuda or H.device != X.device)):
+        raise ValueError(f"X ({X.device}) and H ({None if H is None else H.device}) must be "
+                         f"tensors on one CUDA device")
+
+
 def xtx_accumulate(X, H=None):
     """H += X^T X on the device. X: [..., d] bf16 or float32 CUDA tensor (leading
     dims are flattened into rows, like the hook's reshape(-1, d)); H: [d, d]
     float32 CUDA tensor or None (a zero one is allocated). Returns H."""
+    _on_device(X, H)
     lib = _lib.load()
     d = X.shape[-1]
     X2 = X.reshape(-1, d)
@@ -58,6 +68,7 @@ def xtx_accumulate_many(Xs, Hs):
     lib = _lib.load()
     groups = {}
     for X, H in zip(Xs, Hs):
+        _on_device(X, H)
         d = X.shape[-1]
         X2 = X.reshape(-1, d)
         if X2.dtype not in (torch.bfloat16, torch.float32):
@@ -90,23 +101,89 @@ class HessianAccumulator:
         return self
 
 
-def collect_hessians(model, batches, name_map, gguf_ne0=None, progress_every=16, log=print):
-    """Accumulate X^T X for every nn.Linear named in ``name_map`` ({module name:
-    GGUF tensor name}) over ``batches`` (coldpress/hessians.py:85-179).
+# HF module names of the dense llama-family decoders (llama, mistral, qwen2, qwen3) and
+# the GGUF tensor each maps to -- the entries gguf's TensorNameMap gives these modules.
+NAME_MAP_ARCHES = ("llama", "mistral", "qwen2", "qwen3")
+_PREFIXES = ("model.", "model.language_model.", "language_model.model.")
+_LAYER_KINDS = {"self_attn.q_proj": "attn_q", "self_attn.k_proj": "attn_k",
+                "self_attn.v_proj": "attn_v", "self_attn.o_proj": "attn_output",
+                "mlp.gate_proj": "ffn_gate", "mlp.up_proj": "ffn_up", "mlp.down_proj": "ffn_down"}
 
-    A module whose in_features differs from gguf_ne0[gguf name] is refused before
-    any hook is registered (hessians.py:126-135). Returns
-    ({gguf name: {"H": float32 [d, d] CUDA tensor, "n": rows}}, unmapped)."""
+
+def _gguf_base(module_name, n_layers):
+    """GGUF base name (no ".weight") of an HF module name, or None."""
+    if module_name in ("lm_head", "language_model.lm_head"):
+        return "output"
+    for pre in _PREFIXES:
+        if not module_name.startswith(pre):
+            continue
+        rest = module_name[len(pre):]
+        if rest == "embed_tokens":
+            return "token_embd"
+        head, _, tail = rest.partition(".")
+        layer, _, kind = tail.partition(".")
+        if head == "layers" and layer.isdigit() and int(layer) < n_layers and kind in _LAYER_KINDS:
+            return f"blk.{int(layer)}.{_LAYER_KINDS[kind]}"
+    return None
+
+
+def build_name_map(model, arch, n_layers):
+    """{module name: GGUF base name (no ".weight")} for every nn.Linear / nn.Embedding
+    of ``model`` that maps (coldpress/hessians.py:64-82). Raises ValueError for an
+    architecture without a built-in map."""
     import torch.nn as nn
+    if arch not in NAME_MAP_ARCHES:
+        raise ValueError(f"arch {arch!r} has no built-in module -> GGUF name map "
+                         f"(have {', '.join(NAME_MAP_ARCHES)}); pass name_map")
+    out = {}
+    for name, mod in model.named_modules():
+        if isinstance(mod, (nn.Linear, nn.Embedding)):
+            base = _gguf_base(name, n_layers)
+            if base is not None:
+                out[name] = base
+    return out
+
+
+def _block_of(gguf_name):
+    """Decoder block of a GGUF tensor name, -1 for the non-block tensors."""
+    parts = gguf_name.split(".")
+    return int(parts[1]) if parts[0] == "blk" and len(parts) > 1 and parts[1].isdigit() else -1
+
+
+def collect_hessians(model, batches, gguf_ne0, arch, n_layers, layer_lo=0, layer_hi=None,
+                     progress_every=16, log=print, name_map=None, keep_on_device=False):
+    """Accumulate X^T X on the GPU for every hooked matmul of the layer shard
+    [layer_lo, layer_hi) over ``batches`` (coldpress/hessians.py:85-179).
+
+    gguf_ne0: {GGUF tensor name (with .weight): ne0} of the target artifact; a module whose
+    GGUF name is absent is unmapped, one whose in_features differs is refused with
+    ValueError before any hook is registered. Non-block tensors (output) belong to the
+    shard that starts at layer 0. ``name_map`` ({module name: GGUF base name}) replaces the
+    built-in map of ``arch``. Modules that read one input tensor (q/k/v, gate/up) share one
+    accumulator, formed once per batch. Returns ({GGUF name: {"H": float32 [d, d], "n":
+    rows}}, unmapped module names); H is a host array, as the reference returns it, or
+    with ``keep_on_device`` the CUDA tensor (tensors sharing an input share one object)."""
+    import torch.nn as nn
+    if layer_hi is None:
+        layer_hi = n_layers
+    if name_map is None:
+        name_map = build_name_map(model, arch, n_layers)
     plan, unmapped, mismatched = [], [], []
     for mname, mod in model.named_modules():
         if not isinstance(mod, nn.Linear):
-            continue
-        g = name_map.get(mname)
-        if g is None:
+            continue  # an embedding lookup has no input Hessian
+        base = name_map.get(mname)
+        if base is None:
             unmapped.append(mname)
             continue
-        if gguf_ne0 is not None and g in gguf_ne0 and mod.in_features != gguf_ne0[g]:
+        g = base + ".weight"
+        if g not in gguf_ne0:
+            unmapped.append(f"{mname} (-> {g}, absent from the GGUF)")
+            continue
+        blk = _block_of(g)
+        if not (layer_lo <= blk < layer_hi if blk >= 0 else layer_lo == 0):
+            continue
+        if mod.in_features != gguf_ne0[g]:
             mismatched.append((mname, g, mod.in_features, gguf_ne0[g]))
             continue
         plan.append((mod, g))
@@ -120,6 +197,7 @@ def collect_hessians(model, batches, name_map, gguf_ne0=None, progress_every=16,
     # the input keeps its memory from being reused by a later input of the same pass, so
     # the address identifies one tensor until the pass ends.
     seen = {}
+    dev = torch.device("cuda", torch.cuda.current_device())
 
     def make_hook(g):
         def fn(mod, inp, out):
@@ -128,13 +206,13 @@ def collect_hessians(model, batches, name_map, gguf_ne0=None, progress_every=16,
                 return
             # q/k/v (and gate/up) read one and the same input tensor: accumulate it once and
             # share the accumulator (the reference forms the identical X^T X per module)
-            key = (x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.dtype)
+            key = (x.device, x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.dtype)
             hit = seen.get(key)
             if hit is None:
                 a = acc.get(g)
                 if a is None:
-                    a = HessianAccumulator(x.shape[-1], x.device)
-                a.add(x.detach())
+                    a = HessianAccumulator(x.shape[-1], x.device if x.is_cuda else dev)
+                a.add(x.detach().to(a.H.device))  # a host activation crosses once per batch
                 seen[key] = (a, x)
             else:
                 a = hit[0]
@@ -145,17 +223,27 @@ def collect_hessians(model, batches, name_map, gguf_ne0=None, progress_every=16,
         return fn
 
     handles = [mod.register_forward_hook(make_hook(g)) for mod, g in plan]
+    log(f"hooked {len(handles)} matmuls in layers [{layer_lo},{layer_hi}); "
+        f"{len(unmapped)} module(s) unmapped/skipped")
     try:
         with torch.inference_mode():
             for c, ids in enumerate(batches):
                 seen.clear()
-                model(ids)
+                model(ids.unsqueeze(0) if ids.dim() == 1 else ids)
                 if progress_every and (c + 1) % progress_every == 0:
                     log(f"  chunk {c + 1}")
     finally:
         for h in handles:
             h.remove()
-    return {g: {"H": a.H, "n": a.n} for g, a in acc.items()}, unmapped
+    host = {}
+    out = {}
+    for g, a in acc.items():
+        if a.H.shape[0] != gguf_ne0[g]:
+            raise ValueError(f"{g}: collected H.shape[0]={a.H.shape[0]} != ne0={gguf_ne0[g]}")
+        if not keep_on_device and id(a) not in host:
+            host[id(a)] = a.H.cpu().numpy()
+        out[g] = {"H": a.H if keep_on_device else host[id(a)], "n": a.n}
+    return out, unmapped
 
 
 # ---------------------------------------------------------------- storage

@@ -120,6 +120,79 @@ def permute_hessian(H, p):
     return gather(H, p, p)
 
 
+def _moved(w, rows=None, cols=None):
+    """w[rows][:, cols] (a 1-D w: w[rows]) gathered on the GPU, returned on w's device."""
+    t = w if w.is_cuda else w.cuda()
+    if t.dim() == 1:
+        out = gather(t.reshape(1, -1), None, rows).reshape(-1)
+    else:
+        out = gather(t, rows, cols)
+    return out if w.is_cuda else out.to(w.device)
+
+
+def _hf_moves(perms, dims):
+    """{HF parameter suffix: (row index, column index)} of one decoder layer, per layer,
+    plus the model-level ones: the moves of qwen3.apply_perms (qwen3.py:141-188). Every
+    permutation is checked (IndexError / ValueError) before any of them is used."""
+    P = _check(perms["res"], dims["d_model"], "res permutation")
+    top = {"model.embed_tokens.weight": (None, P), "lm_head.weight": (None, P),
+           "model.norm.weight": (P, None)}
+    layers = []
+    for l in range(dims["n_layers"]):
+        Pf = _check(perms["ffn"][l], dims["d_ffn"], f"ffn permutation of layer {l}")
+        v_idx, o_idx = v_output_index(perms, l, dims), o_input_index(perms, l, dims)
+        layers.append({"input_layernorm.weight": (P, None),
+                       "post_attention_layernorm.weight": (P, None),
+                       "self_attn.q_proj.weight": (None, P), "self_attn.k_proj.weight": (None, P),
+                       "self_attn.v_proj.weight": (v_idx, P), "self_attn.o_proj.weight": (P, o_idx),
+                       "mlp.gate_proj.weight": (Pf, P), "mlp.up_proj.weight": (Pf, P),
+                       "mlp.down_proj.weight": (P, Pf)})
+    return top, layers
+
+
+def apply_perms(sd, perms, dims, consume=False, strip_vision=False):
+    """A new HF state dict with the permutations applied (qwen3.apply_perms,
+    coldpress/perm/spacemaps/qwen3.py:141-188): the embedding (and an untied lm_head) by
+    columns, every RMSNorm gain of the residual space, q/k/v/gate/up input columns, o/down
+    output rows, v output rows per kv head, o input columns per q head, gate/up rows and
+    down columns by the layer's FFN permutation. Every move is one GPU gather (both axes
+    in one pass); tensors come back on their own device and dtype, other entries (q_norm /
+    k_norm gains) unchanged. ``consume`` pops the moved entries from ``sd`` as they go;
+    ``strip_vision`` is accepted for the interface (a text-only architecture)."""
+    top, layers = _hf_moves(perms, dims)
+    out = dict(sd)
+
+    def move(name, rows, cols, required=True):
+        if name not in sd:
+            if required:
+                raise KeyError(name)
+            return
+        w = sd.pop(name) if consume else sd[name]
+        out[name] = _moved(w, rows, cols)
+
+    for name, (rows, cols) in top.items():
+        move(name, rows, cols, required=name != "lm_head.weight")
+    for l, moves in enumerate(layers):
+        for suffix, (rows, cols) in moves.items():
+            move(f"model.layers.{l}.{suffix}", rows, cols)
+    return out
+
+
+def apply_perms_inplace(model, perms, dims):
+    """Permute a loaded HF model's parameters in place (qwen3.apply_perms_inplace,
+    qwen3.py:191-230). A tied lm_head shares the embedding's storage and is moved once."""
+    top, layers = _hf_moves(perms, dims)
+    params = dict(model.named_parameters())  # named_parameters lists a tied weight once
+    with torch.no_grad():
+        for name, (rows, cols) in top.items():
+            if name in params:
+                params[name].data = _moved(params[name].data, rows, cols)
+        for l, moves in enumerate(layers):
+            for suffix, (rows, cols) in moves.items():
+                p = params[f"model.layers.{l}.{suffix}"]
+                p.data = _moved(p.data, rows, cols)
+
+
 def permute_layer(W, perms, layer, dims):
     """Permuted copies of one decoder layer's linear weights, keyed by GGUF kind
     (attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up, ffn_down), each

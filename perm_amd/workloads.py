@@ -121,3 +121,96 @@ def imatrix_means(weights, seed=0):
     rng = np.random.default_rng(seed)
     return {n: (np.abs(rng.standard_normal(w.shape[1])) + 0.1).astype(F32)
             for n, w in weights.items() if n not in ("token_embd.weight", "output.weight")}
+
+
+# ---------------------------------------------------------------- benchmark configs
+# The reference's benchmark configurations beyond the headline one, as tensor lists over
+# Hessian families. A family is one input space of a decoder layer: its Hessian comes
+# from ``rows`` synthetic activation rows of width d; every tensor reading that input
+# shares it. ``qw``: "diag" (imatrix-style channel means diag(H)/N) or None.
+
+LLAMA3_8B_LAYER = [
+    ("attn_q", 4096, 4096, "qkv_in"),
+    ("attn_k", 1024, 4096, "qkv_in"),
+    ("attn_v", 1024, 4096, "qkv_in"),
+    ("attn_output", 4096, 4096, "o_in"),
+    ("ffn_gate", 14336, 4096, "gateup_in"),
+    ("ffn_up", 14336, 4096, "gateup_in"),
+    ("ffn_down", 4096, 14336, "down_in"),
+]
+LLAMA3_8B_FAMILIES = {"qkv_in": 4096, "o_in": 4096, "gateup_in": 4096, "down_in": 14336}
+
+
+def config_spec(name):
+    """{"families": {key: (d, rows, activation kind)}, "tensors": [(key, rows, n, family,
+    container, qw)], "layers", "normalize"} of a named workload:
+
+    single-linear   one 1024 x 1024 Linear, Q2_K, H = X^T X / 8192 from float32 rows
+                    (single_linear: 1 % outlier channels x20), qw = diag(H)
+    tied-output     the Qwen3-0.6B 28-layer set with Q3_K attention and Q2_K MLP, plus the
+                    tied 151936 x 1024 output matrix in Q6_K with no qw, its H from 65536
+                    final-hidden-state rows N(0, 1) with log-normal channel scales
+    llama3-8b-layer one Llama-3-8B decoder layer in Q4_K: H 4096^2 for q/k/v, o and
+                    gate/up, 14336^2 for down, from 131072 rows with 0.5 % outlier
+                    channels x50
+    """
+    if name == "single-linear":
+        return {"families": {"linear_in": (1024, 8192, "single-linear")},
+                "tensors": [("linear", 1024, 1024, "linear_in", "Q2_K", "diag")],
+                "layers": 1, "normalize": True}
+    if name == "tied-output":
+        fams, tens = {}, []
+        for l in range(QWEN3_06B_LAYERS):
+            for fam, d in QWEN3_06B_FAMILIES.items():
+                fams[f"blk.{l}.{fam}"] = (d, 65536, "student-t")
+            for nm, rows, n, fam in QWEN3_06B_LAYER:
+                tens.append((f"blk.{l}.{nm}", rows, n, f"blk.{l}.{fam}",
+                             "Q3_K" if nm.startswith("attn") else "Q2_K", "diag"))
+        fams["output_in"] = (1024, 65536, "lognormal")
+        tens.append(("output", QWEN3_06B_VOCAB, 1024, "output_in", "Q6_K", None))
+        return {"families": fams, "tensors": tens, "layers": QWEN3_06B_LAYERS,
+                "normalize": False}
+    if name == "llama3-8b-layer":
+        fams = {f"blk.0.{fam}": (d, 131072, "outliers") for fam, d in LLAMA3_8B_FAMILIES.items()}
+        tens = [(f"blk.0.{nm}", rows, n, f"blk.0.{fam}", "Q4_K", "diag")
+                for nm, rows, n, fam in LLAMA3_8B_LAYER]
+        return {"families": fams, "tensors": tens, "layers": 1, "normalize": False}
+    raise KeyError(name)
+
+
+def family_activations(kind, rows, d, seed, device="cuda"):
+    """Synthetic activation rows of one Hessian family on the device:
+    student-t   Student-t (nu = 4) times log-normal(sigma 1) channel scales, bfloat16
+    lognormal   N(0, 1) times log-normal(sigma 1) channel scales, bfloat16
+    outliers    as lognormal, with 0.5 % of the channels (at least one) scaled x50
+    single-linear   single_linear's float32 rows (host draw, seed 0; 1 % outliers x20)
+    """
+    import torch
+    if kind == "student-t":
+        return student_t_activations(rows, d, nu=4.0, seed=seed, device=device)
+    if kind == "single-linear":
+        _w, X, _h = single_linear(seed=0, n=d, n_act=rows)
+        return torch.from_numpy(X).to(device)
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    scale = torch.exp(torch.randn((d,), generator=g, device=device))
+    if kind == "outliers":
+        k = max(1, int(0.005 * d))
+        scale[torch.randperm(d, generator=g, device=device)[:k]] *= 50.0
+    elif kind != "lognormal":
+        raise KeyError(kind)
+    return (torch.randn((rows, d), generator=g, device=device) * scale).to(torch.bfloat16)
+
+
+def spec_weights(spec, seed=0, device="cuda"):
+    """Random-init float32 weights N(0, 0.02^2) of every tensor of a spec, on the device
+    (single-linear: single_linear's W, with its per-row log-normal scales)."""
+    import torch
+    if any(kind == "single-linear" for _d, _r, kind in spec["families"].values()):
+        (name, rows, n, *_), = spec["tensors"]
+        W, _x, _h = single_linear(seed=0, nrow=rows, n=n)
+        return {name: torch.from_numpy(W).to(device)}
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return {name: torch.randn((rows, n), generator=g, device=device) * 0.02
+            for name, rows, n, _fam, _tt, _qw in spec["tensors"]}

@@ -62,3 +62,22 @@ def small_qwen3_model(seed=0):
         shapes[f"blk.{l}.ffn_down.weight"] = (D, FFN)
     rng = np.random.default_rng(seed)
     return {n: (rng.standard_normal(s) ** 3 * 0.1).astype(np.float16) for n, s in shapes.items()}
+
+
+def tiny_hf_decoder(kind="qwen3", n_layers=2, tie=False, seed=0):
+    """A random-init HF decoder of the llama family on the CPU, float32: hidden 64,
+    4 q heads / 2 kv heads of 16, FFN 96, vocab 128 (the reference tests' tiny_qwen3
+    shape class, built offline from a config)."""
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM, Qwen3Config, Qwen3ForCausalLM
+    kw = dict(vocab_size=128, hidden_size=64, intermediate_size=96, num_hidden_layers=n_layers,
+              num_attention_heads=4, num_key_value_heads=2, head_dim=16, tie_word_embeddings=tie)
+    torch.manual_seed(seed)
+    if kind == "qwen3":
+        model = Qwen3ForCausalLM(Qwen3Config(**kw))
+    else:
+        model = LlamaForCausalLM(LlamaConfig(**kw))
+    return model.eval()
+
+
+TINY_DIMS = {"d_model": 64, "d_ffn": 96, "n_layers": 2, "n_heads": 4, "n_kv": 2, "head_dim": 16}

@@ -25,5 +25,6 @@ def test_more_than_one_gpu_is_refused():
 def test_workloads_listed():
     r = _run("--help")
     assert r.returncode == 0
-    for w in ("ef", "perm-search", "formats", "gguf", "copy"):
+    for w in ("ef", "single-linear", "tied-output", "llama3-8b-layer", "perm-search",
+              "formats", "gguf", "copy"):
         assert w in r.stdout

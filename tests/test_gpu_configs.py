@@ -102,3 +102,39 @@ def test_llama3_8b_down_q4k(mods):
     (raw, rec), = ef.ef_encode_dev([{"ttype": "Q4_K", "x": W, "qw": qw, "U": U, "order": order}])
     assert raw.shape == (nrow, 56 * 144) and torch.isfinite(rec).all()
     _check_slice(ef, W, "Q4_K", qw, H, U, order, raw, slice(4090, 4096))
+
+
+def test_llama3_8b_layer_other_tensors_q4k(mods):
+    """The rest of the Llama-3-8B layer (config 4): q 4096 x 4096, k / v 1024 x 4096,
+    o 4096 x 4096, gate / up 14336 x 4096 under Q4_K EF in one batched call, each input
+    space's H (4096^2) from 131072 rows with 0.5 % outlier channels x50; row slices at the
+    start, middle and end of every tensor equal the oracle's encode of those rows with the
+    GPU's factor and order."""
+    ef, hs, wl = mods
+    N, n = 131072, 4096
+    _say("config: Llama-3-8B q/k/v/o/gate/up, Q4_K, H 4096^2 from 131072 rows")
+    fams = {}
+    for i, fam in enumerate(("qkv_in", "o_in", "gateup_in")):
+        fams[fam] = hs.xtx_accumulate(_activations(N, n, seed=20 + i, outlier_frac=0.005,
+                                                   gain=50.0))
+    Hb = torch.stack([fams[f] for f in ("qkv_in", "o_in", "gateup_in")])
+    order = ef.act_order_dev(Hb)
+    U, used = ef.factor_dev(Hb, order)
+    assert used == [0.01] * 3
+    slot = {"qkv_in": 0, "o_in": 1, "gateup_in": 2}
+    g = torch.Generator(device="cuda").manual_seed(4)
+    items, shapes = [], []
+    for name, rows, nn_, fam in wl.LLAMA3_8B_LAYER:
+        if fam == "down_in":
+            continue
+        W = torch.randn((rows, nn_), generator=g, device="cuda") * 0.02
+        i = slot[fam]
+        qw = (torch.diagonal(Hb[i]) / N).contiguous()
+        items.append({"ttype": "Q4_K", "x": W, "qw": qw, "U": U[i], "order": order[i]})
+        shapes.append((name, rows))
+    outs = ef.ef_encode_dev(items)
+    for (name, rows), it, (raw, rec) in zip(shapes, items, outs):
+        assert raw.shape == (rows, 16 * 144) and torch.isfinite(rec).all()
+        sel = np.r_[0:2, rows // 2:rows // 2 + 2, rows - 2:rows]
+        _say(f"  {name}: rows {sel.tolist()}")
+        _check_slice(ef, it["x"], "Q4_K", it["qw"], None, it["U"], it["order"], raw, sel)

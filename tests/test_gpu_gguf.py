@@ -123,10 +123,12 @@ def test_shared_input_hessians_are_formed_once():
 
     torch.manual_seed(0)
     m = M().cuda().eval()
-    names = {f"l{i}.{k}": f"blk.{i}.attn_{k}.weight" for i in (0, 1) for k in "qkv"}
-    names.update({f"l{i}.o": f"blk.{i}.attn_output.weight" for i in (0, 1)})
+    names = {f"l{i}.{k}": f"blk.{i}.attn_{k}" for i in (0, 1) for k in "qkv"}
+    names.update({f"l{i}.o": f"blk.{i}.attn_output" for i in (0, 1)})
+    ne0 = {g + ".weight": 64 for g in names.values()}
     batches = [torch.randn(4, 16, 64, device="cuda") for _ in range(3)]
-    got, unmapped = hs.collect_hessians(m, batches, names, log=lambda *_: None)
+    got, unmapped = hs.collect_hessians(m, batches, ne0, "qwen3", 2, name_map=names,
+                                        keep_on_device=True, log=lambda *_: None)
     assert not unmapped
     for i in (0, 1):
         assert got[f"blk.{i}.attn_q.weight"]["H"] is got[f"blk.{i}.attn_k.weight"]["H"]

@@ -59,14 +59,18 @@ def test_collect_hessians_hooks(hs):
     model = torch.nn.Sequential(torch.nn.Linear(256, 512), torch.nn.GELU(),
                                 torch.nn.Linear(512, 256)).cuda().to(torch.bfloat16)
     batches = [torch.randn((4, 64, 256), device="cuda", dtype=torch.bfloat16) for _ in range(3)]
-    res, unmapped = hs.collect_hessians(model, batches, {"0": "blk.0.ffn_up.weight",
-                                                         "2": "blk.0.ffn_down.weight"})
+    ne0 = {"blk.0.ffn_up.weight": 256, "blk.0.ffn_down.weight": 512}
+    res, unmapped = hs.collect_hessians(model, batches, ne0, "qwen3", 1,
+                                        name_map={"0": "blk.0.ffn_up", "2": "blk.0.ffn_down"},
+                                        log=lambda *_: None)
     assert unmapped == [] and set(res) == {"blk.0.ffn_up.weight", "blk.0.ffn_down.weight"}
     assert res["blk.0.ffn_up.weight"]["n"] == 3 * 4 * 64
+    assert isinstance(res["blk.0.ffn_up.weight"]["H"], np.ndarray)
     X0 = torch.cat([b.reshape(-1, 256) for b in batches]).float().cpu().numpy()
-    assert Ho.rel_fro(res["blk.0.ffn_up.weight"]["H"].cpu().numpy(), Ho.xtx(X0)) < 1e-5
+    assert Ho.rel_fro(res["blk.0.ffn_up.weight"]["H"], Ho.xtx(X0)) < 1e-5
     with pytest.raises(ValueError, match="different"):
-        hs.collect_hessians(model, batches, {"0": "x.weight"}, gguf_ne0={"x.weight": 128})
+        hs.collect_hessians(model, batches, {"x.weight": 128}, "qwen3", 1, name_map={"0": "x"},
+                            log=lambda *_: None)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -89,3 +93,47 @@ def test_batched_accumulation(hs, dtype):
     for k in list(range(7)) + [100, 235]:
         ref = base[k] + Ho.xtx(Xs[k].float().cpu().numpy())
         assert Ho.rel_fro(Hs[k].cpu().numpy(), ref) < 1e-5, k
+
+
+def test_collect_hessians_on_a_hf_decoder(hs):
+    """The drop-in collector on a tiny Qwen3 decoder (coldpress/hessians.py:85-179 with the
+    reference test's expectations, test_hessians.py:22-33): every linear keyed by its GGUF
+    name through the built-in map, H equal to X^T X of the inputs the module saw (float64
+    closed form of the same inputs, captured by plain hooks), q/k/v and gate/up sharing one
+    array, and the layer shards [0, 1) (with output) and [1, 2) splitting the set."""
+    from conftest import tiny_hf_decoder
+    model = tiny_hf_decoder("qwen3").cuda()
+    names = hs.build_name_map(model, "qwen3", 2)
+    linears = {n: m for n, m in model.named_modules() if isinstance(m, torch.nn.Linear)}
+    ne0 = {names[n] + ".weight": m.in_features for n, m in linears.items()}
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    batches = [torch.randint(0, 128, (32,), device="cuda", generator=g) for _ in range(3)]
+    seen = {n: [] for n in linears}
+    hooks = [m.register_forward_hook(
+        lambda mod, inp, out, n=n: seen[n].append(inp[0].reshape(-1, inp[0].shape[-1]).double().cpu()))
+        for n, m in linears.items()]
+    with torch.no_grad():
+        for ids in batches:
+            model(ids.unsqueeze(0))
+    for h in hooks:
+        h.remove()
+    full, unmapped = hs.collect_hessians(model, batches, ne0, "qwen3", 2, log=lambda *_: None)
+    assert unmapped == [] and set(full) == set(ne0)
+    for n in linears:
+        gname = names[n] + ".weight"
+        X = torch.cat(seen[n]).numpy()
+        assert full[gname]["n"] == X.shape[0] == 96
+        assert Ho.rel_fro(full[gname]["H"], X.T @ X) < 1e-5, gname
+    for l in (0, 1):
+        assert full[f"blk.{l}.attn_q.weight"]["H"] is full[f"blk.{l}.attn_v.weight"]["H"]
+        assert full[f"blk.{l}.ffn_gate.weight"]["H"] is full[f"blk.{l}.ffn_up.weight"]["H"]
+    lo, _ = hs.collect_hessians(model, batches, ne0, "qwen3", 2, layer_lo=0, layer_hi=1,
+                                log=lambda *_: None)
+    hi, _ = hs.collect_hessians(model, batches, ne0, "qwen3", 2, layer_lo=1, layer_hi=2,
+                                log=lambda *_: None)
+    assert set(lo) == {k for k in ne0 if not k.startswith("blk.1.")}
+    assert set(hi) == {k for k in ne0 if k.startswith("blk.1.")}
+    for k in ne0:
+        part = lo if k in lo else hi
+        assert Ho.rel_fro(part[k]["H"], full[k]["H"]) < 1e-6
