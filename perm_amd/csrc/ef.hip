@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -373,6 +374,156 @@ __device__ __forceinline__ int sweep_item(const SweepTask* tasks, int count, int
   return item - tasks[lo].first;
 }
 
+// Per-wave LDS of the row-stripe sweep, about 14.6 KB: one buffer for the RS x 64
+// target transpose and then the compact diagonal U tile, the storage sub-block offsets
+// of the block's columns, and the grid steps / offsets of a quarter block.
+struct StripeLds {
+  float tile[TILE_FLOATS];
+  int sbo[64];
+  float sg[kGridCols][32], sm[kGridCols][32];
+};
+
+// LDS ordering between the lanes of one wave (each wave has its own StripeLds).
+struct WaveSync {
+  __device__ __forceinline__ void operator()() const {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+  }
+};
+
+template <int RS>
+using StripeVec = float __attribute__((ext_vector_type(StripeLayout<RS>::NV)));
+
+// One k = 1 outer product e (x) u on the matrix cores with the inline-zero accumulator:
+// every product rounded once to float32, as np.outer forms it.
+template <int RS>
+__device__ __forceinline__ StripeVec<RS> stripe_product(float a, float b) {
+  const StripeVec<RS> z = {};
+  if constexpr (RS == 32)
+    return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, z, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, z, 0, 0, 0);
+}
+
+// The block's original targets (visiting order) in the MFMA layout, and the storage
+// sub-block offsets of its columns: lane l stages row rl, columns part * CPP .. + CPP - 1.
+template <int RS>
+__device__ __forceinline__ StripeVec<RS> stage_block(const SweepTask& tk, int i1, int rr, int l,
+                                                     StripeLds& s) {
+  constexpr int B = 64, NV = StripeLayout<RS>::NV, CPP = B * RS / 64;
+  const int rl = l % RS, part = l / RS, nrow = tk.nrow;
+  float (*st)[B + 1] = reinterpret_cast<float (*)[B + 1]>(s.tile);
+  s.sbo[l] = tk.sbidx[i1 + l] * nrow;
+#pragma unroll
+  for (int k = 0; k < CPP; ++k)
+    st[rl][part * CPP + k] = ld_lane(tk.WpT, (int64_t)(i1 + part * CPP + k) * nrow + rr);
+  WaveSync()();
+  StripeVec<RS> t;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) t[v] = st[StripeLayout<RS>::row(v, l)][StripeLayout<RS>::col(v, l)];
+  return t;
+}
+
+// Cross-block updates of the block at i1 from visiting columns j0 .. j1 - 1 (multiples of
+// 64), in ascending column order: t = fl(t - fl(e_jj * U[jj][c])). E and U of eight columns
+// per group, two groups in flight (static buffers a / b, no copies); per column, the MFMA
+// for the next column is issued before the subtractions that consume the current one,
+// fenced by scheduling barriers so the two products stay in separate registers and each
+// MFMA runs under the VALU work of the column before it.
+template <int RS>
+__device__ __forceinline__ void cross_range(const SweepTask& tk, int i1, int rr, int l,
+                                            StripeVec<RS>& t, int j0, int j1) {
+  constexpr int G = 8, NV = StripeLayout<RS>::NV;
+  const int nrow = tk.nrow, n = tk.n;
+  float ea[G], ua[G], eb[G], ub[G];
+  const float* const Eg = tk.E + (int64_t)j0 * nrow + rr;     // column j0 + k at + k * nrow
+  const float* const Ug = tk.U + (int64_t)j0 * n + i1 + l;    // row j0 + k at + k * n
+  auto load = [&](int g, float (&e)[G], float (&u)[G]) {
+    const float* ep = Eg + (int64_t)g * G * nrow;
+    const float* up = Ug + (int64_t)g * G * n;
+#pragma unroll
+    for (int q = 0; q < G; ++q) {
+      e[q] = ld_lane(ep, (int64_t)q * nrow);
+      u[q] = ld_lane(up, (int64_t)q * n);
+    }
+  };
+  StripeVec<RS> P0, P1;
+  auto group = [&](const float (&e)[G], const float (&u)[G], const float (&en)[G],
+                   const float (&un)[G]) {
+#pragma unroll
+    for (int q = 0; q < G; q += 2) {
+      // P0 holds column q of the group on entry; the last group's final product is unused
+      P1 = stripe_product<RS>(e[q + 1], u[q + 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int v = 0; v < NV; ++v) t[v] = t[v] - P0[v];
+      __builtin_amdgcn_sched_barrier(0);
+      P0 = stripe_product<RS>(q + 2 < G ? e[q + 2] : en[0], q + 2 < G ? u[q + 2] : un[0]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int v = 0; v < NV; ++v) t[v] = t[v] - P1[v];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  const int groups = (j1 - j0) / G;  // even: j1 - j0 is a multiple of 64
+  load(0, ea, ua);
+  P0 = stripe_product<RS>(ea[0], ua[0]);
+  for (int g = 0; g < groups; g += 2) {
+    load(g + 1, eb, ub);
+    group(ea, ua, eb, ub);
+    load(g + 2 < groups ? g + 2 : g + 1, ea, ua);  // past the end: a valid group, unused
+    group(eb, ub, ea, ua);
+  }
+}
+
+// The block's own 64 columns for the stripe's rows, after every earlier column's
+// updates: the targets move to the row-split layout (lane l: elements RS * (l / RS)
+// .. + RS - 1 of row l % RS), the compact diagonal tile and the block's committed grid
+// come in through one round trip, and the four quarter blocks are swept in order.
+template <int RS>
+__device__ __forceinline__ void sweep_block_rows(const SweepTask& tk, int i1, int rr, int l,
+                                                 const StripeVec<RS>& t, StripeLds& s) {
+  constexpr int B = 64, NV = StripeLayout<RS>::NV;
+  static_assert(RS * (B + 1) <= TILE_FLOATS, "target transpose fits the tile buffer");
+  const int rl = l % RS, part = l / RS, n = tk.n;
+  float (*st)[B + 1] = reinterpret_cast<float (*)[B + 1]>(s.tile);
+  float (*sg)[RS] = reinterpret_cast<float (*)[RS]>(&s.sg[0][0]);
+  float (*sm)[RS] = reinterpret_cast<float (*)[RS]>(&s.sm[0][0]);
+  WaveSync()();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) st[StripeLayout<RS>::row(v, l)][StripeLayout<RS>::col(v, l)] = t[v];
+  WaveSync()();
+  float tl[RS];
+#pragma unroll
+  for (int k = 0; k < RS; ++k) tl[k] = st[rl][part * RS + k];
+  WaveSync()();
+  // the block's grid steps / offsets (both halves into registers) and the compact
+  // diagonal tile share one round trip to memory; lane l fills column 16 p + l of the
+  // tile rows of piece p
+  GridPart<RS> gp[64 / kGridCols];
+#pragma unroll
+  for (int q = 0; q < 64 / kGridCols; ++q) load_grid<RS>(tk, s.sbo, q * kGridCols, l, rr, gp[q]);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    float u[16];
+    const bool in = l < 64 - 16 * p;
+#pragma unroll
+    for (int a = 0; a < 16; ++a)
+      u[a] = in ? ld_lane(tk.U, (int64_t)(i1 + 16 * p + a) * n + i1 + 16 * p + l) : 0.0f;
+    if (in) {
+#pragma unroll
+      for (int a = 0; a < 16; ++a) s.tile[tile_base(p) + a * (64 - 16 * p) + l] = u[a];
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 64 / kGridCols; ++q) {
+    store_grid<RS>(gp[q], l, sg, sm);
+    WaveSync()();
+    sweep_part_split<RS>(tk, i1, rr, rl, part, tl, s.tile, sg, sm, q * kGridCols);
+    WaveSync()();
+  }
+}
+
 template <int RS>
 __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* __restrict__ tasks, int count,
                                                             int total, int xcd_runs) {
@@ -504,6 +655,54 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
       sweep_part_split<RS>(tk, i1, rr, rl, part, tl, lds, sg, sm, q * kGridCols);
       __syncthreads();
     }
+  }
+}
+
+// W waves per stripe, for calls whose stripes alone would leave most SIMDs idle (few
+// rows, long rows). Wave w owns blocks w, w + W, w + 2W, ...; the blocks are taken in
+// rounds of W. In a round every wave first applies the updates of all columns of
+// earlier rounds to its block (the bulk of the work, in parallel); then the round's
+// blocks are swept in order: wave p sweeps its block while the later waves wait at
+// the barrier, and after it they apply its 64 columns. Every element still receives its
+// updates one at a time in ascending column order, as in the one-wave kernel. The
+// errors a wave writes reach the others through global memory, ordered by the
+// workgroup barrier.
+template <int RS, int W>
+__global__ __launch_bounds__(64 * W, 2) void ef_sweep_pipe_kernel(const SweepTask* __restrict__ tasks,
+                                                                  int count, int total, int xcd_runs) {
+  int ti;
+  const int stripe = sweep_item(tasks, count, total, xcd_runs != 0, &ti);
+  if (stripe < 0) return;  // uniform over the workgroup
+  const SweepTask tk = tasks[ti];
+  const int row0 = stripe * RS;
+  if (row0 >= tk.nrow) return;
+  const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x / 64);
+  const int l = threadIdx.x % 64, rl = l % RS;
+  const int rr = row0 + rl < tk.nrow ? row0 + rl : tk.nrow - 1;
+  if constexpr (RS == 16) asm volatile("" ::: "v175");
+  __shared__ __align__(16) StripeLds s_all[W];
+  StripeLds& s = s_all[wv];
+  const int nblocks = tk.n / 64;
+  for (int r0 = 0; r0 < nblocks; r0 += W) {
+    const int b = r0 + wv;
+    const bool active = b < nblocks;
+    const int i1 = b * 64;
+    StripeVec<RS> t = {};
+    if (active) {
+      t = stage_block<RS>(tk, i1, rr, l, s);
+      if (r0 > 0) cross_range<RS>(tk, i1, rr, l, t, 0, r0 * 64);
+    }
+    // the round's W barriers: barrier p follows wave p's sweep of its block; wave wv
+    // takes the blocks of waves 0 .. wv - 1 after their barriers, then sweeps its own
+    // block, then passes the remaining barriers (the same W barriers for every wave)
+#pragma unroll 1
+    for (int p = 0; p < wv; ++p) {
+      __syncthreads();
+      if (active) cross_range<RS>(tk, i1, rr, l, t, (r0 + p) * 64, (r0 + p) * 64 + 64);
+    }
+    if (active) sweep_block_rows<RS>(tk, i1, rr, l, t, s);
+#pragma unroll 1
+    for (int p = wv; p < W; ++p) __syncthreads();
   }
 }
 
@@ -1007,6 +1206,19 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     same_n = same_n && tk.n == tasks[by_len[0]].n;
   }
   if (total_stripes > ((int64_t)1 << 30)) return set_error(CP_ERR_SHAPE, "too many row stripes");
+  // waves per 16-row stripe: double while the stripes would still fill at most the
+  // GPU's 2048 two-per-SIMD wave slots and every tensor has a block per wave
+  int waves = 1;
+  if (mode == CP_EF_EXACT && RS == 16) {
+    int min_blocks = 1 << 30;
+    for (int i = 0; i < count; ++i) min_blocks = std::min(min_blocks, (int)(ts[i].n / 64));
+    while (waves < 8 && total_stripes * 2 * waves <= 2048 && 2 * waves <= min_blocks) waves *= 2;
+    if (const char* e = getenv("CP_EF_SWEEP_WAVES")) {  // tuning override: 1, 2, 4 or 8
+      const int w = atoi(e);
+      if (w == 1 || w == 2 || w == 4 || w == 8) waves = std::min(w, std::max(1, min_blocks));
+      while (waves > 1 && waves > min_blocks) waves /= 2;
+    }
+  }
   for (int c0 = 0; c0 < count; c0 += kTasksPerLaunch) {
     const int cn = count - c0 < kTasksPerLaunch ? count - c0 : kTasksPerLaunch;
     SweepBatch b;
@@ -1044,9 +1256,18 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     else if (mode == CP_EF_EXACT && RS == 32)
       ef_sweep_rows_kernel<32><<<(unsigned)(8 * ((total_stripes + 7) / 8)), 64, 0, st>>>(
           dtasks, count, (int)total_stripes, same_n ? 1 : 0);
-    else if (mode == CP_EF_EXACT)
+    else if (mode == CP_EF_EXACT && waves == 1)
       ef_sweep_rows_kernel<16><<<(unsigned)(8 * ((total_stripes + 7) / 8)), 64, 0, st>>>(
           dtasks, count, (int)total_stripes, same_n ? 1 : 0);
+    else if (mode == CP_EF_EXACT) {
+      const unsigned g = (unsigned)(8 * ((total_stripes + 7) / 8));
+      const int xr = same_n ? 1 : 0, ns = (int)total_stripes;
+      switch (waves) {
+        case 2: ef_sweep_pipe_kernel<16, 2><<<g, 128, 0, st>>>(dtasks, count, ns, xr); break;
+        case 4: ef_sweep_pipe_kernel<16, 4><<<g, 256, 0, st>>>(dtasks, count, ns, xr); break;
+        default: ef_sweep_pipe_kernel<16, 8><<<g, 512, 0, st>>>(dtasks, count, ns, xr); break;
+      }
+    }
     else
       ef_sweep_mfma_kernel<BLK><<<dim3((unsigned)((max_rows + 63) / 64), (unsigned)count), 64, 0, st>>>(dtasks);
     CP_LAUNCHED("EF sweep");

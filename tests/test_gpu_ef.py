@@ -239,6 +239,24 @@ def test_sweep_bit_exact_iterations(ef, n_iter):
     assert np.array_equal(raw, want_raw)
 
 
+@pytest.mark.parametrize("waves", ["1", "2", "4", "8"])
+def test_sweep_waves_per_stripe_bit_exact(ef, waves, monkeypatch):
+    """Calls with few 16-row stripes spread each stripe over 2, 4 or 8 waves (blocks taken
+    in rounds, the round's blocks swept in order); every wave count gives the oracle's
+    bytes, including tensors with fewer blocks than waves and a partial last round."""
+    monkeypatch.setenv("CP_EF_SWEEP_WAVES", waves)
+    specs = [(40, 1024, "Q2_K", 61), (17, 768, "Q4_K", 62), (33, 256, "Q6_K", 63)]
+    for W, tt, qw, H, order, U in _oracle_items(specs):
+        _say(f"waves {waves}: {tt} {W.shape}")
+        want_raw, want_rec = E.ef_encode(W, tt, qw, H, n_iter=2, U=U, order=order)
+        item = {"ttype": tt, "x": torch.from_numpy(W).cuda(), "qw": torch.from_numpy(qw).cuda(),
+                "U": torch.from_numpy(U).cuda(),
+                "order": torch.from_numpy(order.astype(np.int32)).cuda()}
+        (raw, rec), = ef.ef_encode_dev([item], 2)
+        assert np.array_equal(raw.cpu().numpy(), want_raw)
+        assert np.array_equal(rec.cpu().numpy(), want_rec)
+
+
 def _codes(tt, raw, nrow, n):
     return K.stored_codes(tt, raw).reshape(nrow, n)
 
