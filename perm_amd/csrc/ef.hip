@@ -436,15 +436,19 @@ __device__ __forceinline__ void cross_range(const SweepTask& tk, int i1, int rr,
   constexpr int G = 8, NV = StripeLayout<RS>::NV;
   const int nrow = tk.nrow, n = tk.n;
   float ea[G], ua[G], eb[G], ub[G];
-  const float* const Eg = tk.E + (int64_t)j0 * nrow + rr;     // column j0 + k at + k * nrow
-  const float* const Ug = tk.U + (int64_t)j0 * n + i1 + l;    // row j0 + k at + k * n
+  // buffer loads rebased per group: the lane's byte offset stays in a VGPR and the
+  // column's offset is scalar, so no per-lane address arithmetic runs per column
+  const int eoff = 4 * rr, uoff = 4 * l;
   auto load = [&](int g, float (&e)[G], float (&u)[G]) {
-    const float* ep = Eg + (int64_t)g * G * nrow;
-    const float* up = Ug + (int64_t)g * G * n;
+    const int jg = j0 + g * G;
+    const auto re = __builtin_amdgcn_make_buffer_rsrc((void*)(tk.E + (int64_t)jg * nrow), 0,
+                                                      0x7fffffff, 0x00020000);
+    const auto ru = __builtin_amdgcn_make_buffer_rsrc((void*)(tk.U + (int64_t)jg * n + i1), 0,
+                                                      0x7fffffff, 0x00020000);
 #pragma unroll
     for (int q = 0; q < G; ++q) {
-      e[q] = ld_lane(ep, (int64_t)q * nrow);
-      u[q] = ld_lane(up, (int64_t)q * n);
+      e[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(re, eoff, 4 * q * nrow, 0));
+      u[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ru, uoff, 4 * q * n, 0));
     }
   };
   StripeVec<RS> P0, P1;
@@ -545,9 +549,9 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
   // concurrent stream's workgroups (the factorization's GEMM and diagonal-block
   // kernels need 34-37 KB), instead of the 10 KB a half-block staging left.
   // At most two waves per SIMD: more on some SIMDs leaves others idle while the
-  // busy ones set the kernel's time. The 32-row variant's registers (over 170)
-  // already allow no more; the 16-row variant reserves a register to get there.
-  if constexpr (RS == 16) asm volatile("" ::: "v175");
+  // busy ones set the kernel's time. Both variants reserve a register (v175) so the
+  // allocation stays above a third of the register file.
+  asm volatile("" ::: "v175");
   static_assert(RS * (B + 1) <= TILE_FLOATS, "target transpose fits the tile buffer");
   __shared__ __align__(16) float lds[TILE_FLOATS];
   __shared__ int sbo[B];
@@ -581,15 +585,18 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
       // by scheduling barriers so the two products stay in separate registers
       // and each MFMA runs under the VALU work of the column before it
       float ea[G], ua[G], eb[G], ub[G];
-      const float* const Eg = tk.E + rr;     // column jj at + jj * nrow
-      const float* const Ug = tk.U + i1 + l; // column jj at + jj * n
+      // buffer loads rebased per group: the lane's byte offset stays in a VGPR and the
+      // column's offset is scalar, so no per-lane address arithmetic runs per column
+      const int eoff = 4 * rr, uoff = 4 * l;
       auto load = [&](int g, float (&e)[G], float (&u)[G]) {
-        const float* ep = Eg + (int64_t)g * G * nrow;
-        const float* up = Ug + (int64_t)g * G * n;
+        const auto re = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(tk.E + (int64_t)g * G * nrow), 0, 0x7fffffff, 0x00020000);
+        const auto ru = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(tk.U + (int64_t)g * G * n + i1), 0, 0x7fffffff, 0x00020000);
 #pragma unroll
         for (int q = 0; q < G; ++q) {
-          e[q] = ld_lane(ep, (int64_t)q * nrow);
-          u[q] = ld_lane(up, (int64_t)q * n);
+          e[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(re, eoff, 4 * q * nrow, 0));
+          u[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ru, uoff, 4 * q * n, 0));
         }
       };
       fv P0, P1;
