@@ -47,14 +47,17 @@ constexpr int NW = 256;  // outer block-column width of the left-looking sweep
 // op(B) = B [K,N] or, with BT, B^T for B stored [N,K]. Batched over blockIdx.z
 // as z = z1 * nz2 + z2 with separate strides per level.
 //
-// Block tile BM x BN (BM = 64 or 128, BN = 64), K tile 16; the 4 waves are stacked
-// along M, each BM/4 x BN built from v_mfma_f64_16x16x4f64. The next K tile is
-// fetched into registers while the current one is multiplied, then stored into
-// the other half of a double-buffered LDS, so one barrier separates K tiles.
-// Within a K tile, lane group g = lane/16 supplies k = 4g + s to MFMA step s
-// (the MFMA sums over g, and any fixed assignment of the 16 k values to (g, s)
-// gives the same sum of products), which lets a lane fetch the four A values of
-// a fragment with two 16-byte LDS reads.
+// Block tile BM x BN (BM = 64 or 128, BN = 64 or 128), K tile 16, 4 waves each
+// building a 64-column slab from v_mfma_f64_16x16x4f64: stacked along M for
+// BN = 64 (BM/4 x 64 each), a 2 x 2 grid for BN = 128 (64 x 64 each, half the LDS
+// fragment reads per MFMA of the stacked form). The next K tile is fetched into
+// registers while the current one is multiplied, then stored into the other half
+// of a double-buffered LDS, so one barrier separates K tiles. The operands of one
+// MFMA step s are read from LDS just before its MFMAs, which keeps the 128 x 128
+// tile at two waves per SIMD (its 64 accumulator doubles per lane take half the
+// register file). Within a K tile, lane group g = lane/16 supplies k = 4g + s to
+// MFMA step s (the MFMA sums over g, and any fixed assignment of the 16 k values
+// to (g, s) gives the same sum of products).
 //
 // tri: bit 0 -- A is lower triangular (A[r][k] = 0 for k > r), so row tile bm
 // only needs k < bm + BM; bit 1 -- B ([K,N], not transposed) is lower
@@ -113,13 +116,17 @@ __device__ inline double2 ld_pair(const double* p, bool ok, int c, int lim) {
 }
 
 template <bool BT, int BM, int BN, bool VEC>
-__global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
-  constexpr int TI = BM / 64;  // 16-row MFMA tiles per wave
-  constexpr int TJ = BN / 16;  // 16-column MFMA tiles per wave
+__global__ __launch_bounds__(256, 2) void dgemm_kernel(GemmArgs g) {
+  // waves: stacked along M for BN = 64 (each BM/4 x 64), a 2 x 2 grid for BN = 128
+  // (each BM/2 x 64); fragments of one MFMA step s are read from LDS at a time
+  constexpr int WN = BN / 64;
+  constexpr int WM = 4 / WN;
+  constexpr int TI = BM / WM / 16;  // 16-row MFMA tiles per wave
+  constexpr int TJ = 4;             // 16-column MFMA tiles per wave (64 columns)
   constexpr int AQ = BM / 32;  // A-tile pairs fetched per thread
   constexpr int BQ = BN / 32;  // B-tile pairs fetched per thread
   constexpr int BROWS = BT ? BN : GBK;
-  constexpr int BLD = BT ? GLD : BN + 4;  // [K][BN] rows: lane groups 4 rows apart in opposite bank halves
+  constexpr int BLD = BT ? GLD : BN + 4;
   __shared__ __align__(16) double As[2][BM][GLD];
   __shared__ __align__(16) double Bs[2][BROWS][BLD];
   int bx, by, bz;
@@ -130,10 +137,9 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
   double* C = g.C + z1 * g.sC1 + z2 * g.sC2;
   const int bm = by * BM, bn = bx * BN;
   if ((g.tri & 4) && bn >= bm + BM) return;
-  const int t = threadIdx.x, l = t & 63, wm = (t >> 6) * (BM / 4);
+  const int t = threadIdx.x, l = t & 63, w = t >> 6;
+  const int wm = (w % WM) * (BM / WM), wn = (w / WM) * 64;
   const int lr = l & 15, lg = l >> 4;
-  // loader coordinates: [rows][K] tiles as (row t/8 + 32q, k pair t%8),
-  // [K][BN] tiles as (k t/(BN/2) + (512/BN)q, column pair t%(BN/2))
   const int tr = t >> 3, tk = (t & 7) * 2;
   const int nr = t / (BN / 2), nc = (t % (BN / 2)) * 2;
 
@@ -185,37 +191,20 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
   for (int it = 0; it < nt; ++it) {
     const int b = it & 1;
     if (it + 1 < nt) fetch(kbeg + (it + 1) * GBK);
-    double af[TI][4], bf[TJ][4];
 #pragma unroll
-    for (int ti = 0; ti < TI; ++ti) {
-      const double2* p = reinterpret_cast<const double2*>(&As[b][wm + 16 * ti + lr][4 * lg]);
-      const double2 u = p[0], v = p[1];
-      af[ti][0] = u.x;
-      af[ti][1] = u.y;
-      af[ti][2] = v.x;
-      af[ti][3] = v.y;
-    }
+    for (int s = 0; s < 4; ++s) {
+      double af[TI], bf[TJ];
 #pragma unroll
-    for (int tj = 0; tj < TJ; ++tj) {
-      if (BT) {
-        const double2* p = reinterpret_cast<const double2*>(&Bs[b][16 * tj + lr][4 * lg]);
-        const double2 u = p[0], v = p[1];
-        bf[tj][0] = u.x;
-        bf[tj][1] = u.y;
-        bf[tj][2] = v.x;
-        bf[tj][3] = v.y;
-      } else {
+      for (int ti = 0; ti < TI; ++ti) af[ti] = As[b][wm + 16 * ti + lr][4 * lg + s];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) bf[tj][s] = Bs[b][4 * lg + s][16 * tj + lr];
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
+      for (int tj = 0; tj < TJ; ++tj)
+        bf[tj] = BT ? Bs[b][wn + 16 * tj + lr][4 * lg + s] : Bs[b][4 * lg + s][wn + 16 * tj + lr];
 #pragma unroll
       for (int ti = 0; ti < TI; ++ti)
 #pragma unroll
         for (int tj = 0; tj < TJ; ++tj)
-          acc[ti][tj] = __builtin_amdgcn_mfma_f64_16x16x4f64(af[ti][s], bf[tj][s], acc[ti][tj], 0, 0, 0);
+          acc[ti][tj] = __builtin_amdgcn_mfma_f64_16x16x4f64(af[ti], bf[tj], acc[ti][tj], 0, 0, 0);
+    }
     if (it + 1 < nt) stash(b ^ 1);
     __syncthreads();
   }
@@ -227,7 +216,7 @@ __global__ __launch_bounds__(256) void dgemm_kernel(GemmArgs g) {
       for (int r = 0; r < 4; ++r) {
         // v_mfma_f64_16x16x4f64 result: register r of lane l holds row 4r + l/16, column l%16
         const int i = bm + wm + 16 * ti + 4 * r + lg;
-        const int j = bn + 16 * tj + lr;
+        const int j = bn + wn + 16 * tj + lr;
         if (i < g.M && j < g.N) {
           double* p = C + (int64_t)i * g.ldc + j;
           const double v = g.alpha * acc[ti][tj][r];
@@ -253,12 +242,12 @@ static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
   if (a0.M <= 0 || a0.N <= 0 || nz1 <= 0) return CP_OK;
   const bool vec = pairs_aligned(a0.A, a0.lda, a0.sA1, a0.sA2) &&
                    pairs_aligned(a0.B, a0.ldb, a0.sB1, a0.sB2);
-  // 128-row tiles when they still give two blocks per CU, 64-row ones otherwise. (A
-  // 128 x 128 tile needs ~400 VGPRs, one wave per SIMD, and measured slower: nothing
-  // hides its barrier and staging gaps.)
+  // 128 x 128 tiles when both dimensions reach 128 and the grid still has 512 blocks
+  // (two per CU); else 128-row tiles when they keep two blocks per CU; else 64 x 64.
   const int64_t z = (int64_t)nz1 * a0.nz2;
-  const int bn = 64;
-  const int bm = (a0.M + 127) / 128 * ((a0.N + 63) / 64) * z >= 512 ? 128 : 64;
+  const bool wide = a0.M >= 128 && a0.N >= 128 && (int64_t)((a0.M + 127) / 128) * ((a0.N + 127) / 128) * z >= 512;
+  const int bn = wide ? 128 : 64;
+  const int bm = wide || (a0.M + 127) / 128 * ((a0.N + 63) / 64) * z >= 512 ? 128 : 64;
   GemmArgs a = a0;
   a.ntx = (a.N + bn - 1) / bn;
   a.nty = (a.M + bm - 1) / bm;
@@ -267,9 +256,11 @@ static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
   if (total > (int64_t)1 << 30) return set_error(CP_ERR_SHAPE, "fp64 GEMM grid too large");
   const dim3 grid((unsigned)(8 * ((total + 7) / 8)));
   if (bt)
-    bm == 128 ? launch_gemm<true, 128, 64>(a, grid, vec, st) : launch_gemm<true, 64, 64>(a, grid, vec, st);
+    bn == 128 ? launch_gemm<true, 128, 128>(a, grid, vec, st)
+              : bm == 128 ? launch_gemm<true, 128, 64>(a, grid, vec, st) : launch_gemm<true, 64, 64>(a, grid, vec, st);
   else
-    bm == 128 ? launch_gemm<false, 128, 64>(a, grid, vec, st) : launch_gemm<false, 64, 64>(a, grid, vec, st);
+    bn == 128 ? launch_gemm<false, 128, 128>(a, grid, vec, st)
+              : bm == 128 ? launch_gemm<false, 128, 64>(a, grid, vec, st) : launch_gemm<false, 64, 64>(a, grid, vec, st);
   CP_LAUNCHED("fp64 GEMM launch");
   return CP_OK;
 }
