@@ -32,15 +32,79 @@ METRIC = "EF k-quant encode Mweights/s (Q2_K) + Hessian X^T·X TFLOP/s, 1 GPU"
 ROWS = 65536
 PEAK_BF16_TFLOPS = 2516.6
 PEAK_FP32_TFLOPS = 157.3
-# HBM bytes per ef_sweep_rows_kernel launch of the 28-layer exact-mode workload (mean of
-# the sequential pass's six launches), from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs,
-# each scaled by what the counter reads for a plain 1 GiB copy (`--workload copy`):
-# FETCH_SIZE x 2.0, WRITE_SIZE x 1.0. Source: profiles/ef_sweep_rows_qwen3-0.6b_q2k_pmc.md.
-SWEEP_TRAFFIC_BYTES = 10.594e9
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _pmc_child(counter, regex, argv, outdir, timeout=600):
+    """One rocprofv3 --pmc run of ``bench.py <argv>`` as a child process: [(kernel, value)]
+    of ``counter`` per dispatch of the kernels matching ``regex``, in dispatch order."""
+    import csv
+    import shutil
+    import subprocess
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        raise RuntimeError("rocprofv3 not on PATH")
+    cmd = [prof, "--pmc", counter, "--kernel-include-regex", regex, "--output-format", "csv",
+           "-d", outdir, "-o", "p", "--", sys.executable, "-u", os.path.abspath(__file__), *argv]
+    env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
+    proc = subprocess.run(cmd, cwd=ROOT, env=env, stdout=subprocess.DEVNULL,
+                          stderr=subprocess.PIPE, timeout=timeout, text=True)
+    path = os.path.join(outdir, "p_counter_collection.csv")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{counter} run exited {proc.returncode} without counters: "
+                           f"{proc.stderr.strip().splitlines()[-1:] }")
+    rows = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] == counter:
+                key = int(r["Dispatch_Id"])
+                name, val = rows.get(key, (r["Kernel_Name"], 0.0))
+                rows[key] = (name, val + float(r["Counter_Value"]))
+    # rocprofv3 may end with a signal after the program finished and the file is complete;
+    # the caller checks the dispatch count it expects
+    return [rows[k] for k in sorted(rows)]
+
+
+def measure_sweep_traffic(layers):
+    """HBM bytes per launch of the exact EF sweep (ef_sweep_rows_kernel): the mean over the
+    sequential pass's launches (two per size class) of FETCH_SIZE and WRITE_SIZE, each read
+    in its own rocprofv3 --pmc child run of ``--workload sweep-pass`` and scaled by what the
+    same counter reads for the 1 GiB copy of ``--workload copy`` (reads and writes exactly
+    2^30 bytes). Runs before this process touches the GPU. Returns (bytes, detail)."""
+    import tempfile
+    tmp = tempfile.mkdtemp(prefix="bench_pmc_", dir=os.environ.get("TMPDIR", "/tmp"))
+    t0 = time.perf_counter()
+    kib = float(1 << 30) / 1024.0
+    got = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        copy = _pmc_child(counter, "MulFunctor", ["--workload", "copy", "--steps", "1",
+                                                  "--warmup", "0"],
+                          os.path.join(tmp, f"copy_{counter}"))
+        if len(copy) != 1 or copy[0][1] <= 0:
+            raise RuntimeError(f"copy calibration: {len(copy)} dispatches of the copy kernel")
+        sweep = _pmc_child(counter, "ef_sweep_rows", ["--workload", "sweep-pass", "--layers",
+                                                      str(layers)],
+                           os.path.join(tmp, f"sweep_{counter}"))
+        if len(sweep) != 6:
+            raise RuntimeError(f"sweep pass: {len(sweep)} sweep dispatches, expected 6")
+        scale = kib / copy[0][1]
+        got[counter] = {"copy_kib": copy[0][1], "scale": scale,
+                        "per_launch_bytes": [v * 1024.0 * scale for _n, v in sweep]}
+        log(f"traffic: {counter} measured ({time.perf_counter() - t0:.0f} s so far)")
+    fetch = got["FETCH_SIZE"]["per_launch_bytes"]
+    write = got["WRITE_SIZE"]["per_launch_bytes"]
+    total = (sum(fetch) + sum(write)) / len(fetch)
+    detail = {"source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, one child run each of "
+                        "`bench.py --workload sweep-pass` (the sequential pass's six sweep "
+                        "launches) and of `--workload copy` (1 GiB read + 1 GiB written) for "
+                        "the counter scale, run by this bench before its own timed steps",
+              "fetch_bytes_per_launch": fetch, "write_bytes_per_launch": write,
+              "fetch_scale": got["FETCH_SIZE"]["scale"], "write_scale": got["WRITE_SIZE"]["scale"],
+              "seconds": time.perf_counter() - t0}
+    return total, detail
 
 
 def build_workload(layers, device):
@@ -635,6 +699,22 @@ def gguf_main(args):
         shutil.rmtree(tmp, ignore_errors=True)
 
 
+def sweep_pass_main(args):
+    """The ef workload's sequential exact-mode EF pass alone (one size class at a time, two
+    sweep launches each), after its Hessians: the run whose sweep launches the HBM byte
+    counters are read on. Prints nothing on stdout."""
+    import torch
+    from perm_amd import _lib
+    X, W, H, slot = build_workload(args.layers, "cuda")
+    hessian_phase(X, H, slot)
+    del X
+    torch.cuda.synchronize()
+    for d in sorted(H, reverse=True):
+        ef_phase(W, {d: H[d]}, slot, args.layers, _lib.CP_EF_EXACT, concurrent=False)
+        torch.cuda.synchronize()
+        log(f"sweep pass: class {d} done")
+
+
 def copy_main(args):
     """A plain elementwise device copy of 1 GiB (read 1 GiB, write 1 GiB) per step: the
     known-size kernel against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters are
@@ -878,8 +958,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ef-mode", choices=["mfma", "exact"], default="exact",
                     help="cross-block error propagation: MFMA GEMM or the reference's exact order")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 child runs that measure the sweep's HBM bytes "
+                         "(roofline.traffic is then null)")
     ap.add_argument("--workload", choices=["ef", *CONFIG_WORKLOADS, "perm-search", "formats",
-                                           "gguf", "copy"],
+                                           "gguf", "copy", "sweep-pass"],
                     default="ef",
                     help="ef: the EF encode + Hessians line (default); single-linear, "
                          "tied-output, llama3-8b-layer: the other benchmark configurations "
@@ -887,7 +970,9 @@ def main():
                          "space-map search on the GPU objective; formats: every container's "
                          "codec, the linear form and the Hessian storage format; gguf: the "
                          "encode_gguf driver end to end; copy: a plain "
-                         "1 GiB device copy, the calibration run for the HBM byte counters")
+                         "1 GiB device copy, the calibration run for the HBM byte counters; "
+                         "sweep-pass: the ef workload's sequential EF pass alone, the run "
+                         "the sweep's HBM byte counters are read on")
     args = ap.parse_args()
     if args.gpus != 1:
         msg = (f"bench.py runs on one GPU only (got --gpus {args.gpus}); the encoder path "
@@ -896,11 +981,25 @@ def main():
         print(json.dumps({"metric": METRIC, "error": msg}))
         sys.exit(2)
 
+    # the sweep's HBM bytes, from child rocprofv3 runs started before this process
+    # initializes the GPU
+    traffic, traffic_detail = None, None
+    if (args.workload == "ef" and args.ef_mode == "exact" and not args.no_traffic):
+        log("traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE child runs (sweep pass, copy)")
+        try:
+            traffic, traffic_detail = measure_sweep_traffic(args.layers)
+        except Exception as e:  # reported in the line, never fatal for the bench
+            traffic_detail = {"error": f"{type(e).__name__}: {e}"}
+            log(f"traffic: not measured ({traffic_detail['error']})")
+
     import torch
     from perm_amd import _lib
     from perm_amd import workloads as wl
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a GPU")
+    if args.workload == "sweep-pass":
+        sweep_pass_main(args)
+        return
     if args.workload in CONFIG_WORKLOADS:
         config_main(args)
         return
@@ -996,12 +1095,13 @@ def main():
         avg_ms = ph[2] / sweep_launches
         flops_per_launch = ef_flops / sweep_launches
         ach = flops_per_launch / (avg_ms * 1e-3) / 1e12
-        exact_full = mode == _lib.CP_EF_EXACT and layers == 28
         roof = {"kernel": ("ef_sweep_mfma_kernel" if mode == _lib.CP_EF_MFMA
                            else "ef_sweep_rows_kernel"), "bound": "mfma", "achieved": ach,
                 "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_FP32_TFLOPS,
-                "traffic": SWEEP_TRAFFIC_BYTES if exact_full else None,
-                "avg_launch_ms": avg_ms, "launches_per_step": sweep_launches}
+                "traffic": traffic, "avg_launch_ms": avg_ms,
+                "launches_per_step": sweep_launches}
+        if traffic_detail is not None:
+            roof["traffic_detail"] = traffic_detail
 
     result = {
         "metric": METRIC,

@@ -324,10 +324,11 @@ def optimize(weights, ttypes, qws, dims, rows_sample=16384, log=print):
     base = res_vals[0]
     res_perm, res_val, res_name = np.arange(dims["d_model"]), base, "identity"
     for (kname, perm), val in zip(res_cands[1:], res_vals[1:]):
-        log(f"  res sort[{kname}]: {val:.6g} ({(val / base - 1) * 100:+.2f}%)")
         if val < res_val:
             res_perm, res_val, res_name = perm, val, kname
-    log(f"  res -> {res_name} ({(res_val / base - 1) * 100:+.2f}%)")
+    log("residual space: " + ", ".join(
+        f"{k} {v / base - 1:+.2%}" for (k, _p), v in zip(res_cands[1:], res_vals[1:]))
+        + f" against the identity order; kept {res_name}")
 
     fb_all, fv_all = errs[0:L], errs[L:2 * L]
     ob_all, ov_all = errs[2 * L:3 * L], errs[3 * L:4 * L]

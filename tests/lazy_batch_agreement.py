@@ -1,0 +1,91 @@
+"""Study, not a test (pytest does not collect it): would a right-looking lazy-batch EF,
+whose cross-block update is one float32 GEMM per block (the form an MFMA kernel takes),
+keep the reference's codes? Run from the repository root:
+
+    python tests/lazy_batch_agreement.py
+
+The emulation keeps the in-block updates exact (coldpress/ef.py:198-214: one float32
+subtraction of a float32 product per element, in the visiting order) and replaces the
+cross-block part by W[:, b1:] -= E_blk @ U[blk, b1:] in float32 (BLAS accumulation order),
+which is what an MFMA accumulation computes up to its own summation order. It prints the
+fraction of stored codes equal to the exact oracle's and the relative change of
+tr(dW H dW^T), on the single-Linear workload (1024 columns, 256 rows), for Q2_K and Q4_K,
+with and without an importance vector, at block sizes 32 and 128.
+"""
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+from oracle import ef_oracle as E, kquant_oracle as K  # noqa: E402
+from perm_amd.workloads import single_linear  # noqa: E402
+
+F32 = np.float32
+
+
+def sweep_lazy(xp, U, dl, ml, lo, hi, sub, order, B):
+    """The sweep of coldpress/ef.py:193-214 over permuted rows xp (modified in place), with
+    updates beyond the current block of B columns deferred to one float32 GEMM per block."""
+    nrow, n = xp.shape
+    L = np.zeros((nrow, n), np.int32)
+    diag = np.diag(U).copy()
+    for b0 in range(0, n, B):
+        b1 = min(n, b0 + B)
+        Eb = np.zeros((nrow, b1 - b0), F32)
+        for jj in range(b0, b1):
+            j = order[jj]
+            dlj = dl[:, j // sub]
+            mlj = ml[:, j // sub] if ml is not None else F32(0)
+            nz = dlj != 0
+            with np.errstate(divide="ignore", invalid="ignore"):
+                q = K.rint_magic((xp[:, jj] + mlj) / np.where(nz, dlj, F32(1)))
+            q = np.where(nz, np.clip(q, lo, hi), 0)
+            L[:, j] = q
+            r = xp[:, jj] - (dlj * q.astype(F32) - mlj)
+            e = np.where(nz, r / diag[jj], F32(0)).astype(F32)
+            Eb[:, jj - b0] = e
+            if jj + 1 < b1:
+                xp[:, jj + 1:b1] -= np.outer(e, U[jj, jj + 1:b1])
+        if b1 < n:
+            xp[:, b1:] -= (Eb @ U[b0:b1, b1:]).astype(F32)
+    return L
+
+
+def ef_lazy(x, tt, qw, U, order, B, n_iter=2):
+    """coldpress/ef.py:179-218's outer loop around sweep_lazy."""
+    nrow, n = x.shape
+    w_cur = x.astype(F32).copy()
+    raw = None
+    for _ in range(n_iter):
+        raw = K.QUANTIZE[tt](w_cur, qw)
+        dl, ml, lo, hi, sub = E.committed_grid(tt, raw, nrow, n)
+        xp = x.astype(F32)[:, order].copy()
+        L = sweep_lazy(xp, U, dl, ml, lo, hi, sub, order, B)
+        raw = E.write_codes(tt, raw, L, nrow, n)
+        w_cur = np.empty_like(xp)
+        w_cur[:, order] = xp
+    return raw, K.DEQUANTIZE[tt](raw, n)
+
+
+def main():
+    W, _X, H = single_linear(seed=0, nrow=256, n=1024)
+    order = E.act_order(H, stable=True)
+    U = E.inv_upper_factor(H[np.ix_(order, order)]).astype(F32)
+    for tt in ("Q2_K", "Q4_K"):
+        for qname, qw in (("imatrix", np.diag(H).astype(F32)), ("none", None)):
+            raw0, rec0 = E.ef_encode(W, tt, qw, H, U=U, order=order)
+            c0 = K.stored_codes(tt, raw0)
+            e0 = E.h_weighted_err(W, rec0, H)
+            for B in (32, 128):
+                raw1, rec1 = ef_lazy(W, tt, qw, U, order, B)
+                agree = (K.stored_codes(tt, raw1) == c0).mean()
+                e1 = E.h_weighted_err(W, rec1, H)
+                print(f"{tt} qw={qname} block {B}: codes agree {agree * 100:.3f}%  "
+                      f"tr err rel diff {abs(e1 - e0) / e0:.2e}", flush=True)
+
+
+if __name__ == "__main__":
+    main()

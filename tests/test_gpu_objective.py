@@ -174,13 +174,19 @@ def test_col_sums_and_log_rms(ob, dtype):
     assert ulp.max() <= 2
 
 
-@pytest.mark.parametrize("case", ["q2k-unweighted", "mixed-imatrix"])
+@pytest.mark.parametrize("case", ["q2k-unweighted", "mixed-imatrix", "q2k-scaled-channels"])
 def test_optimize_matches_oracle(case):
-    """The reference optimizer test's model (test_perm_optimize.py:14-61): the GPU
-    search picks the oracle's permutations with bit-identical objective values."""
+    """The reference optimizer test's model (test_perm_optimize.py:14-61), and the same
+    shapes with channel scales under which every space's sorted candidate matters (one
+    layer's value-channel candidate loses): the GPU search picks the oracle's
+    permutations with bit-identical objective values."""
     from perm_amd import perm as gp
     w = small_qwen3_model()
-    if case == "q2k-unweighted":
+    if case == "q2k-scaled-channels":
+        from test_oracle_objective import _scaled_qwen3_model
+        w, _s = _scaled_qwen3_model()
+        ttypes, qws = {n: "Q2_K" for n in w}, {}
+    elif case == "q2k-unweighted":
         ttypes, qws = {n: "Q2_K" for n in w}, {}
     else:
         kinds = ["Q4_K", "Q3_K", "Q6_K", "Q5_K", "Q2_K", "Q8_0"]
