@@ -68,6 +68,16 @@ def _pmc_child(counter, regex, argv, outdir, timeout=600):
     return [rows[k] for k in sorted(rows)]
 
 
+def last_sweep_kernel(lib):
+    """The kernel of the calling thread's last EF sweep launch, as the library reports it."""
+    import ctypes
+    rs, wv = (ctypes.c_int * 1)(), (ctypes.c_int * 1)()
+    lib.cp_ef_last_sweep(ctypes.cast(rs, ctypes.c_void_p), ctypes.cast(wv, ctypes.c_void_p))
+    if wv[0] > 1:
+        return f"ef_sweep_pipe_kernel<{rs[0]}, {wv[0]}>"
+    return f"ef_sweep_rows_kernel<{rs[0]}>"
+
+
 def measure_sweep_traffic(layers):
     """HBM bytes per launch of the exact EF sweep (ef_sweep_rows_kernel): the mean over the
     sequential pass's launches (two per size class) of FETCH_SIZE and WRITE_SIZE, each read
@@ -894,7 +904,7 @@ def config_main(args):
     ef_ms = sum(b.elapsed_time(c) for _, b, c in marks) / args.steps
 
     # sequential pass: per size class, the factorization then the EF with phase timing
-    fact_ms, phases = 0.0, []
+    fact_ms, phases, kernels = 0.0, [], {}
     lib.cp_ef_profile(1)
     for d in sizes:
         f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -903,6 +913,7 @@ def config_main(args):
         U, _ = gef.factor_dev(H[d], order, 0.01, checked=True)
         f1.record()
         gef.ef_encode_dev(builder(d)(U, order), 2, _lib.CP_EF_EXACT, checked=True)
+        kernels[d] = last_sweep_kernel(lib)
         buf = (ctypes.c_float * 5)()
         lib.cp_ef_phase_ms(ctypes.cast(buf, ctypes.c_void_p), 5)
         torch.cuda.synchronize()
@@ -927,10 +938,11 @@ def config_main(args):
                    "hessian_rows": sorted({r for _d, r, _k in fams.values()}),
                    "hessian_sizes": sizes, "containers": containers, "n_iter": 2, "damp": 0.01,
                    "act_order": True, "ef_mode": "exact"},
-        "roofline": {"kernel": "ef_sweep_rows_kernel", "bound": "mfma", "achieved": ach,
-                     "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_FP32_TFLOPS,
-                     "traffic": None, "avg_launch_ms": avg_ms,
-                     "launches_per_step": sweep_launches},
+        "roofline": {"kernel": " / ".join(sorted(set(kernels.values()))), "bound": "mfma",
+                     "achieved": ach, "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                     "frac": ach / PEAK_FP32_TFLOPS, "traffic": None, "avg_launch_ms": avg_ms,
+                     "launches_per_step": sweep_launches,
+                     "sweep_kernel_by_size": {str(d): k for d, k in kernels.items()}},
         "ef": {"ms": ef_ms, "mweights_per_s": ef_mw, "flops_update": ef_flops,
                "sequential_pass": {"factor_ms": fact_ms, "setup": ph[0], "commit": ph[1],
                                    "sweep": ph[2], "repack": ph[3], "decode": ph[4]}},
@@ -1055,9 +1067,10 @@ def main():
     p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     lib.cp_ef_profile(1)
     p0.record()
-    phases = []
+    phases, kernels = [], {}
     for d in sorted(H, reverse=True):
         ef_phase(W, {d: H[d]}, slot, layers, mode, concurrent=False)
+        kernels[d] = last_sweep_kernel(lib)
         buf = (ctypes.c_float * 5)()
         lib.cp_ef_phase_ms(ctypes.cast(buf, ctypes.c_void_p), 5)
         phases.append(list(buf))
@@ -1100,6 +1113,8 @@ def main():
                 "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_FP32_TFLOPS,
                 "traffic": traffic, "avg_launch_ms": avg_ms,
                 "launches_per_step": sweep_launches}
+        if mode == _lib.CP_EF_EXACT:
+            roof["sweep_kernel_by_size"] = {str(d): k for d, k in kernels.items()}
         if traffic_detail is not None:
             roof["traffic_detail"] = traffic_detail
 

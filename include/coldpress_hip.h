@@ -173,6 +173,12 @@ void cp_ef_profile(int enable);
  * Waits for the call's last event. Returns the number of phases written. */
 int cp_ef_phase_ms(float* out, int nphase);
 
+/* Shape of the calling thread's last EF sweep launch: rows per stripe (16 or 32) and
+ * waves per stripe (1: ef_sweep_rows_kernel; 2, 4 or 8: ef_sweep_pipe_kernel). Returns
+ * that call's mode, or -1 when the thread has run no EF call. A profiling aid with no
+ * counterpart in the reference, like cp_ef_profile. */
+int cp_ef_last_sweep(int* rows_per_stripe, int* waves);
+
 /* ---- Hessian accumulation (coldpress/hessians.py:137-154) ---- */
 
 /* H [d, d] float32 += X^T X for X [N, d] row-major (x_dtype 0 = float32,

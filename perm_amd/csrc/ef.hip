@@ -1104,6 +1104,10 @@ static void grid_range(int ttype, int* lo, int* hi, int* sub) {
 static thread_local PhaseClock g_clock;
 #define CP_PHASE(p) CP_PHASE_MARK(g_clock, p)
 
+// The calling thread's last sweep launch (cp_ef_last_sweep): rows per stripe, waves per
+// stripe, mode (-1: none yet).
+static thread_local int g_sweep_shape[3] = {0, 0, -1};
+
 // A run of table rows sharing (type, importance) for the templated codec launches.
 struct EfGroup {
   int first, count, ttype;
@@ -1222,8 +1226,10 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     while (waves < 8 && total_stripes * 2 * waves <= 2048 && 2 * waves <= min_blocks) waves *= 2;
     if (const char* e = getenv("CP_EF_SWEEP_WAVES")) {  // tuning override: 1, 2, 4 or 8
       const int w = atoi(e);
-      if (w == 1 || w == 2 || w == 4 || w == 8) waves = std::min(w, std::max(1, min_blocks));
-      while (waves > 1 && waves > min_blocks) waves /= 2;
+      if (w == 1 || w == 2 || w == 4 || w == 8) {
+        waves = w;  // the largest of 1, 2, 4, 8 within the request and every tensor's blocks
+        while (waves > 1 && waves > min_blocks) waves /= 2;
+      }
     }
   }
   for (int c0 = 0; c0 < count; c0 += kTasksPerLaunch) {
@@ -1258,6 +1264,9 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     ef_grid_kernel<<<dim3((unsigned)((grid_threads + 255) / 256), (unsigned)count), 256, 0, st>>>(dtab);
     CP_LAUNCHED("EF commit");
     CP_PHASE(1);
+    g_sweep_shape[0] = RS;
+    g_sweep_shape[1] = mode == CP_EF_EXACT ? waves : 1;
+    g_sweep_shape[2] = mode;
     if (mode == CP_EF_EXACT_VALU)
       ef_sweep_exact_kernel<BLK><<<dim3((unsigned)((max_rows + 255) / 256), (unsigned)count), 256, 0, st>>>(dtasks);
     else if (mode == CP_EF_EXACT && RS == 32)
@@ -1363,6 +1372,14 @@ int cp_ef_phase_ms(float* out, int nphase) {
   cp::clear_error();
   if (!out || nphase <= 0) return cp::set_error(CP_ERR_ARG, "bad phase buffer");
   return cp::ef_phase_ms(out, nphase);
+}
+
+int cp_ef_last_sweep(int* rows_per_stripe, int* waves) {
+  cp::clear_error();
+  if (!rows_per_stripe || !waves) return cp::set_error(CP_ERR_ARG, "null output");
+  *rows_per_stripe = cp::g_sweep_shape[0];
+  *waves = cp::g_sweep_shape[1];
+  return cp::g_sweep_shape[2];
 }
 
 size_t cp_ef_ws_bytes(const cp_ef_tensor* tensors, int count) {

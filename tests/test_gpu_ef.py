@@ -1,6 +1,8 @@
 """GPU EF path parity: act order, the fp64 inverse-Hessian factor, and the EF
 sweep (bit-exact against the oracle when both use the same factor; within the
 code-agreement and H-weighted-error gates when the GPU computes its own)."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -8,6 +10,7 @@ import torch
 from conftest import correlated_hessian, heavy_tailed
 from oracle import ef_oracle as E
 from oracle import kquant_oracle as K
+from perm_amd import _lib
 
 pytestmark = pytest.mark.gpu
 F32 = np.float32
@@ -255,6 +258,15 @@ def test_sweep_waves_per_stripe_bit_exact(ef, waves, monkeypatch):
         (raw, rec), = ef.ef_encode_dev([item], 2)
         assert np.array_equal(raw.cpu().numpy(), want_raw)
         assert np.array_equal(rec.cpu().numpy(), want_rec)
+        # the launch the library reports: 16-row stripes, the requested waves capped at the
+        # tensor's 64-column blocks (a power of two)
+        rs, wv = (ctypes.c_int * 1)(), (ctypes.c_int * 1)()
+        mode = _lib.load().cp_ef_last_sweep(ctypes.cast(rs, ctypes.c_void_p),
+                                            ctypes.cast(wv, ctypes.c_void_p))
+        want_w = int(waves)
+        while want_w > W.shape[1] // 64:
+            want_w //= 2
+        assert (mode, rs[0], wv[0]) == (_lib.CP_EF_EXACT, 16, want_w)
 
 
 def _codes(tt, raw, nrow, n):
