@@ -103,6 +103,14 @@ int cp_chol_inv_upper_async(const void* H, int h_dtype, int64_t n, int batch,
                             const int32_t* order, double damp, void* U, int u_dtype,
                             int32_t* flags, void* ws, size_t ws_bytes, void* stream);
 
+/* Per-thread GEMM tile policy of the factorizations this thread queues: 0 (the default)
+ * picks the fastest tiles for a GPU the factorization has to itself; 1 keeps every fp64
+ * GEMM at 64 x 64 tiles, which fit on a CU beside the EF sweep's workgroups, for a
+ * factorization queued to run concurrently with EF work (perm_amd.ef.encode_size_classes).
+ * Results are the same either way up to the GEMMs' summation order. No counterpart in
+ * the reference, which factorizes with LAPACK. */
+void cp_chol_compact_tiles(int on);
+
 /* ---- EF encode (coldpress/ef.py:179-218) ---- */
 
 enum cp_ef_mode {

@@ -78,6 +78,7 @@ SIGNATURES = {
     "cp_ef_profile": (None, [_i32]),
     "cp_ef_phase_ms": (_i32, [_vp, _i32]),
     "cp_ef_last_sweep": (_i32, [_vp, _vp]),
+    "cp_chol_compact_tiles": (None, [_i32]),
     "cp_permute_gather": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "cp_lin_extract": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp]),
     "cp_lin_reconstruct": (_i32, [_i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),

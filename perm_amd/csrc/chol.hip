@@ -238,6 +238,12 @@ static bool pairs_aligned(const double* p, int ld, int64_t s1, int64_t s2) {
   return aligned(p, 16) && !(ld & 1) && !(s1 & 1) && !(s2 & 1);
 }
 
+// The calling thread's GEMM tile policy (cp_chol_compact_tiles): 0 picks the fastest tile
+// for a GPU the factorization has to itself; 1 keeps every GEMM at 64 x 64, whose blocks
+// (106 VGPRs, 36 KB of LDS) fit on a CU beside two EF sweep waves per SIMD, where the
+// larger tiles (158-252 VGPRs, 55-72 KB) wait for whole CUs to drain.
+static thread_local int g_compact_tiles = 0;
+
 static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
   if (a0.M <= 0 || a0.N <= 0 || nz1 <= 0) return CP_OK;
   const bool vec = pairs_aligned(a0.A, a0.lda, a0.sA1, a0.sA2) &&
@@ -245,9 +251,10 @@ static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
   // 128 x 128 tiles when both dimensions reach 128 and the grid still has 512 blocks
   // (two per CU); else 128-row tiles when they keep two blocks per CU; else 64 x 64.
   const int64_t z = (int64_t)nz1 * a0.nz2;
-  const bool wide = a0.M >= 128 && a0.N >= 128 && (int64_t)((a0.M + 127) / 128) * ((a0.N + 127) / 128) * z >= 512;
+  const bool wide = !g_compact_tiles && a0.M >= 128 && a0.N >= 128 &&
+                    (int64_t)((a0.M + 127) / 128) * ((a0.N + 127) / 128) * z >= 512;
   const int bn = wide ? 128 : 64;
-  const int bm = wide || (a0.M + 127) / 128 * ((a0.N + 63) / 64) * z >= 512 ? 128 : 64;
+  const int bm = !g_compact_tiles && (wide || (a0.M + 127) / 128 * ((a0.N + 63) / 64) * z >= 512) ? 128 : 64;
   GemmArgs a = a0;
   a.ntx = (a.N + bn - 1) / bn;
   a.nty = (a.M + bm - 1) / bm;
@@ -869,6 +876,8 @@ static int fact_run(const T* H, int64_t sH, int n, int batch, const int* order, 
 extern "C" {
 
 size_t cp_chol_ws_bytes(int64_t n, int batch) { return cp::fact_ws_bytes(n, batch); }
+
+void cp_chol_compact_tiles(int on) { cp::g_compact_tiles = on != 0; }
 
 int cp_act_order(const void* H, int h_dtype, int64_t n, int batch, int32_t* order, void* stream) {
   cp::clear_error();

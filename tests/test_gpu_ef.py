@@ -433,6 +433,26 @@ def test_factor_async_equals_blocking(ef):
     assert torch.equal(Ua, Ub)
 
 
+@pytest.mark.parametrize("n,batch", [(3072, 4), (1000, 3)])
+def test_factor_compact_tiles_give_the_same_factor(ef, n, batch):
+    """cp_chol_compact_tiles(1) (every fp64 GEMM on 64 x 64 tiles, as the concurrent
+    size-class driver queues them) gives bit-identical U: each output element sums its K
+    range in the same order whatever the tile."""
+    lib = _lib.load()
+    _say(f"compact tiles n={n} batch={batch}")
+    Hb = torch.from_numpy(np.stack([correlated_hessian(n, 2 * n, seed=40 + s)
+                                    for s in range(batch)])).cuda()
+    order = ef.act_order_dev(Hb)
+    Ua, _ = ef.factor_dev(Hb, order, 0.01)
+    lib.cp_chol_compact_tiles(1)
+    try:
+        Ub, flags = ef.factor_dev_async(Hb, order, 0.01)
+    finally:
+        lib.cp_chol_compact_tiles(0)
+    assert flags.cpu().tolist() == [0] * batch
+    assert torch.equal(Ua, Ub)
+
+
 def test_factor_async_flags_a_failed_matrix(ef):
     n = 256
     eig = np.linspace(1.0, 100.0, n)
