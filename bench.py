@@ -38,11 +38,14 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def _pmc_child(counter, regex, argv, outdir, timeout=600):
+def _pmc_child(counter, regex, argv, outdir, timeout=180):
     """One rocprofv3 --pmc run of ``bench.py <argv>`` as a child process: [(kernel, value)]
-    of ``counter`` per dispatch of the kernels matching ``regex``, in dispatch order."""
+    of ``counter`` per dispatch of the kernels matching ``regex``, in dispatch order. The
+    child runs in its own session; past ``timeout`` seconds the whole group (the profiler
+    and the profiled program) is killed and the run counts as failed."""
     import csv
     import shutil
+    import signal
     import subprocess
     prof = shutil.which("rocprofv3")
     if prof is None:
@@ -50,12 +53,18 @@ def _pmc_child(counter, regex, argv, outdir, timeout=600):
     cmd = [prof, "--pmc", counter, "--kernel-include-regex", regex, "--output-format", "csv",
            "-d", outdir, "-o", "p", "--", sys.executable, "-u", os.path.abspath(__file__), *argv]
     env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
-    proc = subprocess.run(cmd, cwd=ROOT, env=env, stdout=subprocess.DEVNULL,
-                          stderr=subprocess.PIPE, timeout=timeout, text=True)
+    proc = subprocess.Popen(cmd, cwd=ROOT, env=env, stdout=subprocess.DEVNULL,
+                            stderr=subprocess.PIPE, text=True, start_new_session=True)
+    try:
+        _out, err = proc.communicate(timeout=timeout)
+    except subprocess.TimeoutExpired:
+        os.killpg(proc.pid, signal.SIGKILL)
+        proc.communicate()
+        raise RuntimeError(f"{counter} run of {argv[1]} exceeded {timeout} s")
     path = os.path.join(outdir, "p_counter_collection.csv")
     if not os.path.exists(path):
         raise RuntimeError(f"{counter} run exited {proc.returncode} without counters: "
-                           f"{proc.stderr.strip().splitlines()[-1:] }")
+                           f"{err.strip().splitlines()[-1:]}")
     rows = {}
     with open(path) as f:
         for r in csv.DictReader(f):
