@@ -74,7 +74,9 @@ struct GemmArgs {
   int64_t sA1, sB1, sC1, sA2, sB2, sC2;
   int nz2;
   int tri;
-  int ntx, nty, nzt;  // column tiles, row tiles, batch entries (set by dgemm())
+  int ntx, nty, nzt;  // block grid: column tiles, row tiles, batch entries (set by dgemm())
+  int fold;           // 1: grid row by also takes row tile rt - 1 - by; 2: the same for columns
+  int rt, ct;         // row and column tiles of the product (set by dgemm())
 };
 
 // Block -> tile: items run matrix by matrix, then by groups of 8 row tiles,
@@ -135,94 +137,105 @@ __global__ __launch_bounds__(256, 2) void dgemm_kernel(GemmArgs g) {
   const double* A = g.A + z1 * g.sA1 + z2 * g.sA2;
   const double* B = g.B + z1 * g.sB1 + z2 * g.sB2;
   double* C = g.C + z1 * g.sC1 + z2 * g.sC2;
-  const int bm = by * BM, bn = bx * BN;
-  if ((g.tri & 4) && bn >= bm + BM) return;
   const int t = threadIdx.x, l = t & 63, w = t >> 6;
   const int wm = (w % WM) * (BM / WM), wn = (w / WM) * 64;
   const int lr = l & 15, lg = l >> 4;
   const int tr = t >> 3, tk = (t & 7) * 2;
   const int nr = t / (BN / 2), nc = (t % (BN / 2)) * 2;
+  // A triangular operand makes a tile's K range grow with its row (tri & 1) or shrink
+  // with its column (tri & 2). The block then takes a tile and its mirror, whose ranges
+  // add up to the same length for every block, so no long tile is left running alone
+  // at the end of the grid.
+  const int mir = g.fold == 1 ? g.rt - 1 - by : (g.fold == 2 ? g.ct - 1 - bx : -1);
+  const int np = mir >= 0 && mir != (g.fold == 1 ? by : bx) ? 2 : 1;
+#pragma unroll 1
+  for (int p = 0; p < np; ++p) {
+    const int bm = (p && g.fold == 1 ? mir : by) * BM;
+    const int bn = (p && g.fold == 2 ? mir : bx) * BN;
+    if ((g.tri & 4) && bn >= bm + BM) continue;
 
-  dbl4 acc[TI][TJ];
+    dbl4 acc[TI][TJ];
 #pragma unroll
-  for (int i = 0; i < TI; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) acc[i][j] = dbl4{0.0, 0.0, 0.0, 0.0};
+      for (int j = 0; j < TJ; ++j) acc[i][j] = dbl4{0.0, 0.0, 0.0, 0.0};
 
-  const int kbeg = (g.tri & 2) ? (bn & ~(GBK - 1)) : 0;
-  const int kend = (g.tri & 1) ? min(g.K, bm + BM) : g.K;
-  const int nt = kend > kbeg ? (kend - kbeg + GBK - 1) / GBK : 0;
+    const int kbeg = (g.tri & 2) ? (bn & ~(GBK - 1)) : 0;
+    const int kend = (g.tri & 1) ? min(g.K, bm + BM) : g.K;
+    const int nt = kend > kbeg ? (kend - kbeg + GBK - 1) / GBK : 0;
 
-  double2 ra[AQ], rb[BQ];
-  auto fetch = [&](int k0) {
+    double2 ra[AQ], rb[BQ];
+    auto fetch = [&](int k0) {
 #pragma unroll
-    for (int q = 0; q < AQ; ++q) {
-      const int r = bm + tr + 32 * q;
-      ra[q] = ld_pair<VEC>(A + (int64_t)r * g.lda + k0 + tk, r < g.M, k0 + tk, g.K);
-    }
-#pragma unroll
-    for (int q = 0; q < BQ; ++q) {
-      if (BT) {
-        const int r = bn + tr + 32 * q;
-        rb[q] = ld_pair<VEC>(B + (int64_t)r * g.ldb + k0 + tk, r < g.N, k0 + tk, g.K);
-      } else {
-        const int k = k0 + nr + (512 / BN) * q;
-        rb[q] = ld_pair<VEC>(B + (int64_t)k * g.ldb + bn + nc, k < g.K, bn + nc, g.N);
+      for (int q = 0; q < AQ; ++q) {
+        const int r = bm + tr + 32 * q;
+        ra[q] = ld_pair<VEC>(A + (int64_t)r * g.lda + k0 + tk, r < g.M, k0 + tk, g.K);
       }
-    }
-  };
-  auto stash = [&](int b) {
 #pragma unroll
-    for (int q = 0; q < AQ; ++q) *reinterpret_cast<double2*>(&As[b][tr + 32 * q][tk]) = ra[q];
-#pragma unroll
-    for (int q = 0; q < BQ; ++q) {
-      if (BT)
-        *reinterpret_cast<double2*>(&Bs[b][tr + 32 * q][tk]) = rb[q];
-      else
-        *reinterpret_cast<double2*>(&Bs[b][nr + (512 / BN) * q][nc]) = rb[q];
-    }
-  };
-
-  if (nt > 0) {
-    fetch(kbeg);
-    stash(0);
-  }
-  __syncthreads();
-  for (int it = 0; it < nt; ++it) {
-    const int b = it & 1;
-    if (it + 1 < nt) fetch(kbeg + (it + 1) * GBK);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      double af[TI], bf[TJ];
-#pragma unroll
-      for (int ti = 0; ti < TI; ++ti) af[ti] = As[b][wm + 16 * ti + lr][4 * lg + s];
-#pragma unroll
-      for (int tj = 0; tj < TJ; ++tj)
-        bf[tj] = BT ? Bs[b][wn + 16 * tj + lr][4 * lg + s] : Bs[b][4 * lg + s][wn + 16 * tj + lr];
-#pragma unroll
-      for (int ti = 0; ti < TI; ++ti)
-#pragma unroll
-        for (int tj = 0; tj < TJ; ++tj)
-          acc[ti][tj] = __builtin_amdgcn_mfma_f64_16x16x4f64(af[ti], bf[tj], acc[ti][tj], 0, 0, 0);
-    }
-    if (it + 1 < nt) stash(b ^ 1);
-    __syncthreads();
-  }
-#pragma unroll
-  for (int ti = 0; ti < TI; ++ti)
-#pragma unroll
-    for (int tj = 0; tj < TJ; ++tj)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        // v_mfma_f64_16x16x4f64 result: register r of lane l holds row 4r + l/16, column l%16
-        const int i = bm + wm + 16 * ti + 4 * r + lg;
-        const int j = bn + wn + 16 * tj + lr;
-        if (i < g.M && j < g.N) {
-          double* p = C + (int64_t)i * g.ldc + j;
-          const double v = g.alpha * acc[ti][tj][r];
-          *p = g.beta == 0.0 ? v : v + g.beta * *p;
+      for (int q = 0; q < BQ; ++q) {
+        if (BT) {
+          const int r = bn + tr + 32 * q;
+          rb[q] = ld_pair<VEC>(B + (int64_t)r * g.ldb + k0 + tk, r < g.N, k0 + tk, g.K);
+        } else {
+          const int k = k0 + nr + (512 / BN) * q;
+          rb[q] = ld_pair<VEC>(B + (int64_t)k * g.ldb + bn + nc, k < g.K, bn + nc, g.N);
         }
       }
+    };
+    auto stash = [&](int b) {
+#pragma unroll
+      for (int q = 0; q < AQ; ++q) *reinterpret_cast<double2*>(&As[b][tr + 32 * q][tk]) = ra[q];
+#pragma unroll
+      for (int q = 0; q < BQ; ++q) {
+        if (BT)
+          *reinterpret_cast<double2*>(&Bs[b][tr + 32 * q][tk]) = rb[q];
+        else
+          *reinterpret_cast<double2*>(&Bs[b][nr + (512 / BN) * q][nc]) = rb[q];
+      }
+    };
+
+    // the previous tile's last K step ended with a barrier, so its LDS reads are done
+    if (nt > 0) {
+      fetch(kbeg);
+      stash(0);
+    }
+    __syncthreads();
+    for (int it = 0; it < nt; ++it) {
+      const int b = it & 1;
+      if (it + 1 < nt) fetch(kbeg + (it + 1) * GBK);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        double af[TI], bf[TJ];
+#pragma unroll
+        for (int ti = 0; ti < TI; ++ti) af[ti] = As[b][wm + 16 * ti + lr][4 * lg + s];
+#pragma unroll
+        for (int tj = 0; tj < TJ; ++tj)
+          bf[tj] = BT ? Bs[b][wn + 16 * tj + lr][4 * lg + s] : Bs[b][4 * lg + s][wn + 16 * tj + lr];
+#pragma unroll
+        for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+          for (int tj = 0; tj < TJ; ++tj)
+            acc[ti][tj] = __builtin_amdgcn_mfma_f64_16x16x4f64(af[ti], bf[tj], acc[ti][tj], 0, 0, 0);
+      }
+      if (it + 1 < nt) stash(b ^ 1);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < TJ; ++tj)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          // v_mfma_f64_16x16x4f64 result: register r of lane l holds row 4r + l/16, column l%16
+          const int i = bm + wm + 16 * ti + 4 * r + lg;
+          const int j = bn + wn + 16 * tj + lr;
+          if (i < g.M && j < g.N) {
+            double* q = C + (int64_t)i * g.ldc + j;
+            const double v = g.alpha * acc[ti][tj][r];
+            *q = g.beta == 0.0 ? v : v + g.beta * *q;
+          }
+        }
+  }
 }
 
 template <bool BT, int BM, int BN>
@@ -250,14 +263,22 @@ static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
                    pairs_aligned(a0.B, a0.ldb, a0.sB1, a0.sB2);
   // 128 x 128 tiles when both dimensions reach 128 and the grid still has 512 blocks
   // (two per CU); else 128-row tiles when they keep two blocks per CU; else 64 x 64.
+  // A triangular operand folds the grid: a block takes a tile and its mirror.
   const int64_t z = (int64_t)nz1 * a0.nz2;
-  const bool wide = !g_compact_tiles && a0.M >= 128 && a0.N >= 128 &&
-                    (int64_t)((a0.M + 127) / 128) * ((a0.N + 127) / 128) * z >= 512;
+  const int fold = (a0.tri & 1) ? 1 : ((a0.tri & 2) ? 2 : 0);
+  auto blocks = [&](int tm, int tn) {
+    const int64_t r = (a0.M + tm - 1) / tm, c = (a0.N + tn - 1) / tn;
+    return (fold == 1 ? (r + 1) / 2 : r) * (fold == 2 ? (c + 1) / 2 : c) * z;
+  };
+  const bool wide = !g_compact_tiles && a0.M >= 128 && a0.N >= 128 && blocks(128, 128) >= 512;
   const int bn = wide ? 128 : 64;
-  const int bm = !g_compact_tiles && (wide || (a0.M + 127) / 128 * ((a0.N + 63) / 64) * z >= 512) ? 128 : 64;
+  const int bm = !g_compact_tiles && (wide || blocks(128, 64) >= 512) ? 128 : 64;
   GemmArgs a = a0;
-  a.ntx = (a.N + bn - 1) / bn;
-  a.nty = (a.M + bm - 1) / bm;
+  a.fold = fold;
+  a.ct = (a.N + bn - 1) / bn;
+  a.rt = (a.M + bm - 1) / bm;
+  a.ntx = fold == 2 ? (a.ct + 1) / 2 : a.ct;
+  a.nty = fold == 1 ? (a.rt + 1) / 2 : a.rt;
   a.nzt = (int)z;
   const int64_t total = (int64_t)a.ntx * a.nty * a.nzt;
   if (total > (int64_t)1 << 30) return set_error(CP_ERR_SHAPE, "fp64 GEMM grid too large");
