@@ -47,10 +47,10 @@ constexpr int NW = 256;  // outer block-column width of the left-looking sweep
 // op(B) = B [K,N] or, with BT, B^T for B stored [N,K]. Batched over blockIdx.z
 // as z = z1 * nz2 + z2 with separate strides per level.
 //
-// Block tile BM x BN (BM = 64 or 128, BN = 64 or 128), K tile 16, 4 waves each
-// building a 64-column slab from v_mfma_f64_16x16x4f64: stacked along M for
-// BN = 64 (BM/4 x 64 each), a 2 x 2 grid for BN = 128 (64 x 64 each, half the LDS
-// fragment reads per MFMA of the stacked form). The next K tile is fetched into
+// Block tile 64 x 64 or 128 x 128, K tile 16, 4 waves each building a 64-column
+// slab from v_mfma_f64_16x16x4f64: stacked along M for 64 x 64 (16 x 64 each), a
+// 2 x 2 grid for 128 x 128 (64 x 64 each, half the LDS fragment reads per MFMA of
+// the stacked form). The next K tile is fetched into
 // registers while the current one is multiplied, then stored into the other half
 // of a double-buffered LDS, so one barrier separates K tiles. The operands of one
 // MFMA step s are read from LDS just before its MFMAs, which keeps the 128 x 128
@@ -253,16 +253,18 @@ static bool pairs_aligned(const double* p, int ld, int64_t s1, int64_t s2) {
 
 // The calling thread's GEMM tile policy (cp_chol_compact_tiles): 0 picks the fastest tile
 // for a GPU the factorization has to itself; 1 keeps every GEMM at 64 x 64, whose blocks
-// (106 VGPRs, 36 KB of LDS) fit on a CU beside two EF sweep waves per SIMD, where the
-// larger tiles (158-252 VGPRs, 55-72 KB) wait for whole CUs to drain.
+// (112 VGPRs, 36 KB of LDS) fit on a CU beside two EF sweep waves per SIMD, where the
+// 128 x 128 tile (234-256 VGPRs, 69-72 KB) waits for whole CUs to drain.
 static thread_local int g_compact_tiles = 0;
 
 static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
   if (a0.M <= 0 || a0.N <= 0 || nz1 <= 0) return CP_OK;
   const bool vec = pairs_aligned(a0.A, a0.lda, a0.sA1, a0.sA2) &&
                    pairs_aligned(a0.B, a0.ldb, a0.sB1, a0.sB2);
-  // 128 x 128 tiles when both dimensions reach 128 and the grid still has 512 blocks
-  // (two per CU); else 128-row tiles when they keep two blocks per CU; else 64 x 64.
+  // 64 x 64 tiles: 112 VGPRs and 36 KB of LDS let four blocks (16 waves) share a CU,
+  // which hides the loads and barriers of short K loops better than two 128 x 128
+  // blocks do. 128 x 128 tiles only for K >= 4096 with at least 512 of them (two per
+  // CU): there the larger tile's lower L2 traffic per MFMA wins.
   // A triangular operand folds the grid: a block takes a tile and its mirror.
   const int64_t z = (int64_t)nz1 * a0.nz2;
   const int fold = (a0.tri & 1) ? 1 : ((a0.tri & 2) ? 2 : 0);
@@ -270,9 +272,9 @@ static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
     const int64_t r = (a0.M + tm - 1) / tm, c = (a0.N + tn - 1) / tn;
     return (fold == 1 ? (r + 1) / 2 : r) * (fold == 2 ? (c + 1) / 2 : c) * z;
   };
-  const bool wide = !g_compact_tiles && a0.M >= 128 && a0.N >= 128 && blocks(128, 128) >= 512;
-  const int bn = wide ? 128 : 64;
-  const int bm = !g_compact_tiles && (wide || blocks(128, 64) >= 512) ? 128 : 64;
+  const bool wide = !g_compact_tiles && a0.M >= 128 && a0.N >= 128 && a0.K >= 4096 &&
+                    blocks(128, 128) >= 512;
+  const int bm = wide ? 128 : 64, bn = bm;
   GemmArgs a = a0;
   a.fold = fold;
   a.ct = (a.N + bn - 1) / bn;
@@ -284,11 +286,9 @@ static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
   if (total > (int64_t)1 << 30) return set_error(CP_ERR_SHAPE, "fp64 GEMM grid too large");
   const dim3 grid((unsigned)(8 * ((total + 7) / 8)));
   if (bt)
-    bn == 128 ? launch_gemm<true, 128, 128>(a, grid, vec, st)
-              : bm == 128 ? launch_gemm<true, 128, 64>(a, grid, vec, st) : launch_gemm<true, 64, 64>(a, grid, vec, st);
+    wide ? launch_gemm<true, 128, 128>(a, grid, vec, st) : launch_gemm<true, 64, 64>(a, grid, vec, st);
   else
-    bn == 128 ? launch_gemm<false, 128, 128>(a, grid, vec, st)
-              : bm == 128 ? launch_gemm<false, 128, 64>(a, grid, vec, st) : launch_gemm<false, 64, 64>(a, grid, vec, st);
+    wide ? launch_gemm<false, 128, 128>(a, grid, vec, st) : launch_gemm<false, 64, 64>(a, grid, vec, st);
   CP_LAUNCHED("fp64 GEMM launch");
   return CP_OK;
 }
