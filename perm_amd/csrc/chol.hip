@@ -11,10 +11,12 @@
 //  * the act_order gather, the reversal and the damping shift fuse into one
 //    pass over H (fact_prepare);
 //  * Cholesky is left-looking in two levels: a 256-wide block column first
-//    receives the updates of everything to its left in one large-K fp64 MFMA
-//    GEMM (wide enough in N to fill the GPU); inside it each 64-wide column
-//    takes its left neighbours' updates, then its diagonal block is factored
-//    and inverted by four waves in registers and the panel below it is a GEMM
+//    receives the updates of everything to its left in two large-K fp64 MFMA
+//    GEMMs (wide enough in N to fill the GPU): the columns up to its left
+//    neighbour, queued one block column ahead (on a second stream for small
+//    batches), then the neighbour's 256. Inside it each 64-wide column takes
+//    its left neighbours' updates, then its diagonal block is factored and
+//    inverted by four waves in registers and the panel below it is a GEMM
 //    with that inverse;
 //  * L^{-1} is assembled by recursive doubling: diagonal 64-blocks come from
 //    the panel step, then at block size s, X21 = -X22 (L21 X11) for every pair
@@ -740,6 +742,31 @@ static FactWs fact_ws(char* ws, int n, int batch) {
   return w;
 }
 
+// A second stream per calling stream for the look-ahead outer updates, created on first
+// use and kept for the process, with its events: chain (the calling stream reached the end
+// of a block column), far[2] (a look-ahead update done, by block-column parity) and join.
+// Calls that share a calling stream must not run from two host threads at once.
+struct AheadStreams {
+  hipStream_t aux;
+  hipEvent_t chain, far[2], join;
+};
+static std::mutex g_ahead_mu;
+static std::map<std::pair<int, hipStream_t>, AheadStreams> g_ahead;
+static const AheadStreams* ahead_streams(hipStream_t st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> g(g_ahead_mu);
+  const auto key = std::make_pair(dev, st);
+  auto it = g_ahead.find(key);
+  if (it != g_ahead.end()) return &it->second;
+  AheadStreams a{};
+  if (hipStreamCreateWithFlags(&a.aux, hipStreamNonBlocking) != hipSuccess) return nullptr;
+  hipEvent_t* evs[4] = {&a.chain, &a.far[0], &a.far[1], &a.join};
+  for (hipEvent_t* e : evs)
+    if (hipEventCreateWithFlags(e, hipEventDisableTiming) != hipSuccess) return nullptr;
+  return &(g_ahead[key] = a);
+}
+
 // One factorization attempt of every active matrix at its damp (w.damp_d),
 // raising w.fail[z] on a bad pivot. Stream-ordered, nothing read back.
 template <typename T>
@@ -772,32 +799,76 @@ static int fact_attempt(const T* H, int64_t sH, int n, int batch, const int* ord
   // earlier columns' updates in one large-K GEMM; inside it, each NB-wide
   // column receives its left neighbours' updates, then its diagonal block is
   // factored and the panel below it solved
-  for (int k0 = 0; k0 < n; k0 += NW) {
-    const int w0 = n - k0 < NW ? n - k0 : NW;
-    if (k0 > 0) {
-      // A[k0:, k0:k0+w0] -= L[k0:, 0:k0] * L[k0:k0+w0, 0:k0]^T, lower part
-      GemmArgs ga{A + (int64_t)k0 * n, A + (int64_t)k0 * n, A + (int64_t)k0 * n + k0, n - k0, w0,
-                  k0, n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 4};
-      if (int s = dgemm(ga, batch, true, st)) return s;
-    }
-    for (int k = k0; k < k0 + w0; k += NB) {
-      const int wk = n - k < NB ? n - k : NB;
-      if (k > k0) {
-        // A[k:, k:k+wk] -= L[k:, k0:k] * L[k:k+wk, k0:k]^T
-        GemmArgs gb{A + (int64_t)k * n + k0, A + (int64_t)k * n + k0, A + (int64_t)k * n + k,
-                    n - k, wk, k - k0, n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 0};
-        if (int s = dgemm(gb, batch, true, st)) return s;
+  // Block column J (columns [k0, k0 + w0), k0 = J * NW) takes the outer updates of the
+  // columns left of it in two GEMMs: the far part, columns [0, k0 - NW), and then the near
+  // part, the 256 columns of block column J - 1. The far part of J + 2 only needs block
+  // columns up to J, so with a look-ahead stream it runs there while J + 1's near part and
+  // 64-column chain (inner updates, diagonal blocks, panels: short launches that leave most
+  // of the GPU idle) run on the calling stream. Without one it is queued in the same place
+  // on the calling stream; either way every element takes the same two subtractions.
+  // Batches of up to four matrices take the look-ahead stream. Larger ones keep the GPU
+  // busy through their own chain, and beside other size classes' work a second stream
+  // per class only took hardware queues and CUs from it.
+  const AheadStreams* ah = batch <= 4 ? ahead_streams(st) : nullptr;
+  hipStream_t aux = ah ? ah->aux : st;
+  bool aux_used = false;
+  auto join = [&]() -> int {
+    if (!aux_used) return CP_OK;
+    aux_used = false;
+    CP_HIP(hipEventRecord(ah->join, aux));
+    CP_HIP(hipStreamWaitEvent(st, ah->join, 0));
+    return CP_OK;
+  };
+  // A[kt:, kt:kt+w] -= L[kt:, kb:ke] * L[kt:kt+w, kb:ke]^T, lower part
+  auto outer = [&](int kt, int kb, int ke, hipStream_t s) -> int {
+    const int w = n - kt < NW ? n - kt : NW;
+    GemmArgs g{A + (int64_t)kt * n + kb, A + (int64_t)kt * n + kb, A + (int64_t)kt * n + kt, n - kt,
+               w, ke - kb, n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 4};
+    return dgemm(g, batch, true, s);
+  };
+  auto chol_loop = [&]() -> int {
+    const int nJ = (n + NW - 1) / NW;
+    for (int J = 0; J < nJ; ++J) {
+      const int k0 = J * NW;
+      const int w0 = n - k0 < NW ? n - k0 : NW;
+      if (J >= 2 && ah) CP_HIP(hipStreamWaitEvent(st, ah->far[J & 1], 0));
+      if (J >= 1)
+        if (int s = outer(k0, k0 - NW, k0, st)) return s;
+      for (int k = k0; k < k0 + w0; k += NB) {
+        const int wk = n - k < NB ? n - k : NB;
+        if (k > k0) {
+          // A[k:, k:k+wk] -= L[k:, k0:k] * L[k:k+wk, k0:k]^T
+          GemmArgs gb{A + (int64_t)k * n + k0, A + (int64_t)k * n + k0, A + (int64_t)k * n + k,
+                      n - k, wk, k - k0, n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 0};
+          if (int s = dgemm(gb, batch, true, st)) return s;
+        }
+        fact_diag_kernel<<<batch, 256, 0, st>>>(A, sA, X, sA, n, k, w.fail, w.active);
+        CP_LAUNCHED("factor diagonal block");
+        const int m = n - k - NB;
+        if (m <= 0) break;
+        // panel: A[k+NB:, k:k+NB] <- A[k+NB:, k:k+NB] * inv(L_kk)^T  (in place, row tiles)
+        GemmArgs pa{A + (int64_t)(k + NB) * n + k, X + (int64_t)k * n + k,
+                    A + (int64_t)(k + NB) * n + k, m, NB, NB, n, n, n, 1.0, 0.0, sA, sA, sA,
+                    0, 0, 0, 1, 0};
+        if (int s = dgemm(pa, batch, true, st)) return s;
       }
-      fact_diag_kernel<<<batch, 256, 0, st>>>(A, sA, X, sA, n, k, w.fail, w.active);
-      CP_LAUNCHED("factor diagonal block");
-      const int m = n - k - NB;
-      if (m <= 0) break;
-      // panel: A[k+NB:, k:k+NB] <- A[k+NB:, k:k+NB] * inv(L_kk)^T  (in place, row tiles)
-      GemmArgs pa{A + (int64_t)(k + NB) * n + k, X + (int64_t)k * n + k,
-                  A + (int64_t)(k + NB) * n + k, m, NB, NB, n, n, n, 1.0, 0.0, sA, sA, sA,
-                  0, 0, 0, 1, 0};
-      if (int s = dgemm(pa, batch, true, st)) return s;
+      if (J + 2 < nJ) {
+        if (ah) {
+          CP_HIP(hipEventRecord(ah->chain, st));
+          CP_HIP(hipStreamWaitEvent(aux, ah->chain, 0));
+          aux_used = true;
+        }
+        if (int s = outer(k0 + 2 * NW, 0, k0 + NW, aux)) return s;
+        if (ah) CP_HIP(hipEventRecord(ah->far[J & 1], aux));
+      }
     }
+    return CP_OK;
+  };
+  {
+    const int s = chol_loop();
+    const int j = join();  // nothing of this call is left on the look-ahead stream
+    if (s) return s;
+    if (j) return j;
   }
   // L^{-1} by recursive doubling over neighbouring s-blocks
   for (int s = NB; s < n; s *= 2) {
