@@ -192,11 +192,19 @@ def ef_phase(W, H, slot, layers, mode, concurrent=True, keep=None):
     classes = [(H[d], builder(d)) for d in sorted(H, reverse=True)]
     if concurrent:
         return gef.encode_size_classes(classes, n_iter=2, mode=mode, damp=0.01)
+    # one class at a time, queued as encode_size_classes queues each class: a single
+    # factorization attempt whose flags are read after the class's EF, so the host does
+    # not wait between the factorization and the EF; a failed matrix sends the class
+    # through the escalating factorization and the EF again
     outs = []
     for Hb, build in classes:
         order = gef.act_order_dev(Hb)
-        U, _ = gef.factor_dev(Hb, order, 0.01, checked=True)
-        outs.append(gef.ef_encode_dev(build(U, order), n_iter=2, mode=mode, checked=True))
+        U, flags = gef.factor_dev_async(Hb, order, 0.01, checked=True)
+        out = gef.ef_encode_dev(build(U, order), n_iter=2, mode=mode, checked=True)
+        if int(flags.sum()):
+            U, _ = gef.factor_dev(Hb, order, 0.01, checked=True)
+            out = gef.ef_encode_dev(build(U, order), n_iter=2, mode=mode, checked=True)
+        outs.append(out)
     return outs
 
 
@@ -919,9 +927,12 @@ def config_main(args):
         f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         f0.record()
         order = gef.act_order_dev(H[d])
-        U, _ = gef.factor_dev(H[d], order, 0.01, checked=True)
+        U, flags = gef.factor_dev_async(H[d], order, 0.01, checked=True)
         f1.record()
         gef.ef_encode_dev(builder(d)(U, order), 2, _lib.CP_EF_EXACT, checked=True)
+        if int(flags.sum()):  # a failed matrix: the escalating factorization, EF again
+            U, _ = gef.factor_dev(H[d], order, 0.01, checked=True)
+            gef.ef_encode_dev(builder(d)(U, order), 2, _lib.CP_EF_EXACT, checked=True)
         kernels[d] = last_sweep_kernel(lib)
         buf = (ctypes.c_float * 5)()
         lib.cp_ef_phase_ms(ctypes.cast(buf, ctypes.c_void_p), 5)
