@@ -43,6 +43,8 @@ typedef double dbl4 __attribute__((ext_vector_type(4)));
 
 constexpr int NB = 64;   // diagonal block and panel width
 constexpr int NW = 256;  // outer block-column width of the left-looking sweep
+constexpr int CHUNK_N = 8192;  // n from which outer updates sum K in chunks of KC
+constexpr int KC = 1024;
 
 // ---------------------------------------------------------------- fp64 MFMA GEMM
 // C[M,N] = alpha * A[M,K] * op(B) + beta * C, row-major with leading dims.
@@ -76,6 +78,7 @@ struct GemmArgs {
   int64_t sA1, sB1, sC1, sA2, sB2, sC2;
   int nz2;
   int tri;
+  int kc;              // > 0: batch index z2 picks the K range [z2 * kc, z2 * kc + kc)
   int ntx, nty, nzt;  // block grid: column tiles, row tiles, batch entries (set by dgemm())
   int fold;           // 1: grid row by also takes row tile rt - 1 - by; 2: the same for columns
   int rt, ct;         // row and column tiles of the product (set by dgemm())
@@ -162,8 +165,14 @@ __global__ __launch_bounds__(256, 2) void dgemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < TJ; ++j) acc[i][j] = dbl4{0.0, 0.0, 0.0, 0.0};
 
-    const int kbeg = (g.tri & 2) ? (bn & ~(GBK - 1)) : 0;
-    const int kend = (g.tri & 1) ? min(g.K, bm + BM) : g.K;
+    int kbeg = (g.tri & 2) ? (bn & ~(GBK - 1)) : 0;
+    int kend = (g.tri & 1) ? min(g.K, bm + BM) : g.K;
+    if (g.kc > 0) {
+      kbeg = max(kbeg, z2 * g.kc);
+      kend = min(kend, z2 * g.kc + g.kc);
+    }
+    // columns at or past klim load as zero: K's end, or the end of this block's chunk
+    const int klim = g.kc > 0 ? kend : g.K;
     const int nt = kend > kbeg ? (kend - kbeg + GBK - 1) / GBK : 0;
 
     double2 ra[AQ], rb[BQ];
@@ -171,16 +180,16 @@ __global__ __launch_bounds__(256, 2) void dgemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int q = 0; q < AQ; ++q) {
         const int r = bm + tr + 32 * q;
-        ra[q] = ld_pair<VEC>(A + (int64_t)r * g.lda + k0 + tk, r < g.M, k0 + tk, g.K);
+        ra[q] = ld_pair<VEC>(A + (int64_t)r * g.lda + k0 + tk, r < g.M, k0 + tk, klim);
       }
 #pragma unroll
       for (int q = 0; q < BQ; ++q) {
         if (BT) {
           const int r = bn + tr + 32 * q;
-          rb[q] = ld_pair<VEC>(B + (int64_t)r * g.ldb + k0 + tk, r < g.N, k0 + tk, g.K);
+          rb[q] = ld_pair<VEC>(B + (int64_t)r * g.ldb + k0 + tk, r < g.N, k0 + tk, klim);
         } else {
           const int k = k0 + nr + (512 / BN) * q;
-          rb[q] = ld_pair<VEC>(B + (int64_t)k * g.ldb + bn + nc, k < g.K, bn + nc, g.N);
+          rb[q] = ld_pair<VEC>(B + (int64_t)k * g.ldb + bn + nc, k < klim, bn + nc, g.N);
         }
       }
     };
@@ -274,7 +283,8 @@ static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
     const int64_t r = (a0.M + tm - 1) / tm, c = (a0.N + tn - 1) / tn;
     return (fold == 1 ? (r + 1) / 2 : r) * (fold == 2 ? (c + 1) / 2 : c) * z;
   };
-  const bool wide = !g_compact_tiles && a0.M >= 128 && a0.N >= 128 && a0.K >= 4096 &&
+  const int kblock = a0.kc > 0 ? min(a0.kc, a0.K) : a0.K;  // K of one block's loop
+  const bool wide = !g_compact_tiles && a0.M >= 128 && a0.N >= 128 && kblock >= 4096 &&
                     blocks(128, 128) >= 512;
   const int bm = wide ? 128 : 64, bn = bm;
   GemmArgs a = a0;
@@ -626,6 +636,23 @@ __global__ void fact_output_kernel(const double* X, int64_t sX, int n, OutT* U, 
   U[z * sU + (int64_t)i * n + j] = v;
 }
 
+// C[i][j] -= P[0][i][j], then P[1][i][j], ... P[S-1][i][j], for i >= j (the lower part
+// an outer update keeps): the chunk partials of a split outer update, subtracted in the
+// order a chunk-by-chunk GEMM would subtract them.
+__global__ void fact_chunk_sub_kernel(const double* P, int64_t sP, int64_t sPc, int S, double* C,
+                                      int ldc, int64_t sC, int M, int N, const int* active) {
+  const int z = blockIdx.z;
+  if (active && !active[z]) return;
+  const int j = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int i = blockIdx.y * 4 + (threadIdx.x >> 6);
+  if (i >= M || j >= N || i < j) return;
+  const double* p = P + z * sP + (int64_t)i * N + j;
+  double* c = C + z * sC + (int64_t)i * ldc + j;
+  double v = *c;
+  for (int s = 0; s < S; ++s) v = v - p[s * sPc];
+  *c = v;
+}
+
 __global__ void fill_kernel(double* p, int64_t count, double v) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   for (; i < count; i += (int64_t)gridDim.x * blockDim.x) p[i] = v;
@@ -777,8 +804,8 @@ static int fact_attempt(const T* H, int64_t sH, int n, int batch, const int* ord
   double *A = w.A, *X = w.X, *Tm = w.Tm;
   fill_i32_kernel<<<(batch + 255) / 256, 256, 0, st>>>(w.fail, batch, 0);
   fill_kernel<<<1024, 256, 0, st>>>(X, (int64_t)nn * batch, 0.0);
-  // the order check's marks live in the GEMM scratch Tm, which the doubling GEMMs
-  // later overwrite without reading (beta = 0)
+  // the order check's marks live in the GEMM scratch Tm, which the split outer updates
+  // and the doubling GEMMs later overwrite before reading
   fact_shift_kernel<T><<<batch, 256, 0, st>>>(H, n, sH, order, sO, w.damp_d, w.diag_tmp, w.shift,
                                                 w.active, reinterpret_cast<int*>(Tm),
                                                 (int64_t)(2 * nn), w.fail);
@@ -819,12 +846,37 @@ static int fact_attempt(const T* H, int64_t sH, int n, int batch, const int* ord
     CP_HIP(hipStreamWaitEvent(st, ah->join, 0));
     return CP_OK;
   };
-  // A[kt:, kt:kt+w] -= L[kt:, kb:ke] * L[kt:kt+w, kb:ke]^T, lower part
+  // A[kt:, kt:kt+w] -= L[kt:, kb:ke] * L[kt:kt+w, kb:ke]^T, lower part. For n >= CHUNK_N
+  // the K range is summed in chunks of KC columns from kb, each chunk's product subtracted
+  // in turn: by one GEMM per chunk when the GEMM has blocks enough to fill the GPU, else
+  // (few row tiles left, long K) by one GEMM whose blocks each take one chunk, writing
+  // the chunk products into Tm (free during the Cholesky), and fact_chunk_sub_kernel.
+  // Both give every element the same subtractions, so U does not depend on the choice.
   auto outer = [&](int kt, int kb, int ke, hipStream_t s) -> int {
-    const int w = n - kt < NW ? n - kt : NW;
-    GemmArgs g{A + (int64_t)kt * n + kb, A + (int64_t)kt * n + kb, A + (int64_t)kt * n + kt, n - kt,
-               w, ke - kb, n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 4};
-    return dgemm(g, batch, true, s);
+    const int nw = n - kt < NW ? n - kt : NW;
+    const int M = n - kt, K = ke - kb;
+    const int S = n >= CHUNK_N ? (K + KC - 1) / KC : 1;
+    auto part = [&](int c0, int c1) -> int {
+      GemmArgs g{A + (int64_t)kt * n + c0, A + (int64_t)kt * n + c0, A + (int64_t)kt * n + kt, M,
+                 nw, c1 - c0, n, n, n, -1.0, 1.0, sA, sA, sA, 0, 0, 0, 1, 4};
+      return dgemm(g, batch, true, s);
+    };
+    if (S == 1) return part(kb, ke);
+    const int64_t blocks = (int64_t)((M + 63) / 64) * ((nw + 63) / 64) * batch;
+    if (blocks < 512) {
+      // chunk products P[z][c][i][j] = sum over chunk c of L[kt+i][k] L[kt+j][k]
+      GemmArgs g{A + (int64_t)kt * n + kb, A + (int64_t)kt * n + kb, Tm, M, nw, K, n, n, nw,
+                 1.0, 0.0, sA, sA, (int64_t)nn, 0, 0, (int64_t)M * nw, S, 4};
+      g.kc = KC;
+      if (int e = dgemm(g, batch, true, s)) return e;
+      fact_chunk_sub_kernel<<<dim3((nw + 63) / 64, (M + 3) / 4, batch), 256, 0, s>>>(
+          Tm, (int64_t)nn, (int64_t)M * nw, S, A + (int64_t)kt * n + kt, n, sA, M, nw, w.active);
+      CP_LAUNCHED("factor chunk subtraction");
+      return CP_OK;
+    }
+    for (int c = 0; c < S; ++c)
+      if (int e = part(kb + c * KC, kb + (c + 1) * KC < ke ? kb + (c + 1) * KC : ke)) return e;
+    return CP_OK;
   };
   auto chol_loop = [&]() -> int {
     const int nJ = (n + NW - 1) / NW;

@@ -453,6 +453,33 @@ def test_factor_compact_tiles_give_the_same_factor(ef, n, batch):
     assert torch.equal(Ua, Ub)
 
 
+def test_factor_chunked_outer_updates_do_not_depend_on_the_schedule(ef):
+    """From n = 8192 the outer updates sum K in 1024-column chunks. A single matrix has
+    too few row tiles to fill the GPU, so each outer update computes all its chunk
+    products at once and subtracts them in order afterwards; in a batch of eight most
+    outer updates run one GEMM per chunk instead. Both must give the same U bit for bit,
+    and U must invert H + lambda I."""
+    from perm_amd.hessians import xtx_accumulate_many
+    from perm_amd import workloads as wl
+    n, batch = 8448, 8
+    _say(f"chunked outer updates n={n} batch={batch}")
+    Hb = torch.zeros(batch, n, n, device="cuda")
+    for z in range(batch):
+        xtx_accumulate_many([wl.student_t_activations(2 * n, n, seed=70 + z)], [Hb[z]])
+    order = ef.act_order_dev(Hb)
+    Ub, used = ef.factor_dev(Hb, order, 0.01, out_dtype=torch.float64)
+    assert used == [0.01] * batch
+    for z in (0, 5):
+        Uz, _ = ef.factor_dev(Hb[z].contiguous(), order[z], 0.01, out_dtype=torch.float64)
+        assert torch.equal(Ub[z], Uz)
+    o = order[0].long()
+    Hp = Hb[0].double()[o][:, o]
+    lam = 0.01 * float(torch.diagonal(Hp).mean()) + 1e-8
+    v = torch.randn((n, 4), device="cuda", dtype=torch.float64)
+    r = Ub[0].T @ (Ub[0] @ (Hp @ v + lam * v))
+    assert float((r - v).abs().max() / v.abs().max()) < 1e-8
+
+
 def test_factor_async_flags_a_failed_matrix(ef):
     n = 256
     eig = np.linspace(1.0, 100.0, n)
