@@ -15,9 +15,9 @@
 //    GEMMs (wide enough in N to fill the GPU): the columns up to its left
 //    neighbour, queued one block column ahead (on a second stream for small
 //    batches), then the neighbour's 256. Inside it each 64-wide column takes
-//    its left neighbours' updates, then its diagonal block is factored and
-//    inverted by four waves in registers and the panel below it is a GEMM
-//    with that inverse;
+//    its left neighbours' updates, then its diagonal block is factored by
+//    four waves in registers and inverted by blocked doubling, and the panel
+//    below it is a GEMM with that inverse;
 //  * L^{-1} is assembled by recursive doubling: diagonal 64-blocks come from
 //    the panel step, then at block size s, X21 = -X22 (L21 X11) for every pair
 //    of neighbouring s-blocks -- two batched fp64 MFMA GEMMs per level that
@@ -528,9 +528,10 @@ __global__ __launch_bounds__(256) void fact_prepare_kernel(const T* H, int n, in
 // after one barrier every wave subtracts L[i][j] L[c][j] from its columns
 // c > j, reading L[c][j] from lane c by readlane. Entries above the diagonal
 // collect finite garbage on the way and are never stored. The inverse is
-// column-oriented forward substitution with the same layout turned round: lane
-// i solves for column i of inv(L_kk), wave w owns its rows 4m + w, and the
-// owner of row r publishes x_r before the others eliminate it.
+// blocked doubling: each wave inverts one 16 x 16 diagonal block by forward
+// substitution (lane c solves column c, no exchange between lanes), then two
+// levels of X21 = -X22 (L21 X11) on v_mfma_f64_16x16x4f64 join them into 32 x 32
+// and 64 x 64: three barriers where a column-by-column inverse needs 64.
 __device__ inline double readlane_f64(double v, int lane) {
   const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
   const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, lane);
@@ -591,30 +592,90 @@ __global__ __launch_bounds__(256) void fact_diag_kernel(double* A, int64_t sA, d
   for (int m = 0; m < 16; ++m) L[i][4 * m + w] = a[m];
   __syncthreads();
 
-  // a[m] now accumulates row 4m + w of column i of inv(L_kk)
+  // inv(L_kk) by blocked doubling. X = inv(L_kk) shares the LDS array with L: X[r][c]
+  // (c <= r) sits at L[c][r + 1], in the strict upper triangle and the padding column,
+  // which L does not use.
+  const int lr = i & 15, lg = i >> 4;
+  auto xget = [&](int r, int c) -> double { return c <= r ? L[c][r + 1] : 0.0; };
+  // 1) the four 16 x 16 diagonal blocks, one per wave: lane c < 16 solves column c by
+  //    forward substitution, x_r = (e_c[r] - sum_{m<r} L[r][m] x_m) / L[r][r] (the other
+  //    lanes compute zeros and store nothing)
+  {
+    const int o = 16 * w;
+    double x[16];
 #pragma unroll
-  for (int m = 0; m < 16; ++m) a[m] = 4 * m + w == i ? 1.0 : 0.0;
+    for (int r = 0; r < 16; ++r) {
+      double v = r == i ? 1.0 : 0.0;
 #pragma unroll
-  for (int J = 0; J < 16; ++J) {
+      for (int m = 0; m < r; ++m) v = __builtin_fma(-L[o + r][o + m], x[m], v);
+      x[r] = v / L[o + r][o + r];
+      asm volatile("" :: "v"(x[r]) : "memory");  // x_r before row r + 1's reads
+    }
+    if (i < 16) {
 #pragma unroll
-    for (int jw = 0; jw < 4; ++jw) {
-      const int r = 4 * J + jw;
-      if (w == jw) {
-        a[J] = a[J] / L[r][r];
-        pub[r & 1][i] = a[J];
-      }
-      __syncthreads();
-      const double xr = pub[r & 1][i];
-      if (w > jw) a[J] = __builtin_fma(-L[4 * J + w][r], xr, a[J]);
-#pragma unroll
-      for (int m = J + 1; m < 16; ++m) a[m] = __builtin_fma(-L[4 * m + w][r], xr, a[m]);
+      for (int m = 0; m < 16; ++m)
+        if (m >= i) L[o + i][o + m + 1] = x[m];
     }
   }
+  __syncthreads();
+  // 2) 16 -> 32: for the block pairs at 0 and 32, X21 = -X22 (L21 X11), waves 0 and 2.
+  //    In v_mfma_f64_16x16x4f64, lane l gives A[l % 16][k] and B[k][l % 16] with
+  //    k = 4 s + l / 16 at step s, and result register q holds row 4 q + l / 16, column
+  //    l % 16: so T's register s is the B operand of step s of the second product.
+  if (w == 0 || w == 2) {
+    const int o0 = 16 * w, o1 = o0 + 16;
+    dbl4 tacc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const int k = 4 * s4 + lg;
+      tacc = __builtin_amdgcn_mfma_f64_16x16x4f64(L[o1 + lr][o0 + k], xget(o0 + k, o0 + lr), tacc,
+                                                  0, 0, 0);
+    }
+    dbl4 xacc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const int k = 4 * s4 + lg;
+      xacc = __builtin_amdgcn_mfma_f64_16x16x4f64(xget(o1 + lr, o1 + k), tacc[s4], xacc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) L[o0 + lr][o1 + 4 * q + lg + 1] = -xacc[q];
+  }
+  __syncthreads();
+  // 3) 32 -> 64: X21 = -X22 (L21 X11) with 32 x 32 blocks; wave w owns 16 x 16 block
+  //    (bi, bj) of each product. T goes where X21 will be stored.
+  {
+    const int bi = w >> 1, bj = w & 1;
+    dbl4 tacc = {0.0, 0.0, 0.0, 0.0};
+    for (int bk = bj; bk < 2; ++bk) {  // X11[bk][bj] = 0 for bk < bj
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int k = 16 * bk + 4 * s4 + lg;
+        tacc = __builtin_amdgcn_mfma_f64_16x16x4f64(L[32 + 16 * bi + lr][k], xget(k, 16 * bj + lr),
+                                                    tacc, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) L[16 * bj + lr][33 + 16 * bi + 4 * q + lg] = tacc[q];
+    __syncthreads();
+    dbl4 xacc = {0.0, 0.0, 0.0, 0.0};
+    for (int bk = 0; bk <= bi; ++bk) {  // X22[bi][bk] = 0 for bk > bi
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int k = 16 * bk + 4 * s4 + lg;
+        xacc = __builtin_amdgcn_mfma_f64_16x16x4f64(xget(32 + 16 * bi + lr, 32 + k),
+                                                    L[16 * bj + lr][33 + k], xacc, 0, 0, 0);
+      }
+    }
+    __syncthreads();  // every wave has read T
+#pragma unroll
+    for (int q = 0; q < 4; ++q) L[16 * bj + lr][33 + 16 * bi + 4 * q + lg] = -xacc[q];
+  }
+  __syncthreads();
 #pragma unroll
   for (int m = 0; m < 16; ++m) {
     const int r = 4 * m + w;
     if (r < nb && i < nb) {
-      Xk[(int64_t)r * n + i] = a[m];
+      Xk[(int64_t)r * n + i] = i <= r ? L[i][r + 1] : 0.0;
       Ak[(int64_t)r * n + i] = i <= r ? L[r][i] : 0.0;
     }
   }
