@@ -833,11 +833,14 @@ static FactWs fact_ws(char* ws, int n, int batch) {
 // A second stream per calling stream for the look-ahead outer updates, created on first
 // use and kept for the process, with its events: chain (the calling stream reached the end
 // of a block column), far[2] (a look-ahead update done, by block-column parity) and join.
-// Calls that share a calling stream must not run from two host threads at once.
+// Calls that share a calling stream must not run from two host threads at once. At most
+// kMaxAhead calling streams get one; calls on further streams queue the look-ahead
+// updates in place on the calling stream (same result).
 struct AheadStreams {
   hipStream_t aux;
   hipEvent_t chain, far[2], join;
 };
+constexpr size_t kMaxAhead = 64;
 static std::mutex g_ahead_mu;
 static std::map<std::pair<int, hipStream_t>, AheadStreams> g_ahead;
 static const AheadStreams* ahead_streams(hipStream_t st) {
@@ -847,6 +850,7 @@ static const AheadStreams* ahead_streams(hipStream_t st) {
   const auto key = std::make_pair(dev, st);
   auto it = g_ahead.find(key);
   if (it != g_ahead.end()) return &it->second;
+  if (g_ahead.size() >= kMaxAhead) return nullptr;
   AheadStreams a{};
   if (hipStreamCreateWithFlags(&a.aux, hipStreamNonBlocking) != hipSuccess) return nullptr;
   hipEvent_t* evs[4] = {&a.chain, &a.far[0], &a.far[1], &a.join};
