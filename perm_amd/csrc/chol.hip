@@ -851,11 +851,22 @@ static const AheadStreams* ahead_streams(hipStream_t st) {
   auto it = g_ahead.find(key);
   if (it != g_ahead.end()) return &it->second;
   if (g_ahead.size() >= kMaxAhead) return nullptr;
+  // on any failure: release what was made, clear HIP's last error, and let the call queue
+  // its look-ahead updates on the calling stream
   AheadStreams a{};
-  if (hipStreamCreateWithFlags(&a.aux, hipStreamNonBlocking) != hipSuccess) return nullptr;
+  if (hipStreamCreateWithFlags(&a.aux, hipStreamNonBlocking) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
   hipEvent_t* evs[4] = {&a.chain, &a.far[0], &a.far[1], &a.join};
-  for (hipEvent_t* e : evs)
-    if (hipEventCreateWithFlags(e, hipEventDisableTiming) != hipSuccess) return nullptr;
+  for (int e = 0; e < 4; ++e) {
+    if (hipEventCreateWithFlags(evs[e], hipEventDisableTiming) != hipSuccess) {
+      for (int f = 0; f < e; ++f) (void)hipEventDestroy(*evs[f]);
+      (void)hipStreamDestroy(a.aux);
+      (void)hipGetLastError();
+      return nullptr;
+    }
+  }
   return &(g_ahead[key] = a);
 }
 
