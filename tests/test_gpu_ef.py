@@ -480,6 +480,44 @@ def test_factor_chunked_outer_updates_do_not_depend_on_the_schedule(ef):
     assert float((r - v).abs().max() / v.abs().max()) < 1e-8
 
 
+def test_factor_on_many_streams_gives_one_factor(ef):
+    """A factorization of a small batch runs its look-ahead updates on a second stream kept
+    per calling stream, for up to 64 calling streams; past that it queues them on the
+    calling stream. U must be the same bit for bit on every stream: 70 raw HIP streams
+    here (torch's pool would hand out only 32 distinct ones), so the last ones take the
+    in-place path."""
+    n = 1280
+    _say(f"factor on 70 streams n={n}")
+    hip = ctypes.CDLL(_lib.LIB_PATH)  # resolves the HIP runtime the library links
+    hip.hipStreamCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipStreamDestroy.argtypes = [ctypes.c_void_p]
+    H = torch.from_numpy(correlated_hessian(n, 2 * n, seed=17)).cuda()
+    order = ef.act_order_dev(H)
+    U0, _ = ef.factor_dev(H, order, 0.01)
+    raw = []
+    try:
+        for _ in range(70):
+            h = ctypes.c_void_p()
+            assert hip.hipStreamCreate(ctypes.byref(h)) == 0
+            raw.append(h)
+        outs = []
+        for h in raw:
+            s = torch.cuda.ExternalStream(h.value)
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                outs.append(ef.factor_dev_async(H, order, 0.01))
+        torch.cuda.synchronize()
+        for U, flags in outs:
+            assert int(flags.sum()) == 0
+            assert torch.equal(U, U0)
+    finally:
+        torch.cuda.synchronize()
+        outs = None
+        torch.cuda.empty_cache()  # no cached block stays tied to a stream destroyed below
+        for h in raw:
+            hip.hipStreamDestroy(h)
+
+
 def test_factor_async_flags_a_failed_matrix(ef):
     n = 256
     eig = np.linspace(1.0, 100.0, n)
