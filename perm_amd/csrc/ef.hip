@@ -181,13 +181,14 @@ __device__ __forceinline__ float bcast_group(float x, int own) {
   }
 }
 
-// Columns hb .. hb + kGridCols - 1 (one quarter block; sg / sm hold its grid). tile is
-// the compact diagonal tile; row cb holds columns 16 * (cb / 16) .. 63.
-template <int RS>
+// Columns HB .. HB + kGridCols - 1 (one quarter block; sg / sm hold its grid). tile is
+// the compact diagonal tile; row cb holds columns 16 * (cb / 16) .. 63. HB is a
+// template argument so every column's lane group and register are compile-time.
+template <int RS, int HB>
 __device__ __forceinline__ void sweep_part_split(const SweepTask& tk, int i1, int rr, int rl, int g,
                                                  float (&tl)[RS], const float* tile,
-                                                 const float (*sg)[RS], const float (*sm)[RS],
-                                                 int hb) {
+                                                 const float (*sg)[RS], const float (*sm)[RS]) {
+  constexpr int hb = HB;
   const int nrow = tk.nrow;
   // Running output pointers (row rr, column i1 + hb + a), opaque to the
   // compiler so the unrolled columns do not each keep a precomputed address.
@@ -200,17 +201,63 @@ __device__ __forceinline__ void sweep_part_split(const SweepTask& tk, int i1, in
   float* pe = tk.E + o0;
   float* pw = tk.WcurT + o0;
   uint8_t* pl = tk.LT + o0;
+  // Column cb's LDS operands (grid step and offset of the row, the diagonal entry and
+  // the lane's part of tile row cb) do not depend on the column chain. They are read
+  // one column ahead, so no LDS round trip sits between one column's error and the
+  // next column's quantization.
+  struct ColOps {
+    float dl, ml, diag;
+    float4 u[RS / 4];
+  };
+  // row cb of the tile, indexed by block column (entries below 16 p are not stored;
+  // only lanes whose elements are finished read them); only the tile pieces a column
+  // updates (from jlo on) are read
+  const auto jlo_of = [](int cb) { return cb / RS == 64 / RS - 1 ? (cb % RS + 1) & ~3 : 0; };
+  const auto read_ops = [&](int a, ColOps& c) {
+    const int cb = hb + a, p = cb / 16;
+    const float* row = tile + tile_base(p) + (cb % 16) * (64 - 16 * p) - 16 * p;
+    c.dl = sg[a][rl];
+    c.ml = sm[a][rl];
+    c.diag = row[cb];
+    const float4* ul = reinterpret_cast<const float4*>(row + RS * g);
+    const int jlo = jlo_of(cb);
+#pragma unroll
+    for (int j4 = 0; j4 < RS / 4; ++j4)
+      if (4 * j4 >= jlo) c.u[j4] = ul[j4];  // constant once the column loop is unrolled
+  };
+  // Column cb's update of register k of every lane group, t = fl(t - fl(e * u)).
+  const auto apply = [&](float e, const ColOps& c, int k) {
+    const float4 u = c.u[k / 4];
+    const float uk = (k % 4 == 0) ? u.x : (k % 4 == 1) ? u.y : (k % 4 == 2) ? u.z : u.w;
+    tl[k] = tl[k] - e * uk;
+  };
+  // The updates of a column are split in two. The register holding the next column's
+  // target (index (cb + 1) % RS in every lane group) takes column cb's update at once,
+  // so the next quantization can start; the other registers take it in the next
+  // column's scheduling region, where those independent subtractions fill the latency
+  // of that column's divisions. Each register still receives the columns' updates in
+  // ascending order, each exactly once; registers of finished columns take updates
+  // that are never read.
+  ColOps ops[3];
+  read_ops(0, ops[0]);
+  float e_prev = 0.0f;
 #pragma unroll
   for (int a = 0; a < kGridCols; ++a) {
     const int cb = hb + a;
-    const int own = cb / RS, i = cb % RS, p = cb / 16;
-    // row cb of the tile, indexed by block column (entries below 16 p are not
-    // stored; only lanes whose elements are finished read them)
-    const float* row = tile + tile_base(p) + (cb % 16) * (64 - 16 * p) - 16 * p;
+    const int own = cb / RS, i = cb % RS;
+    ColOps& cur = ops[a % 3];
+    if (a + 1 < kGridCols) read_ops(a + 1, ops[(a + 1) % 3]);
+    if (a > 0) {  // column cb - 1's remaining updates; register i took it already
+      const ColOps& prev = ops[(a + 2) % 3];
+      const int jlo = jlo_of(cb - 1);
+#pragma unroll
+      for (int k = 0; k < RS; ++k)
+        if (k >= jlo && k != i) apply(e_prev, prev, k);  // constant once unrolled
+    }
     const float tb = bcast_group<RS>(tl[i], own);
     float e;
     int q;
-    quantize_col(tk, tb, sg[a][rl], sm[a][rl], row[cb], e, q);
+    quantize_col(tk, tb, cur.dl, cur.ml, cur.diag, e, q);
     *(GlobFw)pe = e;
     *(GlobFw)pw = tb;
     *(GlobBw)pl = (uint8_t)(q - tk.lo);
@@ -218,18 +265,18 @@ __device__ __forceinline__ void sweep_part_split(const SweepTask& tk, int i1, in
     pw += nrow;
     pl += nrow;
     asm volatile("" : "+v"(pe), "+v"(pw), "+v"(pl));
-    const int jlo = own == 64 / RS - 1 ? (i + 1) & ~3 : 0;
-    const float4* ul = reinterpret_cast<const float4*>(row + RS * g);
+    if (cb + 1 < 64) apply(e, cur, (cb + 1) % RS);  // the next column's target first
+    e_prev = e;
+    // one column's region at a time; the next column's operands are already in flight
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  {  // the part's last column: its remaining updates before the next part's grid
+    const int cb = hb + kGridCols - 1;
+    const ColOps& last = ops[(kGridCols - 1) % 3];
+    const int jlo = jlo_of(cb), nx = (cb + 1) % RS;
 #pragma unroll
-    for (int j4 = 0; j4 < RS / 4; ++j4) {
-      if (4 * j4 < jlo) continue;  // constant once the column loop is unrolled
-      const float4 u = ul[j4];
-      tl[4 * j4] = tl[4 * j4] - e * u.x;
-      tl[4 * j4 + 1] = tl[4 * j4 + 1] - e * u.y;
-      tl[4 * j4 + 2] = tl[4 * j4 + 2] - e * u.z;
-      tl[4 * j4 + 3] = tl[4 * j4 + 3] - e * u.w;
-    }
-    __builtin_amdgcn_sched_barrier(0);  // one column's tile row in registers at a time
+    for (int k = 0; k < RS; ++k)
+      if (k >= jlo && (cb + 1 >= 64 || k != nx)) apply(e_prev, last, k);
   }
 }
 
@@ -268,6 +315,34 @@ __device__ __forceinline__ void store_grid(const GridPart<RS>& g, int l, float (
     sg[part + P * k][rl] = g.d[k];
     sm[part + P * k][rl] = g.m[k];
   }
+}
+
+// The block's four quarter blocks in order: each stages its grid in LDS, then sweeps
+// its 16 columns. sync orders the LDS writes against the reads (a wave barrier when
+// the LDS is the wave's own, a workgroup barrier otherwise).
+template <int RS, class Sync>
+__device__ __forceinline__ void sweep_quarters(const SweepTask& tk, int i1, int rr, int l,
+                                               float (&tl)[RS], const float* tile,
+                                               const GridPart<RS> (&gp)[64 / kGridCols],
+                                               float (*sg)[RS], float (*sm)[RS], Sync sync) {
+  static_assert(64 / kGridCols == 4, "four quarter blocks");
+  const int rl = l % RS, part = l / RS;
+  store_grid<RS>(gp[0], l, sg, sm);
+  sync();
+  sweep_part_split<RS, 0>(tk, i1, rr, rl, part, tl, tile, sg, sm);
+  sync();
+  store_grid<RS>(gp[1], l, sg, sm);
+  sync();
+  sweep_part_split<RS, kGridCols>(tk, i1, rr, rl, part, tl, tile, sg, sm);
+  sync();
+  store_grid<RS>(gp[2], l, sg, sm);
+  sync();
+  sweep_part_split<RS, 2 * kGridCols>(tk, i1, rr, rl, part, tl, tile, sg, sm);
+  sync();
+  store_grid<RS>(gp[3], l, sg, sm);
+  sync();
+  sweep_part_split<RS, 3 * kGridCols>(tk, i1, rr, rl, part, tl, tile, sg, sm);
+  sync();
 }
 
 template <int B>
@@ -519,13 +594,7 @@ __device__ __forceinline__ void sweep_block_rows(const SweepTask& tk, int i1, in
       for (int a = 0; a < 16; ++a) s.tile[tile_base(p) + a * (64 - 16 * p) + l] = u[a];
     }
   }
-#pragma unroll
-  for (int q = 0; q < 64 / kGridCols; ++q) {
-    store_grid<RS>(gp[q], l, sg, sm);
-    WaveSync()();
-    sweep_part_split<RS>(tk, i1, rr, rl, part, tl, s.tile, sg, sm, q * kGridCols);
-    WaveSync()();
-  }
+  sweep_quarters<RS>(tk, i1, rr, l, tl, s.tile, gp, sg, sm, WaveSync());
 }
 
 template <int RS>
@@ -655,13 +724,7 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
         for (int a = 0; a < 16; ++a) lds[tile_base(p) + a * (64 - 16 * p) + l] = u[a];
       }
     }
-#pragma unroll
-    for (int q = 0; q < 64 / kGridCols; ++q) {
-      store_grid<RS>(gp[q], l, sg, sm);
-      __syncthreads();
-      sweep_part_split<RS>(tk, i1, rr, rl, part, tl, lds, sg, sm, q * kGridCols);
-      __syncthreads();
-    }
+    sweep_quarters<RS>(tk, i1, rr, l, tl, lds, gp, sg, sm, [] { __syncthreads(); });
   }
 }
 
