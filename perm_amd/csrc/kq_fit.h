@@ -19,31 +19,59 @@ namespace cp {
 
 template <int N>
 __device__ __forceinline__ float affine_err(const float (&x)[N], const float (&w)[N],
-                                            const int (&L)[N], float scale, float off,
+                                            const float (&lf)[N], float scale, float off,
                                             bool mad) {
   float t[N];
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    float r = (scale * (float)L[i] + off) - x[i];
+    float r = (scale * lf[i] + off) - x[i];
     r = mad ? fabsf(r) : r * r;
     t[i] = w[i] * r;
   }
   return psum<N>(t);
 }
 
+// Codes of one candidate, clip(nearest_int(inv * (x - lo)), 0, nmax), as floats.
+// fast: the same codes through a float round trip of the 1.5*2^23 magic add and one
+// v_med3_f32, valid when every inv * (x - lo) is finite and inside (-2^22, 2^22 - 1/2)
+// (there the magic add rounds to the nearest integer, ties to even, in both forms;
+// outside it the integer form returns a bit pattern the float form does not).
+template <int N, bool FAST>
+__device__ __forceinline__ void affine_codes(const float (&x)[N], float inv, float lo, int nmax,
+                                             float (&lf)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float v = inv * (x[i] - lo);
+    if constexpr (FAST)
+      lf[i] = __builtin_amdgcn_fmed3f((v + 12582912.0f) - 12582912.0f, 0.0f, (float)nmax);
+    else
+      lf[i] = (float)clampi(rint_magic(v), 0, nmax);
+  }
+}
+
 // Weighted affine fit x ~ scale * L + lo, L in [0, nmax]. Returns scale and -lo
 // (the "min" the containers store); L receives the codes.
+//
+// The candidate codes depend only on the candidate's inverse scale and the running
+// min, so the search keeps that pair for the best candidate and forms its codes
+// once at the end. A candidate takes the float form of the codes when, on every
+// lane of the wave, x is finite, inv is finite and inv * (min(x) - lo) > -2^22:
+// inv > 0 and rounding is monotonic, so every inv * (x_i - lo) then lies between
+// that bound and inv * (hi - lo), which is at most about nmax + 1.
 template <int N>
 __device__ __forceinline__ void fit_affine(const float (&x)[N], const float (&w)[N], int nmax,
                                            float rmin, float rdelta, int nstep, bool mad,
                                            bool strict_dead, float* scale_out, float* min_out,
                                            int (&L)[N]) {
   float hi = x[0], lo = x[0];
+  bool fin = isfinite(x[0]);
 #pragma unroll
   for (int i = 1; i < N; ++i) {
     hi = fmaxf(hi, x[i]);
     lo = fminf(lo, x[i]);
+    fin = fin && isfinite(x[i]);
   }
+  const float xmin = lo;
   lo = fminf(lo, 0.0f);
   float t[N];
   float sw = psum<N>(w);
@@ -54,23 +82,26 @@ __device__ __forceinline__ void fit_affine(const float (&x)[N], const float (&w)
 
   float inv = (float)nmax / (dead ? 1.0f : hi - lo);
   float scale = 1.0f / inv;
-#pragma unroll
-  for (int i = 0; i < N; ++i) L[i] = clampi(rint_magic(inv * (x[i] - lo)), 0, nmax);
-  float best = affine_err<N>(x, w, L, scale, lo, mad);
+  float lf[N];
+  affine_codes<N, false>(x, inv, lo, nmax, lf);
+  float best = affine_err<N>(x, w, lf, scale, lo, mad);
+  float best_inv = inv, best_lo = lo;  // the pair whose codes are the best so far
 
   for (int step = 0; step <= nstep; ++step) {
     float span = hi - lo;
     span = span > 0.0f ? span : 1.0f;
     float inv_c = ((rmin + rdelta * (float)step) + (float)nmax) / span;
-    int Lc[N];
+    const bool fast = fin && inv_c <= 3.40282347e38f && inv_c * (xmin - lo) > -4194304.0f;
+    if (__all(fast))
+      affine_codes<N, true>(x, inv_c, lo, nmax, lf);
+    else
+      affine_codes<N, false>(x, inv_c, lo, nmax, lf);
     float a[N], b[N], c[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      Lc[i] = clampi(rint_magic(inv_c * (x[i] - lo)), 0, nmax);
-      float lf = (float)Lc[i];
-      float wl = w[i] * lf;
+      float wl = w[i] * lf[i];
       a[i] = wl;
-      b[i] = wl * lf;
+      b[i] = wl * lf[i];
       c[i] = wl * x[i];
     }
     float sl = psum<N>(a);
@@ -84,20 +115,18 @@ __device__ __forceinline__ void fit_affine(const float (&x)[N], const float (&w)
       m_c = 0.0f;
       s_c = s_alt;
     }
-    float e_c = affine_err<N>(x, w, Lc, s_c, m_c, mad);
+    float e_c = affine_err<N>(x, w, lf, s_c, m_c, mad);
     if (det > 0.0f && e_c < best && !dead) {
-#pragma unroll
-      for (int i = 0; i < N; ++i) L[i] = Lc[i];
+      best_inv = inv_c;
+      best_lo = lo;
       best = e_c;
       scale = s_c;
       lo = m_c;
     }
   }
-  if (dead) {
-    scale = 0.0f;
 #pragma unroll
-    for (int i = 0; i < N; ++i) L[i] = 0;
-  }
+  for (int i = 0; i < N; ++i) L[i] = dead ? 0 : clampi(rint_magic(best_inv * (x[i] - best_lo)), 0, nmax);
+  if (dead) scale = 0.0f;
   *scale_out = scale;
   *min_out = -lo;
 }
