@@ -325,6 +325,14 @@ int cp_col_sq_sums(const void* x, int x_dtype, int64_t nrow, int64_t n, int64_t 
 int cp_col_log_rms(const void* x, int x_dtype, int64_t nrow, int64_t n, int64_t row_step,
                    double* out, void* ws, size_t ws_bytes, void* stream);
 
+/* Self-check of the device division shortcut the k-quant fits and the EF sweep use
+ * for divisions that share a divisor (a refined reciprocal formed once per divisor):
+ * n pseudo-random float32 pairs (seeded) inside its operand range, zero numerators
+ * and the range's end values, each compared bit for bit with the compiler's IEEE
+ * division. *mismatches receives the count (0 expected). Synchronizes the stream.
+ * No counterpart in the reference: it checks an implementation choice of this library. */
+int cp_check_division(int64_t n, uint64_t seed, int64_t* mismatches, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

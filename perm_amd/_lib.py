@@ -95,6 +95,7 @@ SIGNATURES = {
     "cp_col_sq_sums_batch": (_i32, [_col_p, _i32, _i64, _i32, _vp, _sz, _vp]),
     "cp_col_sq_sums": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "cp_col_log_rms": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
+    "cp_check_division": (_i32, [_i64, ctypes.c_uint64, _vp, _vp]),
 }
 
 

@@ -19,6 +19,36 @@ __device__ __forceinline__ int rint_magic(float v) {
   return (__float_as_int(s) & 0x7FFFFF) - 0x400000;
 }
 
+// IEEE float32 division with a shared divisor. The correctly rounded quotient the
+// compiler emits for a / b is: y = rcp(b') refined once, y1 = fma(fma(-b', y, 1), y, y);
+// q0 = a' * y1; two corrections q = fma(fma(-b', q, a'), y1, q); then v_div_fixup.
+// a' and b' are a and b after v_div_scale, which rescales only operands near the
+// ends of the exponent range, and v_div_fixup changes only special results. For a
+// and b inside div_box both are identities, so div_by(a, b, div_recip(b)) runs the
+// same operations on the same values and returns the same bits, while the refined
+// reciprocal y1 is formed once per divisor instead of once per quotient. A zero a
+// keeps its sign (a * y1). cp_check_division compares the two on the device.
+__device__ __forceinline__ bool div_box(float v) {
+  const float m = fabsf(v);
+  return m >= 0x1p-40f && m <= 0x1p40f;
+}
+
+__device__ __forceinline__ float div_recip(float b) {
+  const float y = __builtin_amdgcn_rcpf(b);
+  return __fmaf_rn(__fmaf_rn(-b, y, 1.0f), y, y);
+}
+
+// a / b for b in div_box and a == 0 or in div_box; y1 = div_recip(b).
+__device__ __forceinline__ float div_by(float a, float b, float y1) {
+  const float q0 = a * y1;
+  const float q1 = __fmaf_rn(__fmaf_rn(-b, q0, a), y1, q0);
+  const float q2 = __fmaf_rn(__fmaf_rn(-b, q1, a), y1, q1);
+  return a == 0.0f ? q0 : q2;
+}
+
+// Whether div_by gives a / b for this numerator (the divisor checked separately).
+__device__ __forceinline__ bool div_num_ok(float a) { return a == 0.0f || div_box(a); }
+
 __device__ __forceinline__ uint16_t half_bits(float v) {
   _Float16 h = (_Float16)v;  // v_cvt_f16_f32, round to nearest even
   return __builtin_bit_cast(uint16_t, h);

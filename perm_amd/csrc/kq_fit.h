@@ -90,7 +90,12 @@ __device__ __forceinline__ void fit_affine(const float (&x)[N], const float (&w)
   for (int step = 0; step <= nstep; ++step) {
     float span = hi - lo;
     span = span > 0.0f ? span : 1.0f;
-    float inv_c = ((rmin + rdelta * (float)step) + (float)nmax) / span;
+    const float num = (rmin + rdelta * (float)step) + (float)nmax;  // in div_box
+    float inv_c;
+    if (__all(div_box(span)))
+      inv_c = div_by(num, span, div_recip(span));
+    else
+      inv_c = num / span;
     const bool fast = fin && inv_c <= 3.40282347e38f && inv_c * (xmin - lo) > -4194304.0f;
     if (__all(fast))
       affine_codes<N, true>(x, inv_c, lo, nmax, lf);
@@ -108,12 +113,26 @@ __device__ __forceinline__ void fit_affine(const float (&x)[N], const float (&w)
     float sl2 = psum<N>(b);
     float sxl = psum<N>(c);
     float det = sw * sl2 - sl * sl;
-    float s_c = (sw * sxl - swx * sl) / det;
-    float m_c = (sl2 * swx - sl * sxl) / det;
-    float s_alt = sxl / sl2;
-    if (m_c > 0.0f) {
-      m_c = 0.0f;
-      s_c = s_alt;
+    const float ns = sw * sxl - swx * sl, nm = sl2 * swx - sl * sxl;
+    float s_c, m_c;
+    // both quotients share det; lanes that reject the candidate whatever its fit
+    // (det <= 0 or a dead block) do not hold the wave to the general division
+    if (__all(!(det > 0.0f) || dead || (div_box(det) && div_num_ok(ns) && div_num_ok(nm)))) {
+      const float y = div_recip(det);
+      s_c = div_by(ns, det, y);
+      m_c = div_by(nm, det, y);
+    } else {
+      s_c = ns / det;
+      m_c = nm / det;
+    }
+    // the scale without an offset is needed only where the fitted offset is positive;
+    // its division (about as costly as 18 subtractions) runs only when some lane needs it
+    if (__any(m_c > 0.0f)) {
+      float s_alt = sxl / sl2;
+      if (m_c > 0.0f) {
+        m_c = 0.0f;
+        s_c = s_alt;
+      }
     }
     float e_c = affine_err<N>(x, w, lf, s_c, m_c, mad);
     if (det > 0.0f && e_c < best && !dead) {
