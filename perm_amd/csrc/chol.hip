@@ -497,21 +497,57 @@ __global__ __launch_bounds__(256) void fact_prepare_kernel(const T* H, int n, in
   const int i0 = blockIdx.x * R;
   const int* o = order ? order + z * sO : nullptr;
   const T* h = H + z * sH;
-  for (int r = 0; r < R && i0 + r < n; ++r) {
+  const int rows_here = min(R, n - i0);
+  // stage the block's source rows: every load of a batch is issued before the LDS
+  // stores that consume it (16-byte loads when rows are 16-byte aligned)
+  constexpr int V = 16 / sizeof(T), B = 4;
+  const bool vec = (n % V) == 0 && (reinterpret_cast<uintptr_t>(h) % 16) == 0;
+  for (int r = 0; r < rows_here; ++r) {
     const int qi = o ? clamp_index(o[n - 1 - (i0 + r)], n) : n - 1 - (i0 + r);
-    for (int c = threadIdx.x; c < n; c += blockDim.x) rows[(int64_t)r * n + c] = h[(int64_t)qi * n + c];
+    const T* src = h + (int64_t)qi * n;
+    T* dst = rows + (int64_t)r * n;
+    if (vec) {
+      const uint4* s4 = reinterpret_cast<const uint4*>(src);
+      uint4* d4 = reinterpret_cast<uint4*>(dst);
+      const int nv = n / V;
+      for (int c0 = threadIdx.x; c0 < nv; c0 += B * blockDim.x) {
+        uint4 t[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+          const int c = c0 + b * blockDim.x;
+          if (c < nv) t[b] = s4[c];
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+          const int c = c0 + b * blockDim.x;
+          if (c < nv) d4[c] = t[b];
+        }
+      }
+    } else {
+      for (int c = threadIdx.x; c < n; c += blockDim.x) dst[c] = src[c];
+    }
   }
   __syncthreads();
   double* a = A + z * sA;
   const int jend = min(n, i0 + R);  // columns up to the block's last row
-  for (int j = threadIdx.x; j < jend; j += blockDim.x) {
-    const int qj = o ? clamp_index(o[n - 1 - j], n) : n - 1 - j;
-    for (int r = 0; r < R && i0 + r < n; ++r) {
-      const int i = i0 + r;
-      if (j <= i) {
-        double v = (double)rows[(int64_t)r * n + qj];
-        if (j == i) v = v + shift[z];
-        a[(int64_t)i * n + j] = v;
+  for (int j0 = threadIdx.x; j0 < jend; j0 += B * blockDim.x) {
+    int qj[B];  // the batch's column indices, loaded before any of them is used
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const int j = j0 + b * blockDim.x;
+      qj[b] = j < jend ? (o ? clamp_index(o[n - 1 - j], n) : n - 1 - j) : 0;
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const int j = j0 + b * blockDim.x;
+      if (j >= jend) continue;
+      for (int r = 0; r < rows_here; ++r) {
+        const int i = i0 + r;
+        if (j <= i) {
+          double v = (double)rows[(int64_t)r * n + qj[b]];
+          if (j == i) v = v + shift[z];
+          a[(int64_t)i * n + j] = v;
+        }
       }
     }
   }
@@ -743,11 +779,13 @@ __global__ __launch_bounds__(256) void act_order_kernel(const T* H, int n, int64
   }
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const double di = (double)(STAGE ? dg[i] : h[(int64_t)i * n + i]);
+  // compared in T: widening to double is monotonic, so the order is the same
+  const T di = STAGE ? dg[i] : h[(int64_t)i * n + i];
   const bool nan_i = di != di;
   int rank = 0;
+#pragma unroll 8
   for (int j = 0; j < n; ++j) {
-    const double dj = (double)(STAGE ? dg[j] : h[(int64_t)j * n + j]);
+    const T dj = STAGE ? dg[j] : h[(int64_t)j * n + j];
     const bool nan_j = dj != dj;
     rank += nan_i ? (!nan_j || j < i) : (dj > di || (dj == di && j < i));
   }
