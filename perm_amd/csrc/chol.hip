@@ -917,7 +917,14 @@ static int fact_attempt(const T* H, int64_t sH, int n, int batch, const int* ord
   const int64_t sA = (int64_t)nn;
   double *A = w.A, *X = w.X, *Tm = w.Tm;
   fill_i32_kernel<<<(batch + 255) / 256, 256, 0, st>>>(w.fail, batch, 0);
-  fill_kernel<<<1024, 256, 0, st>>>(X, (int64_t)nn * batch, 0.0);
+  // Every entry of X that is read is written first: the diagonal-block kernel stores
+  // whole 64 x 64 blocks (zeros above their diagonal), each doubling level stores its
+  // X21 blocks with beta = 0, and the output reads the lower triangle only. The one
+  // exception is a 128 x 128 GEMM tile, whose K range starts at its first row or
+  // column and so covers the zero 64-block above a diagonal pair. Those tiles need a
+  // K loop of at least 4096, i.e. a doubling level with s >= 4096, i.e. n > 4096; only
+  // there is X cleared first.
+  if (n > 4096) fill_kernel<<<1024, 256, 0, st>>>(X, (int64_t)nn * batch, 0.0);
   // the order check's marks live in the GEMM scratch Tm, which the split outer updates
   // and the doubling GEMMs later overwrite before reading
   fact_shift_kernel<T><<<batch, 256, 0, st>>>(H, n, sH, order, sO, w.damp_d, w.diag_tmp, w.shift,

@@ -596,3 +596,30 @@ def test_mfma_accumulate_mode_bounds(ef, tt):
     _say(f"mfma {tt}: codes agree {agree:.6f}, err rel diff {abs(e_gpu - e_ref) / e_ref:.2e}")
     assert agree >= (0.98 if tt == "Q5_K" else 0.99)
     assert abs(e_gpu - e_ref) / e_ref < 5e-3
+
+
+@pytest.mark.parametrize("n,batch", [(1000, 3), (3072, 2), (4096, 1)])
+def test_factor_reads_no_workspace_it_did_not_write(ef, n, batch):
+    """The factorization clears its inverse workspace only where a 128 x 128 GEMM tile can
+    read an entry nothing wrote (n > 4096). Below that every entry it reads is written
+    first, so a workspace full of NaN must give the same U, bit for bit, as a zeroed one."""
+    from perm_amd import _lib
+    lib = _lib.load()
+    _say(f"factor on a NaN workspace n={n} batch={batch}")
+    Hb = torch.stack([torch.from_numpy(correlated_hessian(n, 2 * n, seed=40 + z)) for z in range(batch)]
+                     ).float().cuda()
+    order = ef.act_order_dev(Hb)
+    nbytes = lib.cp_chol_ws_bytes(n, batch)
+    outs = []
+    for fill in (0.0, float("nan")):
+        ws = torch.full(((nbytes + 7) // 8,), fill, dtype=torch.float64, device="cuda")
+        U = torch.empty((batch, n, n), dtype=torch.float64, device="cuda")
+        used = (ctypes.c_double * batch)()
+        st = lib.cp_chol_inv_upper(_lib.ptr(Hb), 0, n, batch, _lib.ptr(order), 0.01, 6,
+                                   _lib.ptr(U), 1, ctypes.cast(used, ctypes.c_void_p), _lib.ptr(ws),
+                                   ws.numel() * 8, _lib.stream_ptr())
+        assert st == 0, lib.cp_last_error()
+        assert list(used) == [0.01] * batch
+        outs.append(U)
+    assert torch.isfinite(outs[1]).all()
+    assert torch.equal(outs[0], outs[1])
