@@ -909,6 +909,72 @@ __global__ __launch_bounds__(256) void ef_transpose_kernel(const EfDev* __restri
   __shared__ T tile[64][65];
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   const int* __restrict__ inv = t.inv;
+  const T* vsrc = WHICH == 0 ? (const T*)t.x : (const T*)t.WcurT;
+  const T* vdst = WHICH == 0 ? (const T*)t.WpT : (const T*)t.Wcur;
+  const bool vec = (nrow % 4) == 0 && (n % 4) == 0 &&
+                   ((reinterpret_cast<uintptr_t>(vsrc) | reinterpret_cast<uintptr_t>(vdst)) & 15) == 0;
+  if (vec) {
+    // 16-byte accesses on both sides: lane l holds 4 consecutive entries of one tile
+    // row (storage side: 4 columns of row r; visiting side: 4 rows of column v).
+    // Rows and columns are multiples of 4, so a quad is wholly inside or outside.
+    const int q = threadIdx.x & 15, g = threadIdx.x >> 4;  // quad within a line, line
+    if (WHICH == 0) {  // storage [nrow][n] -> visiting [n][nrow]
+      const float4* src = reinterpret_cast<const float4*>(t.x);
+      float4 v[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = r0 + g + 16 * k, c = c0 + 4 * q;
+        v[k] = (r < nrow && c < n) ? src[((int64_t)r * n + c) / 4] : make_float4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = g + 16 * k;
+        tile[i][4 * q] = v[k].x;
+        tile[i][4 * q + 1] = v[k].y;
+        tile[i][4 * q + 2] = v[k].z;
+        tile[i][4 * q + 3] = v[k].w;
+      }
+      __syncthreads();
+      float4* dst = reinterpret_cast<float4*>(t.WpT);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int j = g + 16 * k, c = c0 + j, r = r0 + 4 * q;
+        const int vv = c < n ? inv[c] : -1;
+        if (r < nrow && (unsigned)vv < (unsigned)n)
+          dst[((int64_t)vv * nrow + r) / 4] =
+              make_float4(tile[4 * q][j], tile[4 * q + 1][j], tile[4 * q + 2][j], tile[4 * q + 3][j]);
+      }
+    } else {  // visiting [n][nrow] -> storage [nrow][n]
+      const float4* src = reinterpret_cast<const float4*>(t.WcurT);
+      float4 v[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int j = g + 16 * k, c = c0 + j, r = r0 + 4 * q;
+        const int vv = c < n ? inv[c] : -1;
+        v[k] = (r < nrow && (unsigned)vv < (unsigned)n) ? src[((int64_t)vv * nrow + r) / 4]
+                                                         : make_float4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int j = g + 16 * k;
+        tile[4 * q][j] = v[k].x;
+        tile[4 * q + 1][j] = v[k].y;
+        tile[4 * q + 2][j] = v[k].z;
+        tile[4 * q + 3][j] = v[k].w;
+      }
+      __syncthreads();
+      float4* dst = reinterpret_cast<float4*>(t.Wcur);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = r0 + g + 16 * k, c = c0 + 4 * q;
+        const int i = g + 16 * k;
+        if (r < nrow && c < n)
+          dst[((int64_t)r * n + c) / 4] =
+              make_float4(tile[i][4 * q], tile[i][4 * q + 1], tile[i][4 * q + 2], tile[i][4 * q + 3]);
+      }
+    }
+    return;
+  }
   if (WHICH == 0) {  // storage -> visiting
     const float* src = t.x;
     float* dst = t.WpT;
