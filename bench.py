@@ -88,7 +88,8 @@ def last_sweep_kernel(lib):
 
 
 def measure_sweep_traffic(layers):
-    """HBM bytes per launch of the exact EF sweep (ef_sweep_rows_kernel): the mean over the
+    """HBM bytes per launch of the exact EF sweep (ef_sweep_rows_kernel / ef_sweep_pipe_kernel,
+    one launch per size class and iteration): the mean over the
     sequential pass's launches (two per size class) of FETCH_SIZE and WRITE_SIZE, each read
     in its own rocprofv3 --pmc child run of ``--workload sweep-pass`` and scaled by what the
     same counter reads for the 1 GiB copy of ``--workload copy`` (reads and writes exactly
@@ -104,8 +105,8 @@ def measure_sweep_traffic(layers):
                           os.path.join(tmp, f"copy_{counter}"))
         if len(copy) != 1 or copy[0][1] <= 0:
             raise RuntimeError(f"copy calibration: {len(copy)} dispatches of the copy kernel")
-        sweep = _pmc_child(counter, "ef_sweep_rows", ["--workload", "sweep-pass", "--layers",
-                                                      str(layers)],
+        sweep = _pmc_child(counter, "ef_sweep_(rows|pipe)", ["--workload", "sweep-pass",
+                                                             "--layers", str(layers)],
                            os.path.join(tmp, f"sweep_{counter}"))
         if len(sweep) != 6:
             raise RuntimeError(f"sweep pass: {len(sweep)} sweep dispatches, expected 6")
@@ -1137,7 +1138,8 @@ def main():
         flops_per_launch = ef_flops / sweep_launches
         ach = flops_per_launch / (avg_ms * 1e-3) / 1e12
         roof = {"kernel": ("ef_sweep_mfma_kernel" if mode == _lib.CP_EF_MFMA
-                           else "ef_sweep_rows_kernel"), "bound": "mfma", "achieved": ach,
+                           else " / ".join(sorted(set(kernels.values())))),
+                "bound": "mfma", "achieved": ach,
                 "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_FP32_TFLOPS,
                 "traffic": traffic, "avg_launch_ms": avg_ms,
                 "launches_per_step": sweep_launches}

@@ -1332,11 +1332,52 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     ++g.count;
     g.max_nb = nb > g.max_nb ? nb : g.max_nb;
   }
-  // row-stripe sweep items: 32-row stripes unless they would leave SIMDs with
-  // fewer than two waves (256 CUs x 4)
-  int64_t stripes32 = 0;
-  for (int i = 0; i < count; ++i) stripes32 += (ts[i].nrow + 31) / 32;
-  const int RS = stripes32 >= 2 * 1024 ? 32 : 16;
+  // Row stripes and waves per stripe (exact mode). A stripe of RS rows is one wave, or W
+  // waves (blocks in rounds): W doubles while the call's waves still fit the GPU's 2048
+  // two-per-SIMD slots and every tensor has a 64-column block per wave. 32-row stripes
+  // halve the in-block quantization chain per row, so they are taken whenever some W
+  // fills at least 1536 of those slots; otherwise 16-row stripes, which double the waves.
+  int64_t stripes32 = 0, stripes16 = 0;
+  int min_blocks = 1 << 30;
+  for (int i = 0; i < count; ++i) {
+    stripes32 += (ts[i].nrow + 31) / 32;
+    stripes16 += (ts[i].nrow + 15) / 16;
+    min_blocks = std::min(min_blocks, (int)(ts[i].n / 64));
+  }
+  const auto fill = [&](int64_t stripes) {
+    int w = 1;
+    while (w < 8 && stripes * 2 * w <= 2048 && 2 * w <= min_blocks) w *= 2;
+    return w;
+  };
+  int RS, waves = 1;
+  {
+    const int w32 = fill(stripes32);
+    if (stripes32 * w32 >= 1536) {
+      RS = 32;
+      waves = w32;
+    } else {
+      RS = 16;
+      waves = fill(stripes16);
+    }
+  }
+  if (mode == CP_EF_EXACT) {
+    if (const char* e = getenv("CP_EF_SWEEP_ROWS")) {  // tuning override: 16 or 32
+      const int r = atoi(e);
+      if (r == 16 || r == 32) {
+        RS = r;
+        waves = fill(r == 32 ? stripes32 : stripes16);
+      }
+    }
+    if (const char* e = getenv("CP_EF_SWEEP_WAVES")) {  // tuning override: 1, 2, 4 or 8
+      const int w = atoi(e);
+      if (w == 1 || w == 2 || w == 4 || w == 8) {
+        waves = w;  // the largest of 1, 2, 4, 8 within the request and every tensor's blocks
+        while (waves > 1 && waves > min_blocks) waves /= 2;
+      }
+    }
+  } else {
+    waves = 1;
+  }
   int64_t total_stripes = 0;
   bool same_n = true;
   for (int k = 0; k < count; ++k) {
@@ -1346,21 +1387,6 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     same_n = same_n && tk.n == tasks[by_len[0]].n;
   }
   if (total_stripes > ((int64_t)1 << 30)) return set_error(CP_ERR_SHAPE, "too many row stripes");
-  // waves per 16-row stripe: double while the stripes would still fill at most the
-  // GPU's 2048 two-per-SIMD wave slots and every tensor has a block per wave
-  int waves = 1;
-  if (mode == CP_EF_EXACT && RS == 16) {
-    int min_blocks = 1 << 30;
-    for (int i = 0; i < count; ++i) min_blocks = std::min(min_blocks, (int)(ts[i].n / 64));
-    while (waves < 8 && total_stripes * 2 * waves <= 2048 && 2 * waves <= min_blocks) waves *= 2;
-    if (const char* e = getenv("CP_EF_SWEEP_WAVES")) {  // tuning override: 1, 2, 4 or 8
-      const int w = atoi(e);
-      if (w == 1 || w == 2 || w == 4 || w == 8) {
-        waves = w;  // the largest of 1, 2, 4, 8 within the request and every tensor's blocks
-        while (waves > 1 && waves > min_blocks) waves /= 2;
-      }
-    }
-  }
   for (int c0 = 0; c0 < count; c0 += kTasksPerLaunch) {
     const int cn = count - c0 < kTasksPerLaunch ? count - c0 : kTasksPerLaunch;
     SweepBatch b;
@@ -1398,7 +1424,7 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     g_sweep_shape[2] = mode;
     if (mode == CP_EF_EXACT_VALU)
       ef_sweep_exact_kernel<BLK><<<dim3((unsigned)((max_rows + 255) / 256), (unsigned)count), 256, 0, st>>>(dtasks);
-    else if (mode == CP_EF_EXACT && RS == 32)
+    else if (mode == CP_EF_EXACT && waves == 1 && RS == 32)
       ef_sweep_rows_kernel<32><<<(unsigned)(8 * ((total_stripes + 7) / 8)), 64, 0, st>>>(
           dtasks, count, (int)total_stripes, same_n ? 1 : 0);
     else if (mode == CP_EF_EXACT && waves == 1)
@@ -1407,10 +1433,18 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     else if (mode == CP_EF_EXACT) {
       const unsigned g = (unsigned)(8 * ((total_stripes + 7) / 8));
       const int xr = same_n ? 1 : 0, ns = (int)total_stripes;
-      switch (waves) {
-        case 2: ef_sweep_pipe_kernel<16, 2><<<g, 128, 0, st>>>(dtasks, count, ns, xr); break;
-        case 4: ef_sweep_pipe_kernel<16, 4><<<g, 256, 0, st>>>(dtasks, count, ns, xr); break;
-        default: ef_sweep_pipe_kernel<16, 8><<<g, 512, 0, st>>>(dtasks, count, ns, xr); break;
+      if (RS == 32) {
+        switch (waves) {
+          case 2: ef_sweep_pipe_kernel<32, 2><<<g, 128, 0, st>>>(dtasks, count, ns, xr); break;
+          case 4: ef_sweep_pipe_kernel<32, 4><<<g, 256, 0, st>>>(dtasks, count, ns, xr); break;
+          default: ef_sweep_pipe_kernel<32, 8><<<g, 512, 0, st>>>(dtasks, count, ns, xr); break;
+        }
+      } else {
+        switch (waves) {
+          case 2: ef_sweep_pipe_kernel<16, 2><<<g, 128, 0, st>>>(dtasks, count, ns, xr); break;
+          case 4: ef_sweep_pipe_kernel<16, 4><<<g, 256, 0, st>>>(dtasks, count, ns, xr); break;
+          default: ef_sweep_pipe_kernel<16, 8><<<g, 512, 0, st>>>(dtasks, count, ns, xr); break;
+        }
       }
     }
     else

@@ -242,11 +242,14 @@ def test_sweep_bit_exact_iterations(ef, n_iter):
     assert np.array_equal(raw, want_raw)
 
 
+@pytest.mark.parametrize("rows", ["16", "32"])
 @pytest.mark.parametrize("waves", ["1", "2", "4", "8"])
-def test_sweep_waves_per_stripe_bit_exact(ef, waves, monkeypatch):
-    """Calls with few 16-row stripes spread each stripe over 2, 4 or 8 waves (blocks taken
-    in rounds, the round's blocks swept in order); every wave count gives the oracle's
-    bytes, including tensors with fewer blocks than waves and a partial last round."""
+def test_sweep_waves_per_stripe_bit_exact(ef, rows, waves, monkeypatch):
+    """Calls with few stripes spread each stripe over 2, 4 or 8 waves (blocks taken in
+    rounds, the round's blocks swept in order); every stripe height and wave count gives
+    the oracle's bytes, including tensors with fewer blocks than waves, a partial last
+    round and rows that do not fill the last stripe."""
+    monkeypatch.setenv("CP_EF_SWEEP_ROWS", rows)
     monkeypatch.setenv("CP_EF_SWEEP_WAVES", waves)
     specs = [(40, 1024, "Q2_K", 61), (17, 768, "Q4_K", 62), (33, 256, "Q6_K", 63)]
     for W, tt, qw, H, order, U in _oracle_items(specs):
@@ -258,15 +261,15 @@ def test_sweep_waves_per_stripe_bit_exact(ef, waves, monkeypatch):
         (raw, rec), = ef.ef_encode_dev([item], 2)
         assert np.array_equal(raw.cpu().numpy(), want_raw)
         assert np.array_equal(rec.cpu().numpy(), want_rec)
-        # the launch the library reports: 16-row stripes, the requested waves capped at the
-        # tensor's 64-column blocks (a power of two)
+        # the launch the library reports: the requested stripe height and waves, the waves
+        # capped at the tensor's 64-column blocks (a power of two)
         rs, wv = (ctypes.c_int * 1)(), (ctypes.c_int * 1)()
         mode = _lib.load().cp_ef_last_sweep(ctypes.cast(rs, ctypes.c_void_p),
                                             ctypes.cast(wv, ctypes.c_void_p))
         want_w = int(waves)
         while want_w > W.shape[1] // 64:
             want_w //= 2
-        assert (mode, rs[0], wv[0]) == (_lib.CP_EF_EXACT, 16, want_w)
+        assert (mode, rs[0], wv[0]) == (_lib.CP_EF_EXACT, int(rows), want_w)
 
 
 def _codes(tt, raw, nrow, n):
