@@ -131,15 +131,28 @@ __device__ __forceinline__ void sweep_block(const SweepTask& tk, int i1, int r, 
 // The block's diagonal U tile is kept compact in LDS: a tile row is read only
 // by the columns of its 16-column piece onwards, so row cb (piece p = cb / 16)
 // holds block columns 16 p .. 63 from tile_base(p) + (cb % 16) * (64 - 16 p):
-// 10 KB instead of 16. sg[k][rl] / sm[k][rl] hold the committed grid step and
-// offset of column k of the current quarter block (kGridCols columns) for the
-// stripe's row rl, staged in LDS so no global load sits on the column-to-column
-// chain.
+// 10 KB instead of 16. Within a row the columns are ordered by lane group of
+// the row-split sweep (tile_pos), so a group's entries are contiguous.
+// sg[k][rl] / sm[k][rl] hold the committed grid step and offset of column k of
+// the current quarter block (kGridCols columns) for the stripe's row rl, staged
+// in LDS so no global load sits on the column-to-column chain.
 constexpr int TILE_FLOATS = 16 * (64 + 48 + 32 + 16);
 constexpr int kGridCols = 16;  // block columns per staged part of the grid
 
 __device__ __forceinline__ constexpr int tile_base(int piece) {
   return piece == 0 ? 0 : piece == 1 ? 16 * 64 : piece == 2 ? 16 * (64 + 48) : 16 * (64 + 48 + 32);
+}
+
+// Position of block column c (16 p <= c < 64) in a tile row of piece p. In the
+// row-split sweep lane group g (of P = 64 / RS) holds columns g, g + P, g + 2P, ...,
+// register k holding column P k + g; a row of piece p stores, group after group,
+// the registers k >= kp = RS p / 4 (the columns c >= 16 p), so group g's entry
+// for register k sits at g (RS - kp) + k - kp.
+template <int RS>
+__device__ __forceinline__ constexpr int tile_pos(int c, int p) {
+  constexpr int P = 64 / RS;
+  const int kp = RS * p / 4;
+  return (c % P) * (RS - kp) + c / P - kp;
 }
 
 // Quantization of one column for one row (ef.py:199-208): code q on the
@@ -157,16 +170,21 @@ __device__ __forceinline__ void quantize_col(const SweepTask& tk, float t, float
   e = nz ? ev : 0.0f;
 }
 
-// In-block sweep with each row split over the wave: RS rows, 64 / RS lanes per
-// row, lane l holding elements RS * (l / RS) .. + RS - 1 of row l % RS of the
-// block (all 64 lanes work, where the one-lane-per-row queue above keeps
-// 64 - RS of them idle). Column cb's target lives in the lanes of group
-// cb / RS; it is broadcast to the row's other lanes with v_permlane16/32_swap,
-// every lane quantizes it (the same value, the same code and error), and every
-// lane applies the column's update to its own RS elements. Elements already
-// quantized receive updates too and are never read again; past the last
-// group's column only its remaining elements are updated. Each element still
-// receives its updates one at a time in ascending column order (ef.py:199-213).
+// In-block sweep with each row split over the wave: RS rows, P = 64 / RS lanes
+// per row, lane l of group g = l / RS holding elements g, g + P, g + 2P, ... of
+// row l % RS of the block in registers 0 .. RS - 1 (all 64 lanes work, where
+// the one-lane-per-row queue above keeps 64 - RS of them idle). Column cb's
+// target is register cb / P of group cb % P; it is broadcast to the row's other
+// lanes with v_permlane16/32_swap, every lane quantizes it (the same value, the
+// same code and error), and every lane applies the column's update to its
+// registers from (cb + 1) / P on, the first register that holds a later column
+// in some group. Interleaving the columns over the groups keeps every group's
+// remaining columns in the same registers, so a column updates about
+// (63 - cb) / P registers per lane, where contiguous column ranges per group
+// left the whole register set of the later groups to update. An element
+// already quantized that shares a register index with a later one receives
+// updates too and is never read again. Each element still receives its
+// updates one at a time in ascending column order (ef.py:199-213).
 template <int RS>
 __device__ __forceinline__ float bcast_group(float x, int own) {
   const unsigned v = __float_as_uint(x);
@@ -209,17 +227,19 @@ __device__ __forceinline__ void sweep_part_split(const SweepTask& tk, int i1, in
     float dl, ml, diag;
     float4 u[RS / 4];
   };
-  // row cb of the tile, indexed by block column (entries below 16 p are not stored;
-  // only lanes whose elements are finished read them); only the tile pieces a column
-  // updates (from jlo on) are read
-  const auto jlo_of = [](int cb) { return cb / RS == 64 / RS - 1 ? (cb % RS + 1) & ~3 : 0; };
+  // Column cb updates registers jlo_of(cb) .. RS - 1: from (cb + 1) / P, the first
+  // register holding a later column in some group, rounded down to a float4 of the
+  // tile row (never below kp, the row's first stored register).
+  constexpr int P = 64 / RS;
+  const auto jlo_of = [](int cb) { return ((cb + 1) / P) & ~3; };
   const auto read_ops = [&](int a, ColOps& c) {
-    const int cb = hb + a, p = cb / 16;
-    const float* row = tile + tile_base(p) + (cb % 16) * (64 - 16 * p) - 16 * p;
+    const int cb = hb + a, p = cb / 16, kp = RS * p / 4;
+    const float* row = tile + tile_base(p) + (cb % 16) * (64 - 16 * p);
     c.dl = sg[a][rl];
     c.ml = sm[a][rl];
-    c.diag = row[cb];
-    const float4* ul = reinterpret_cast<const float4*>(row + RS * g);
+    c.diag = row[tile_pos<RS>(cb, p)];
+    // the group's entry of register k is ul[k / 4] component k % 4 (k >= kp)
+    const float4* ul = reinterpret_cast<const float4*>(row + g * (RS - kp) - kp);
     const int jlo = jlo_of(cb);
 #pragma unroll
     for (int j4 = 0; j4 < RS / 4; ++j4)
@@ -232,7 +252,7 @@ __device__ __forceinline__ void sweep_part_split(const SweepTask& tk, int i1, in
     tl[k] = tl[k] - e * uk;
   };
   // The updates of a column are split in two. The register holding the next column's
-  // target (index (cb + 1) % RS in every lane group) takes column cb's update at once,
+  // target (index (cb + 1) / P in every lane group) takes column cb's update at once,
   // so the next quantization can start; the other registers take it in the next
   // column's scheduling region, where those independent subtractions fill the latency
   // of that column's divisions. Each register still receives the columns' updates in
@@ -244,7 +264,7 @@ __device__ __forceinline__ void sweep_part_split(const SweepTask& tk, int i1, in
 #pragma unroll
   for (int a = 0; a < kGridCols; ++a) {
     const int cb = hb + a;
-    const int own = cb / RS, i = cb % RS;
+    const int own = cb % P, i = cb / P;
     ColOps& cur = ops[a % 3];
     if (a + 1 < kGridCols) read_ops(a + 1, ops[(a + 1) % 3]);
     if (a > 0) {  // column cb - 1's remaining updates; register i took it already
@@ -265,7 +285,7 @@ __device__ __forceinline__ void sweep_part_split(const SweepTask& tk, int i1, in
     pw += nrow;
     pl += nrow;
     asm volatile("" : "+v"(pe), "+v"(pw), "+v"(pl));
-    if (cb + 1 < 64) apply(e, cur, (cb + 1) % RS);  // the next column's target first
+    if (cb + 1 < 64) apply(e, cur, (cb + 1) / P);  // the next column's target first
     e_prev = e;
     // one column's region at a time; the next column's operands are already in flight
     __builtin_amdgcn_sched_barrier(0);
@@ -273,7 +293,7 @@ __device__ __forceinline__ void sweep_part_split(const SweepTask& tk, int i1, in
   {  // the part's last column: its remaining updates before the next part's grid
     const int cb = hb + kGridCols - 1;
     const ColOps& last = ops[(kGridCols - 1) % 3];
-    const int jlo = jlo_of(cb), nx = (cb + 1) % RS;
+    const int jlo = jlo_of(cb), nx = (cb + 1) / P;
 #pragma unroll
     for (int k = 0; k < RS; ++k)
       if (k >= jlo && (cb + 1 >= 64 || k != nx)) apply(e_prev, last, k);
@@ -556,8 +576,8 @@ __device__ __forceinline__ void cross_range(const SweepTask& tk, int i1, int rr,
 }
 
 // The block's own 64 columns for the stripe's rows, after every earlier column's
-// updates: the targets move to the row-split layout (lane l: elements RS * (l / RS)
-// .. + RS - 1 of row l % RS), the compact diagonal tile and the block's committed grid
+// updates: the targets move to the row-split layout (lane l: elements l / RS,
+// l / RS + P, ... of row l % RS, P = 64 / RS), the compact diagonal tile and the block's committed grid
 // come in through one round trip, and the four quarter blocks are swept in order.
 template <int RS>
 __device__ __forceinline__ void sweep_block_rows(const SweepTask& tk, int i1, int rr, int l,
@@ -574,7 +594,7 @@ __device__ __forceinline__ void sweep_block_rows(const SweepTask& tk, int i1, in
   WaveSync()();
   float tl[RS];
 #pragma unroll
-  for (int k = 0; k < RS; ++k) tl[k] = st[rl][part * RS + k];
+  for (int k = 0; k < RS; ++k) tl[k] = st[rl][(64 / RS) * k + part];
   WaveSync()();
   // the block's grid steps / offsets (both halves into registers) and the compact
   // diagonal tile share one round trip to memory; lane l fills column 16 p + l of the
@@ -591,7 +611,7 @@ __device__ __forceinline__ void sweep_block_rows(const SweepTask& tk, int i1, in
       u[a] = in ? ld_lane(tk.U, (int64_t)(i1 + 16 * p + a) * n + i1 + 16 * p + l) : 0.0f;
     if (in) {
 #pragma unroll
-      for (int a = 0; a < 16; ++a) s.tile[tile_base(p) + a * (64 - 16 * p) + l] = u[a];
+      for (int a = 0; a < 16; ++a) s.tile[tile_base(p) + a * (64 - 16 * p) + tile_pos<RS>(16 * p + l, p)] = u[a];
     }
   }
   sweep_quarters<RS>(tk, i1, rr, l, tl, s.tile, gp, sg, sm, WaveSync());
@@ -701,10 +721,10 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
 #pragma unroll
     for (int v = 0; v < NV; ++v) st[StripeLayout<RS>::row(v, l)][StripeLayout<RS>::col(v, l)] = t[v];
     __syncthreads();
-    // lane l: elements RS * (l / RS) .. + RS - 1 of row l % RS
+    // lane l: elements l / RS, l / RS + P, ... of row l % RS (P = 64 / RS)
     float tl[RS];
 #pragma unroll
-    for (int k = 0; k < RS; ++k) tl[k] = trow[part * RS + k];
+    for (int k = 0; k < RS; ++k) tl[k] = trow[(64 / RS) * k + part];
     __syncthreads();
     // the block's grid steps / offsets (both halves into registers) and the
     // compact diagonal tile share one round trip to memory; lane l fills
@@ -721,7 +741,7 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
         u[a] = in ? ld_lane(tk.U, (int64_t)(i1 + 16 * p + a) * n + i1 + 16 * p + l) : 0.0f;
       if (in) {
 #pragma unroll
-        for (int a = 0; a < 16; ++a) lds[tile_base(p) + a * (64 - 16 * p) + l] = u[a];
+        for (int a = 0; a < 16; ++a) lds[tile_base(p) + a * (64 - 16 * p) + tile_pos<RS>(16 * p + l, p)] = u[a];
       }
     }
     sweep_quarters<RS>(tk, i1, rr, l, tl, lds, gp, sg, sm, [] { __syncthreads(); });

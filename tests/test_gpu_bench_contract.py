@@ -31,7 +31,14 @@ def test_ef_line(monkeypatch, capsys):
     roof = r["roofline"]
     assert {"bound", "achieved", "peak", "unit", "frac", "traffic"} <= set(roof)
     assert roof["bound"] in ("hbm", "mfma") and 0 < roof["frac"] < 1
-    assert roof["traffic"] is None  # quoted for the 28-layer workload only
+    # measured by the bench's own counter runs of the same (2-layer) workload, or null
+    # when they could not run; every sweep kernel of the pass is counted
+    if roof["traffic"] is not None:
+        d = roof["traffic_detail"]
+        assert roof["traffic"] > 0
+        assert len(d["fetch_bytes_per_launch"]) == len(d["write_bytes_per_launch"]) == 6
+    else:
+        assert roof.get("traffic_detail") is None or "error" in roof["traffic_detail"]
 
 
 def test_perm_search_line(monkeypatch, capsys):
