@@ -136,6 +136,7 @@ __device__ __forceinline__ void sweep_block(const SweepTask& tk, int i1, int r, 
 // sg[k][rl] / sm[k][rl] hold the committed grid step and offset of column k of
 // the current quarter block (kGridCols columns) for the stripe's row rl, staged
 // in LDS so no global load sits on the column-to-column chain.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int TILE_FLOATS = 16 * (64 + 48 + 32 + 16);
 constexpr int kGridCols = 16;  // block columns per staged part of the grid
 
@@ -225,7 +226,7 @@ __device__ __forceinline__ void sweep_part_split(const SweepTask& tk, int i1, in
   // next column's quantization.
   struct ColOps {
     float dl, ml, diag;
-    float4 u[RS / 4];
+    f32x4 u[RS / 4];
   };
   // Column cb updates registers jlo_of(cb) .. RS - 1: from (cb + 1) / P, the first
   // register holding a later column in some group, rounded down to a float4 of the
@@ -238,8 +239,13 @@ __device__ __forceinline__ void sweep_part_split(const SweepTask& tk, int i1, in
     c.dl = sg[a][rl];
     c.ml = sm[a][rl];
     c.diag = row[tile_pos<RS>(cb, p)];
-    // the group's entry of register k is ul[k / 4] component k % 4 (k >= kp)
-    const float4* ul = reinterpret_cast<const float4*>(row + g * (RS - kp) - kp);
+    // the group's entry of register k is ul[k / 4] component k % 4 (k >= kp). The
+    // address is formed in 4-float units (the row start, kp and RS - kp are multiples
+    // of 4 floats) and read as a native 4-vector (HIP's float4 struct is copied element
+    // by element, which left two-dword reads and an address add per pair), so each read
+    // is one 16-byte LDS load with an immediate offset.
+    const f32x4* ul = reinterpret_cast<const f32x4*>(__builtin_assume_aligned(tile, 16)) +
+                      (tile_base(p) + (cb % 16) * (64 - 16 * p) - kp) / 4 + g * ((RS - kp) / 4);
     const int jlo = jlo_of(cb);
 #pragma unroll
     for (int j4 = 0; j4 < RS / 4; ++j4)
@@ -247,7 +253,7 @@ __device__ __forceinline__ void sweep_part_split(const SweepTask& tk, int i1, in
   };
   // Column cb's update of register k of every lane group, t = fl(t - fl(e * u)).
   const auto apply = [&](float e, const ColOps& c, int k) {
-    const float4 u = c.u[k / 4];
+    const f32x4 u = c.u[k / 4];
     const float uk = (k % 4 == 0) ? u.x : (k % 4 == 1) ? u.y : (k % 4 == 2) ? u.z : u.w;
     tl[k] = tl[k] - e * uk;
   };
