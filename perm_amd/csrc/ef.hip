@@ -526,21 +526,26 @@ __device__ __forceinline__ StripeVec<RS> stage_block(const SweepTask& tk, int i1
 }
 
 // Cross-block updates of the block at i1 from visiting columns j0 .. j1 - 1 (multiples of
-// 64), in ascending column order: t = fl(t - fl(e_jj * U[jj][c])). E and U of eight columns
-// per group, two groups in flight (static buffers a / b, no copies); per column, the MFMA
-// for the next column is issued before the subtractions that consume the current one,
-// fenced by scheduling barriers so the two products stay in separate registers and each
-// MFMA runs under the VALU work of the column before it.
-template <int RS>
+// 64), in ascending column order: t = fl(t - fl(e_jj * U[jj][c])). E and U come in
+// groups of G columns through a ring of 16 / G static register buffers, each group
+// loaded 16 / G - 1 groups ahead (16 - G columns before its first use; the ring holds 16
+// columns of E and U whatever G); per column, the MFMA for the next column is issued
+// before the subtractions that consume the current one, fenced by scheduling barriers so
+// the two products stay in separate registers and each MFMA runs under the VALU work of
+// the column before it.
+constexpr int kSweepGroup = 8;  // cross-block columns per E / U load group
+
+template <int RS, int G = kSweepGroup>
 __device__ __forceinline__ void cross_range(const SweepTask& tk, int i1, int rr, int l,
                                             StripeVec<RS>& t, int j0, int j1) {
-  constexpr int G = 8, NV = StripeLayout<RS>::NV;
+  constexpr int NB = 16 / G, NV = StripeLayout<RS>::NV;
+  static_assert(G * NB == 16 && G % 2 == 0, "16 columns in flight, columns in pairs");
   const int nrow = tk.nrow, n = tk.n;
-  float ea[G], ua[G], eb[G], ub[G];
+  float e[NB][G], u[NB][G];
   // buffer loads rebased per group: the lane's byte offset stays in a VGPR and the
   // column's offset is scalar, so no per-lane address arithmetic runs per column
   const int eoff = 4 * rr, uoff = 4 * l;
-  auto load = [&](int g, float (&e)[G], float (&u)[G]) {
+  auto load = [&](int g, float (&eg)[G], float (&ug)[G]) {
     const int jg = j0 + g * G;
     const auto re = __builtin_amdgcn_make_buffer_rsrc((void*)(tk.E + (int64_t)jg * nrow), 0,
                                                       0x7fffffff, 0x00020000);
@@ -548,36 +553,43 @@ __device__ __forceinline__ void cross_range(const SweepTask& tk, int i1, int rr,
                                                       0x7fffffff, 0x00020000);
 #pragma unroll
     for (int q = 0; q < G; ++q) {
-      e[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(re, eoff, 4 * q * nrow, 0));
-      u[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ru, uoff, 4 * q * n, 0));
+      eg[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(re, eoff, 4 * q * nrow, 0));
+      ug[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ru, uoff, 4 * q * n, 0));
     }
   };
   StripeVec<RS> P0, P1;
-  auto group = [&](const float (&e)[G], const float (&u)[G], const float (&en)[G],
+  auto group = [&](const float (&eg)[G], const float (&ug)[G], const float (&en)[G],
                    const float (&un)[G]) {
 #pragma unroll
     for (int q = 0; q < G; q += 2) {
       // P0 holds column q of the group on entry; the last group's final product is unused
-      P1 = stripe_product<RS>(e[q + 1], u[q + 1]);
+      P1 = stripe_product<RS>(eg[q + 1], ug[q + 1]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int v = 0; v < NV; ++v) t[v] = t[v] - P0[v];
       __builtin_amdgcn_sched_barrier(0);
-      P0 = stripe_product<RS>(q + 2 < G ? e[q + 2] : en[0], q + 2 < G ? u[q + 2] : un[0]);
+      P0 = stripe_product<RS>(q + 2 < G ? eg[q + 2] : en[0], q + 2 < G ? ug[q + 2] : un[0]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int v = 0; v < NV; ++v) t[v] = t[v] - P1[v];
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  const int groups = (j1 - j0) / G;  // even: j1 - j0 is a multiple of 64
-  load(0, ea, ua);
-  P0 = stripe_product<RS>(ea[0], ua[0]);
-  for (int g = 0; g < groups; g += 2) {
-    load(g + 1, eb, ub);
-    group(ea, ua, eb, ub);
-    load(g + 2 < groups ? g + 2 : g + 1, ea, ua);  // past the end: a valid group, unused
-    group(eb, ub, ea, ua);
+  const int groups = (j1 - j0) / G;  // a multiple of NB: j1 - j0 is a multiple of 64
+  // past the end: a valid group, loaded and unused
+  const auto clampg = [groups](int h) { return h < groups ? h : groups - 1; };
+#pragma unroll
+  for (int b = 0; b + 1 < NB; ++b) load(clampg(b), e[b], u[b]);
+  P0 = stripe_product<RS>(e[0][0], u[0][0]);
+  for (int g = 0; g < groups; g += NB) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      // the buffer group b - 1 has just consumed takes group g + b + NB - 1 (for b = 0 the
+      // last group of this window, always valid: groups is a multiple of NB)
+      const int h = g + b + NB - 1;
+      load(b == 0 ? h : clampg(h), e[(b + NB - 1) % NB], u[(b + NB - 1) % NB]);
+      group(e[b], u[b], e[(b + 1) % NB], u[(b + 1) % NB]);
+    }
   }
 }
 
@@ -626,8 +638,7 @@ __device__ __forceinline__ void sweep_block_rows(const SweepTask& tk, int i1, in
 template <int RS>
 __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* __restrict__ tasks, int count,
                                                             int total, int xcd_runs) {
-  constexpr int B = 64, G = 8, NV = StripeLayout<RS>::NV, CPP = B * RS / 64;
-  typedef float fv __attribute__((ext_vector_type(NV)));
+  constexpr int B = 64, NV = StripeLayout<RS>::NV, CPP = B * RS / 64;
   int ti;
   const int stripe = sweep_item(tasks, count, total, xcd_runs != 0, &ti);
   if (stripe < 0) return;
@@ -655,13 +666,6 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
   float (*sm)[RS] = reinterpret_cast<float (*)[RS]>(&sm_[0][0]);
   float (*st)[B + 1] = reinterpret_cast<float (*)[B + 1]>(lds);
   float* trow = st[rl];
-  auto mfma = [](float a, float b) -> fv {
-    const fv z = {};
-    if constexpr (RS == 32)
-      return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, z, 0, 0, 0);
-    else
-      return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, z, 0, 0, 0);
-  };
   for (int i1 = 0; i1 < n; i1 += B) {
     // targets: lane l stages row rl, columns part * CPP .. + CPP - 1, then
     // moves to the MFMA layout
@@ -670,59 +674,10 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
     for (int k = 0; k < CPP; ++k)
       trow[part * CPP + k] = ld_lane(tk.WpT, (int64_t)(i1 + part * CPP + k) * nrow + rr);
     __syncthreads();
-    fv t;
+    StripeVec<RS> t;
 #pragma unroll
     for (int v = 0; v < NV; ++v) t[v] = st[StripeLayout<RS>::row(v, l)][StripeLayout<RS>::col(v, l)];
-    if (i1 > 0) {
-      // E and U of eight columns per group, two groups in flight (static
-      // buffers a / b, no copies); per column, the MFMA for the next column is
-      // issued before the subtractions that consume the current one, fenced
-      // by scheduling barriers so the two products stay in separate registers
-      // and each MFMA runs under the VALU work of the column before it
-      float ea[G], ua[G], eb[G], ub[G];
-      // buffer loads rebased per group: the lane's byte offset stays in a VGPR and the
-      // column's offset is scalar, so no per-lane address arithmetic runs per column
-      const int eoff = 4 * rr, uoff = 4 * l;
-      auto load = [&](int g, float (&e)[G], float (&u)[G]) {
-        const auto re = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(tk.E + (int64_t)g * G * nrow), 0, 0x7fffffff, 0x00020000);
-        const auto ru = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(tk.U + (int64_t)g * G * n + i1), 0, 0x7fffffff, 0x00020000);
-#pragma unroll
-        for (int q = 0; q < G; ++q) {
-          e[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(re, eoff, 4 * q * nrow, 0));
-          u[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ru, uoff, 4 * q * n, 0));
-        }
-      };
-      fv P0, P1;
-      auto group = [&](const float (&e)[G], const float (&u)[G], const float (&en)[G],
-                       const float (&un)[G]) {
-#pragma unroll
-        for (int q = 0; q < G; q += 2) {
-          // P0 holds column q of the group on entry; the last group's final
-          // product is unused
-          P1 = mfma(e[q + 1], u[q + 1]);
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int v = 0; v < NV; ++v) t[v] = t[v] - P0[v];
-          __builtin_amdgcn_sched_barrier(0);
-          P0 = mfma(q + 2 < G ? e[q + 2] : en[0], q + 2 < G ? u[q + 2] : un[0]);
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int v = 0; v < NV; ++v) t[v] = t[v] - P1[v];
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      };
-      const int groups = i1 / G;  // even: i1 is a multiple of 64
-      load(0, ea, ua);
-      P0 = mfma(ea[0], ua[0]);
-      for (int g = 0; g < groups; g += 2) {
-        load(g + 1, eb, ub);
-        group(ea, ua, eb, ub);
-        load(g + 2 < groups ? g + 2 : g + 1, ea, ua);  // past the end: a valid group, unused
-        group(eb, ub, ea, ua);
-      }
-    }
+    if (i1 > 0) cross_range<RS>(tk, i1, rr, l, t, 0, i1);
     __syncthreads();
 #pragma unroll
     for (int v = 0; v < NV; ++v) st[StripeLayout<RS>::row(v, l)][StripeLayout<RS>::col(v, l)] = t[v];
