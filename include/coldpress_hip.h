@@ -325,8 +325,8 @@ int cp_col_sq_sums(const void* x, int x_dtype, int64_t nrow, int64_t n, int64_t 
 int cp_col_log_rms(const void* x, int x_dtype, int64_t nrow, int64_t n, int64_t row_step,
                    double* out, void* ws, size_t ws_bytes, void* stream);
 
-/* Self-check of the device division shortcut the k-quant fits and the EF sweep use
- * for divisions that share a divisor (a refined reciprocal formed once per divisor):
+/* Self-check of the device division shortcut the k-quant affine fits use for
+ * divisions that share a divisor (a refined reciprocal formed once per divisor):
  * n pseudo-random float32 pairs (seeded) inside its operand range, zero numerators
  * and the range's end values, each compared bit for bit with the compiler's IEEE
  * division. *mismatches receives the count (0 expected). Synchronizes the stream.
