@@ -709,15 +709,31 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
   }
 }
 
+// Wait (bounded) until *done > c, the count of the stripe's blocks complete so far, and
+// return that count. The producing wave releases the count at workgroup scope after
+// its error stores, so the acquire here orders this wave's later reads of those errors.
+// The bound (about 30 ms of sleeps) is far above any wait the schedule makes; past it
+// the wave goes on with one more block rather than spin for ever.
+__device__ __forceinline__ int wait_blocks(int* done, int c) {
+  int v = __hip_atomic_load(done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  for (int spins = 0; v <= c && spins < (1 << 16); ++spins) {
+    __builtin_amdgcn_s_sleep(8);
+    v = __hip_atomic_load(done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  return __builtin_amdgcn_readfirstlane(v > c ? v : c + 1);
+}
+
 // W waves per stripe, for calls whose stripes alone would leave most SIMDs idle (few
-// rows, long rows). Wave w owns blocks w, w + W, w + 2W, ...; the blocks are taken in
-// rounds of W. In a round every wave first applies the updates of all columns of
-// earlier rounds to its block (the bulk of the work, in parallel); then the round's
-// blocks are swept in order: wave p sweeps its block while the later waves wait at
-// the barrier, and after it they apply its 64 columns. Every element still receives its
+// rows, long rows). Wave w owns blocks w, w + W, w + 2W, ... For each of its blocks a
+// wave applies the updates of every earlier block's columns in ascending order, taking
+// at each step all the leading blocks that are complete, and waits only when the next
+// block it needs is still being swept; then it sweeps its own block and publishes the
+// new count of complete blocks. Blocks complete in order (block b is swept only after
+// blocks 0 .. b - 1 are applied to it), so one counter in LDS describes them, and every
+// wait ends: block c depends only on blocks below c. Every element still receives its
 // updates one at a time in ascending column order, as in the one-wave kernel. The
 // errors a wave writes reach the others through global memory, ordered by the
-// workgroup barrier.
+// counter's release and acquire.
 template <int RS, int W>
 __global__ __launch_bounds__(64 * W, 2) void ef_sweep_pipe_kernel(const SweepTask* __restrict__ tasks,
                                                                   int count, int total, int xcd_runs) {
@@ -732,28 +748,21 @@ __global__ __launch_bounds__(64 * W, 2) void ef_sweep_pipe_kernel(const SweepTas
   const int rr = row0 + rl < tk.nrow ? row0 + rl : tk.nrow - 1;
   if constexpr (RS == 16) asm volatile("" ::: "v175");
   __shared__ __align__(16) StripeLds s_all[W];
+  __shared__ int done;  // the stripe's blocks complete so far
   StripeLds& s = s_all[wv];
+  if (threadIdx.x == 0) done = 0;
+  __syncthreads();
   const int nblocks = tk.n / 64;
-  for (int r0 = 0; r0 < nblocks; r0 += W) {
-    const int b = r0 + wv;
-    const bool active = b < nblocks;
+  for (int b = wv; b < nblocks; b += W) {
     const int i1 = b * 64;
-    StripeVec<RS> t = {};
-    if (active) {
-      t = stage_block<RS>(tk, i1, rr, l, s);
-      if (r0 > 0) cross_range<RS>(tk, i1, rr, l, t, 0, r0 * 64);
+    StripeVec<RS> t = stage_block<RS>(tk, i1, rr, l, s);
+    for (int c = 0; c < b;) {
+      const int avail = min(wait_blocks(&done, c), b);
+      cross_range<RS>(tk, i1, rr, l, t, c * 64, avail * 64);
+      c = avail;
     }
-    // the round's W barriers: barrier p follows wave p's sweep of its block; wave wv
-    // takes the blocks of waves 0 .. wv - 1 after their barriers, then sweeps its own
-    // block, then passes the remaining barriers (the same W barriers for every wave)
-#pragma unroll 1
-    for (int p = 0; p < wv; ++p) {
-      __syncthreads();
-      if (active) cross_range<RS>(tk, i1, rr, l, t, (r0 + p) * 64, (r0 + p) * 64 + 64);
-    }
-    if (active) sweep_block_rows<RS>(tk, i1, rr, l, t, s);
-#pragma unroll 1
-    for (int p = wv; p < W; ++p) __syncthreads();
+    sweep_block_rows<RS>(tk, i1, rr, l, t, s);
+    __hip_atomic_store(&done, b + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 }
 
