@@ -990,8 +990,10 @@ def config_main(args):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=3)
-    ap.add_argument("--warmup", type=int, default=1)
+    # two warm-up steps: the first step of a process runs its first Hessian and EF
+    # launches (slower, whichever size class it hits) and the second still settles
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--layers", type=int, default=28,
                     help="decoder layers (28 = the full workload; fewer only for quick checks)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
