@@ -35,7 +35,8 @@ enum cp_status {
   CP_ERR_ARG = -5,       /* null pointer / invalid argument                      */
   CP_ERR_ALIGN = -6,     /* pointer alignment requirement violated               */
   CP_ERR_WORKSPACE = -7, /* workspace too small                                  */
-  CP_ERR_INDEX = -8      /* an index argument out of range / not a permutation    */
+  CP_ERR_INDEX = -8,     /* an index argument out of range / not a permutation    */
+  CP_ERR_TIMEOUT = -9    /* a device-side bounded wait gave up (results invalid)  */
 };
 
 enum cp_ttype { CP_Q8_0 = 8, CP_Q2_K = 10, CP_Q3_K = 11, CP_Q4_K = 12, CP_Q5_K = 13, CP_Q6_K = 14 };
@@ -132,7 +133,10 @@ typedef struct cp_ef_tensor {
   float* recon;          /* out: [nrow, n] decoded weights, or NULL                     */
 } cp_ef_tensor;
 
-/* Workspace bytes cp_ef_encode_batch needs for these tensors. */
+/* Workspace bytes cp_ef_encode_batch needs for these tensors. The first 4 bytes of the
+ * workspace are the call's status word (int32, cleared by the call before its sweep):
+ * bit 0 set means a sweep wave gave up a bounded wait and the call's bytes are not
+ * valid. cp_ef_read_status reads it. */
 size_t cp_ef_ws_bytes(const cp_ef_tensor* tensors, int count);
 
 /* GPTQ error feedback into committed k-quant grids for ``count`` independent
@@ -170,6 +174,20 @@ int cp_ef_encode_noalloc(int ttype, const float* x, int64_t nrow, int64_t n, con
 /* Bytes of the static workspace behind cp_ef_encode_noalloc. */
 size_t cp_ef_noalloc_max_ws_bytes(void);
 
+/* Status of the EF call that last used workspace ``ws`` (NULL: the static workspace of
+ * cp_ef_encode_noalloc on the current device), after the work queued on ``stream``:
+ * CP_OK, or CP_ERR_TIMEOUT when one of the call's multi-wave sweep waves waited for an
+ * earlier block of its stripe past the spin bound (cp_ef_wait_limit) and went on without
+ * it, so the call's raw and recon are not valid. Synchronizes ``stream``. No counterpart
+ * in the reference, whose sweep is one sequential loop. */
+int cp_ef_read_status(const void* ws, void* stream);
+
+/* Per-thread spin bound of the multi-wave sweep's waits for this thread's later EF calls:
+ * ``spins`` sleeps of about 512 clocks each; negative restores the default 65536 (about
+ * 14 ms at 2.4 GHz, far above a block's sweep time). A small bound makes waves give up
+ * early (a test of the status path); every kernel still ends. */
+void cp_ef_wait_limit(int spins);
+
 /* Per-thread switch for phase timing of EF calls (hipEvents recorded on the
  * call's stream; no synchronization inside the call). No counterpart in the
  * reference, which times whole tensors with time.time() (coldpress/ef.py:277, 304). */
@@ -192,16 +210,33 @@ int cp_ef_last_sweep(int* rows_per_stripe, int* waves);
 /* H [d, d] float32 += X^T X for X [N, d] row-major (x_dtype 0 = float32,
  * 1 = bfloat16 with d % 8 == 0). Float32 accumulation on MFMA. Replaces the
  * forward hook's ``acc += (x.float().T @ x)`` (coldpress/hessians.py:142-152),
- * with the accumulator kept on the device. The summation order over rows is
- * not fixed (split-K partials are added with float32 atomics). */
+ * with the accumulator kept on the device. Reproducible: the summation order
+ * over rows is fixed by the shapes alone (row splits are summed in split order,
+ * then added to H), so the same X and H give the same result bit for bit. For
+ * bf16 X the result is symmetric and H's upper triangle is not read (the lower
+ * triangle is mirrored into it). The workspace the row splits need is taken
+ * stream-ordered (hipMallocAsync / hipFreeAsync on ``stream``); use
+ * cp_hess_accum_batch_ws to pass one instead. */
 int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, float* H, void* stream);
 
 /* H[z] += X[z]^T X[z] for ``count`` jobs of one shape (host arrays of device pointers),
  * bf16 jobs in as few launches as fit (224 per launch): many Hessians share one grid, so
  * small d needs fewer row splits. The batched form of cp_hess_accum (the hook of
- * coldpress/hessians.py:137-154 for every hooked module of a forward pass). */
+ * coldpress/hessians.py:137-154 for every hooked module of a forward pass); the same
+ * summation order per job as cp_hess_accum with count = 1 only when the launch plans
+ * agree, so compare a job with itself, not across batch sizes. */
 int cp_hess_accum_batch(const void* const* X, float* const* H, int count, int x_dtype,
                         int64_t N, int64_t d, void* stream);
+
+/* Workspace bytes cp_hess_accum_batch_ws needs for these jobs (0 when every launch
+ * runs as one row split). */
+size_t cp_hess_ws_bytes(int count, int x_dtype, int64_t N, int64_t d);
+
+/* cp_hess_accum_batch with a caller workspace (device, 16-byte aligned, at least
+ * cp_hess_ws_bytes bytes; CP_ERR_WORKSPACE otherwise): the row splits' partial tiles.
+ * Its contents need no clearing. Same results as cp_hess_accum_batch, bit for bit. */
+int cp_hess_accum_batch_ws(const void* const* X, float* const* H, int count, int x_dtype,
+                           int64_t N, int64_t d, void* ws, size_t ws_bytes, void* stream);
 
 /* ---- Hessian storage (coldpress/hessians.py:163-243) ---- */
 

@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcoldpres
 
 CP_OK, CP_ERR_SHAPE, CP_ERR_TTYPE, CP_ERR_NOT_PD = 0, -1, -2, -3
 CP_ERR_HIP, CP_ERR_ARG, CP_ERR_ALIGN, CP_ERR_WORKSPACE, CP_ERR_INDEX = -4, -5, -6, -7, -8
+CP_ERR_TIMEOUT = -9
 
 TTYPE = {"Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
 
@@ -73,8 +74,12 @@ SIGNATURES = {
     "cp_ef_encode_noalloc": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _vp, _i32, _vp, _vp,
                                     _vp]),
     "cp_ef_noalloc_max_ws_bytes": (_sz, []),
+    "cp_ef_read_status": (_i32, [_vp, _vp]),
+    "cp_ef_wait_limit": (None, [_i32]),
     "cp_hess_accum": (_i32, [_vp, _i32, _i64, _i64, _vp, _vp]),
     "cp_hess_accum_batch": (_i32, [_vp, _vp, _i32, _i32, _i64, _i64, _vp]),
+    "cp_hess_ws_bytes": (_sz, [_i32, _i32, _i64, _i64]),
+    "cp_hess_accum_batch_ws": (_i32, [_vp, _vp, _i32, _i32, _i64, _i64, _vp, _sz, _vp]),
     "cp_ef_profile": (None, [_i32]),
     "cp_ef_phase_ms": (_i32, [_vp, _i32]),
     "cp_ef_last_sweep": (_i32, [_vp, _vp]),
@@ -110,6 +115,10 @@ class HipError(RuntimeError):
     """A HIP runtime failure reported by the library."""
 
 
+class SweepTimeout(RuntimeError):
+    """An EF sweep wave gave up a bounded wait: that call's bytes are not valid."""
+
+
 def load(require_gpu=True):
     """The loaded library. Raises if it is not built, or (by default) if no GPU is visible."""
     global _lib
@@ -142,6 +151,8 @@ def check(status, exc_for_shape=ValueError):
         raise HipError(msg)
     if status == CP_ERR_INDEX:
         raise IndexError(msg)
+    if status == CP_ERR_TIMEOUT:
+        raise SweepTimeout(msg)
     raise ValueError(f"{msg} (status {status})")
 
 

@@ -58,8 +58,10 @@ static_assert(sizeof(SweepBatch) <= 4000, "kernel argument block");
 // The task table reaches device memory through the kernel arguments of a
 // one-block copy kernel (no host staging buffer whose lifetime would have to
 // outlast an asynchronous copy).
-__global__ void ef_tasks_store_kernel(const SweepBatch batch, int count, SweepTask* dst) {
+// status (when not null): the call's status word, cleared before any sweep can set it
+__global__ void ef_tasks_store_kernel(const SweepBatch batch, int count, SweepTask* dst, int* status) {
   if ((int)threadIdx.x < count) dst[threadIdx.x] = batch.t[threadIdx.x];
+  if (status && threadIdx.x == 0) *status = 0;
 }
 
 // Address-space views. U is read-only for the whole sweep and its row
@@ -712,15 +714,23 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
 // Wait (bounded) until *done > c, the count of the stripe's blocks complete so far, and
 // return that count. The producing wave releases the count at workgroup scope after
 // its error stores, so the acquire here orders this wave's later reads of those errors.
-// The bound (about 30 ms of sleeps) is far above any wait the schedule makes; past it
-// the wave goes on with one more block rather than spin for ever.
-__device__ __forceinline__ int wait_blocks(int* done, int c) {
+// The bound is ``limit`` sleeps of s_sleep 8 (about 512 clocks each): the default
+// 2^16 is about 14 ms at 2.4 GHz, far above any wait the schedule makes (one block's
+// sweep). Past it the wave sets bit 0 of the call's status word (read by the host,
+// which then rejects the call's bytes) and goes on with one more block rather than
+// spin for ever, so every wave still ends.
+__device__ __forceinline__ int wait_blocks(int* done, int c, int limit, int* status, int lane) {
   int v = __hip_atomic_load(done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-  for (int spins = 0; v <= c && spins < (1 << 16); ++spins) {
+  for (int spins = 0; v <= c && spins < limit; ++spins) {
     __builtin_amdgcn_s_sleep(8);
     v = __hip_atomic_load(done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
-  return __builtin_amdgcn_readfirstlane(v > c ? v : c + 1);
+  v = __builtin_amdgcn_readfirstlane(v);
+  if (v <= c) {
+    if (lane == 0) __hip_atomic_fetch_or(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return c + 1;
+  }
+  return v;
 }
 
 // W waves per stripe, for calls whose stripes alone would leave most SIMDs idle (few
@@ -736,7 +746,8 @@ __device__ __forceinline__ int wait_blocks(int* done, int c) {
 // counter's release and acquire.
 template <int RS, int W>
 __global__ __launch_bounds__(64 * W, 2) void ef_sweep_pipe_kernel(const SweepTask* __restrict__ tasks,
-                                                                  int count, int total, int xcd_runs) {
+                                                                  int count, int total, int xcd_runs,
+                                                                  int wait_limit, int* status) {
   int ti;
   const int stripe = sweep_item(tasks, count, total, xcd_runs != 0, &ti);
   if (stripe < 0) return;  // uniform over the workgroup
@@ -757,12 +768,13 @@ __global__ __launch_bounds__(64 * W, 2) void ef_sweep_pipe_kernel(const SweepTas
     const int i1 = b * 64;
     StripeVec<RS> t = stage_block<RS>(tk, i1, rr, l, s);
     for (int c = 0; c < b;) {
-      const int avail = min(wait_blocks(&done, c), b);
+      const int avail = min(wait_blocks(&done, c, wait_limit, status, l), b);
       cross_range<RS>(tk, i1, rr, l, t, c * 64, avail * 64);
       c = avail;
     }
     sweep_block_rows<RS>(tk, i1, rr, l, t, s);
-    __hip_atomic_store(&done, b + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    // a maximum, not a store: after a wait gave up, a late wave must not move the count back
+    __hip_atomic_fetch_max(&done, b + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 }
 
@@ -1197,9 +1209,10 @@ static EfLayout ef_layout(int64_t nrow, int64_t n, size_t base) {
   return L;
 }
 
-// workspace: [sweep task table][tensor table][per-tensor buffers]
+// workspace: [status word (256 bytes)][sweep task table][tensor table][per-tensor buffers]
+constexpr size_t kStatusBytes = 256;
 static size_t ef_tables_bytes(int count) {
-  return a256((size_t)count * sizeof(SweepTask)) + a256((size_t)count * sizeof(EfDev));
+  return kStatusBytes + a256((size_t)count * sizeof(SweepTask)) + a256((size_t)count * sizeof(EfDev));
 }
 
 size_t ef_ws_bytes(const cp_ef_tensor* t, int count) {
@@ -1221,7 +1234,14 @@ static void grid_range(int ttype, int* lo, int* hi, int* sub) {
 // Optional per-phase timing of an EF call (cp_ef_profile / cp_ef_phase_ms):
 // setup, commit, sweep, repack, decode.
 static thread_local PhaseClock g_clock;
-#define CP_PHASE(p) CP_PHASE_MARK(g_clock, p)
+#define CP_PHASE(p)                                                                \
+  do {                                                                             \
+    if (timed && g_clock.on) CP_HIP((p) < 0 ? g_clock.start(st) : g_clock.mark((p), st)); \
+  } while (0)
+
+// Spin bound of the pipe sweep's waits for the calling thread's EF calls (cp_ef_wait_limit).
+constexpr int kDefaultWaitLimit = 1 << 16;
+static thread_local int g_wait_limit = kDefaultWaitLimit;
 
 // The calling thread's last sweep launch (cp_ef_last_sweep): rows per stripe, waves per
 // stripe, mode (-1: none yet).
@@ -1251,8 +1271,9 @@ static void launch_decode(const EfDev* tab, const EfGroup& g, hipStream_t st) {
   ef_decode_kernel<TT><<<grid, 256, 0, st>>>(tab + g.first);
 }
 
+// timed: phases are recorded when the calling thread has timing on (cp_ef_profile)
 int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, void* ws,
-                    size_t ws_bytes, hipStream_t st) {
+                    size_t ws_bytes, hipStream_t st, bool timed = true) {
   if (!ts || count <= 0) return set_error(CP_ERR_ARG, "no tensors");
   if (count > 65535) return set_error(CP_ERR_ARG, "at most 65535 tensors per call (got %d)", count);
   if (n_iter < 1) return set_error(CP_ERR_ARG, "n_iter must be >= 1");
@@ -1276,8 +1297,9 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
   if (!aligned(ws, 256)) return set_error(CP_ERR_ALIGN, "workspace needs 256-byte alignment");
   CP_PHASE(-1);
   char* base = (char*)ws;
-  SweepTask* dtasks = (SweepTask*)base;
-  EfDev* dtab = (EfDev*)(base + a256((size_t)count * sizeof(SweepTask)));
+  int* dstatus = (int*)base;
+  SweepTask* dtasks = (SweepTask*)(base + kStatusBytes);
+  EfDev* dtab = (EfDev*)(base + kStatusBytes + a256((size_t)count * sizeof(SweepTask)));
   std::vector<SweepTask> tasks(count);
   std::vector<EfDev> devs(count);
   int max_n = 0, max_rows = 0;
@@ -1381,7 +1403,7 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
     const int cn = count - c0 < kTasksPerLaunch ? count - c0 : kTasksPerLaunch;
     SweepBatch b;
     for (int i = 0; i < cn; ++i) b.t[i] = tasks[by_len[c0 + i]];
-    ef_tasks_store_kernel<<<1, 64, 0, st>>>(b, cn, dtasks + c0);
+    ef_tasks_store_kernel<<<1, 64, 0, st>>>(b, cn, dtasks + c0, c0 == 0 ? dstatus : nullptr);
   }
   for (int c0 = 0; c0 < count; c0 += kDevPerStore) {
     const int cn = count - c0 < kDevPerStore ? count - c0 : kDevPerStore;
@@ -1422,18 +1444,18 @@ int ef_encode_batch(const cp_ef_tensor* ts, int count, int n_iter, int mode, voi
           dtasks, count, (int)total_stripes, same_n ? 1 : 0);
     else if (mode == CP_EF_EXACT) {
       const unsigned g = (unsigned)(8 * ((total_stripes + 7) / 8));
-      const int xr = same_n ? 1 : 0, ns = (int)total_stripes;
+      const int xr = same_n ? 1 : 0, ns = (int)total_stripes, wl = g_wait_limit;
       if (RS == 32) {
         switch (waves) {
-          case 2: ef_sweep_pipe_kernel<32, 2><<<g, 128, 0, st>>>(dtasks, count, ns, xr); break;
-          case 4: ef_sweep_pipe_kernel<32, 4><<<g, 256, 0, st>>>(dtasks, count, ns, xr); break;
-          default: ef_sweep_pipe_kernel<32, 8><<<g, 512, 0, st>>>(dtasks, count, ns, xr); break;
+          case 2: ef_sweep_pipe_kernel<32, 2><<<g, 128, 0, st>>>(dtasks, count, ns, xr, wl, dstatus); break;
+          case 4: ef_sweep_pipe_kernel<32, 4><<<g, 256, 0, st>>>(dtasks, count, ns, xr, wl, dstatus); break;
+          default: ef_sweep_pipe_kernel<32, 8><<<g, 512, 0, st>>>(dtasks, count, ns, xr, wl, dstatus); break;
         }
       } else {
         switch (waves) {
-          case 2: ef_sweep_pipe_kernel<16, 2><<<g, 128, 0, st>>>(dtasks, count, ns, xr); break;
-          case 4: ef_sweep_pipe_kernel<16, 4><<<g, 256, 0, st>>>(dtasks, count, ns, xr); break;
-          default: ef_sweep_pipe_kernel<16, 8><<<g, 512, 0, st>>>(dtasks, count, ns, xr); break;
+          case 2: ef_sweep_pipe_kernel<16, 2><<<g, 128, 0, st>>>(dtasks, count, ns, xr, wl, dstatus); break;
+          case 4: ef_sweep_pipe_kernel<16, 4><<<g, 256, 0, st>>>(dtasks, count, ns, xr, wl, dstatus); break;
+          default: ef_sweep_pipe_kernel<16, 8><<<g, 512, 0, st>>>(dtasks, count, ns, xr, wl, dstatus); break;
         }
       }
     }
@@ -1507,12 +1529,28 @@ int ef_encode_noalloc(const cp_ef_tensor& t, int n_iter, hipStream_t st) {
                      (long long)t.nrow, (long long)t.n, need, kNoAllocWsBytes);
   void* ws = nullptr;
   if (int e = scratch_ptr(&ws)) return e;
-  // phase timing would create events on first use: off for this call
-  const bool timing = g_clock.on;
-  g_clock.on = false;
-  const int r = ef_encode_batch(&t, 1, n_iter, CP_EF_EXACT, ws, kNoAllocWsBytes, st);
-  g_clock.on = timing;
-  return r;
+  // untimed: phase timing would create events on first use
+  return ef_encode_batch(&t, 1, n_iter, CP_EF_EXACT, ws, kNoAllocWsBytes, st, false);
+}
+
+// CP_OK, or CP_ERR_TIMEOUT when the status word of the EF call that used workspace ws
+// (the static one of cp_ef_encode_noalloc on the current device when ws is null) says
+// a sweep wave gave up waiting. Synchronizes st.
+int ef_read_status(const void* ws, hipStream_t st) {
+  const void* src = ws;
+  if (!src) {
+    void* p = nullptr;
+    if (int e = scratch_ptr(&p)) return e;
+    src = p;
+  }
+  int status = 0;
+  CP_HIP(hipMemcpyAsync(&status, src, sizeof(int), hipMemcpyDeviceToHost, st));
+  CP_HIP(hipStreamSynchronize(st));
+  if (status & 1)
+    return set_error(CP_ERR_TIMEOUT,
+                     "EF sweep: a wave gave up waiting for an earlier block of its stripe (spin "
+                     "bound exhausted); the call's bytes are not valid");
+  return CP_OK;
 }
 
 }  // namespace cp
@@ -1520,6 +1558,13 @@ int ef_encode_noalloc(const cp_ef_tensor& t, int n_iter, hipStream_t st) {
 extern "C" {
 
 void cp_ef_profile(int enable) { cp::g_clock.on = enable != 0; }
+
+void cp_ef_wait_limit(int spins) { cp::g_wait_limit = spins < 0 ? cp::kDefaultWaitLimit : spins; }
+
+int cp_ef_read_status(const void* ws, void* stream) {
+  cp::clear_error();
+  return cp::ef_read_status(ws, (hipStream_t)stream);
+}
 
 int cp_ef_phase_ms(float* out, int nphase) {
   cp::clear_error();

@@ -3,16 +3,21 @@
 // X is [N, d] row-major activations (bf16 or f32), H is [d, d] float32 and is
 // accumulated in place (beta = 1), so hook batches can stream in. Split-K over
 // rows of X: N is 65536-131072 while d is 1024-14336, so the row dimension is
-// what fills 256 CUs. Each workgroup adds its finished tile into H with
-// float32 atomics (one per element per workgroup): the sum over row splits is
-// exact up to float32 rounding order.
+// what fills 256 CUs. The result does not depend on scheduling: with one row
+// split a workgroup adds its finished tile into H itself (one writer per
+// element); with several, each split stores its tile into a workspace slot of
+// its own and one reduction pass adds the splits' tiles to H in split order
+// (H + ((p0 + p1) + p2 ...)). The same X therefore gives the same H bit for
+// bit, run after run.
 //
 //  bf16: lower-triangle 256 x 256 tiles on v_mfma_f32_32x32x16_bf16, operands
-//        read transposed from LDS (hess_bf16_tri_kernel), then a mirror pass;
+//        read transposed from LDS (hess_bf16_tri_kernel), then a pass that
+//        reduces the splits and mirrors the lower triangle into the upper one;
 //  f32:  128 x 128 tiles on v_mfma_f32_32x32x2f32, which takes one row t per
 //        lane, so the [t][i] panel is used as loaded.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <type_traits>
 
 #include "cp_host.h"
@@ -29,7 +34,7 @@ constexpr int KT = 32;   // f32 kernel: rows of X per step
 __device__ __forceinline__ int mfma32_row(int v, int l) { return 8 * (v >> 2) + 4 * (l >> 5) + (v & 3); }
 
 // ---------------------------------------------------------------- bf16 input
-// Lower-triangle tiles of 256 x 256 (H is symmetric; hess_mirror_kernel copies
+// Lower-triangle tiles of 256 x 256 (H is symmetric; hess_tri_reduce_kernel copies
 // the lower triangle into the upper one afterwards), split-K over rows of X.
 // A workgroup is 4 waves, each owning a 128 x 128 block as 4 x 4 MFMA 32x32
 // tiles (256 float32 accumulators): the largest block a wave can hold, because
@@ -242,9 +247,13 @@ struct HessJobs {
 };
 static_assert(sizeof(HessJobs) <= 4000, "kernel argument block");
 
+// part == nullptr (one row split): the workgroup adds its tile into H's lower
+// triangle. Otherwise it stores the whole 256 x 256 tile, row-major, into slot
+// (job, split, tile) of part, for hess_tri_reduce_kernel.
 __global__ __launch_bounds__(HNT) void hess_bf16_tri_kernel(const HessJobs jobs, int njobs,
                                                             int64_t N, int d, int ntiles, int splits,
-                                                            int64_t rows_per_split) {
+                                                            int64_t rows_per_split,
+                                                            float* __restrict__ part) {
   __shared__ __align__(16) char lds[NSLOT * 2 * PANEL];
   // items run job by job, then split by split: the XCD-contiguous hand-out keeps one
   // XCD on the same rows of one X
@@ -282,6 +291,20 @@ __global__ __launch_bounds__(HNT) void hess_bf16_tri_kernel(const HessJobs jobs,
     tile_rows<true>(X, r0, r1, d, i0, j0, lds, acc);
   // lane l holds, for register v of tile (x, y), row wm + 32x + mfma32_row(v, l)
   // and column wn + 32y + l % 32 of the workgroup tile
+  if (part) {
+    // every register stored (zeros where the wave skipped its block; rows and
+    // columns past d hold sums of zero-filled loads): the reduction reads only
+    // the lower-triangle entries inside d
+    float* Pb = part + ((int64_t)(job * splits + split) * ntiles + tile) * (BT * BT) +
+                (wm + 4 * (l >> 5)) * BT + wn + (l & 31);
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 4; ++y)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) Pb[(x * 32 + 8 * (v >> 2) + (v & 3)) * BT + y * 32] = acc[x][y][v];
+    return;
+  }
   float* Hb = H + (int64_t)(i0 + wm + 4 * (l >> 5)) * d + (j0 + wn + (l & 31));
   const bool full = ti != tj && i0 + BT <= d;  // interior tile strictly below the diagonal
 #pragma unroll
@@ -292,39 +315,62 @@ __global__ __launch_bounds__(HNT) void hess_bf16_tri_kernel(const HessJobs jobs,
       for (int v = 0; v < 16; ++v) {
         const int i = i0 + wm + x * 32 + mfma32_row(v, l);
         const int j = j0 + wn + y * 32 + (l & 31);
-        if (full || (i < d && j <= i))
-          atomicAdd(Hb + (int64_t)(x * 32 + 8 * (v >> 2) + (v & 3)) * d + y * 32, acc[x][y][v]);
+        float* p = Hb + (int64_t)(x * 32 + 8 * (v >> 2) + (v & 3)) * d + y * 32;
+        if (full || (i < d && j <= i)) *p = *p + acc[x][y][v];
       }
 }
 
-// H[i][j] = H[j][i] for i < j, through 64 x 64 LDS tiles; blockIdx.z is the job.
-__global__ __launch_bounds__(256) void hess_mirror_kernel(const HessJobs jobs, int d) {
+// Finishes a bf16 accumulation over 64 x 64 blocks (bi, bj) of the lower triangle
+// (blockIdx.z is the job): with part, each entry (i, j <= i) becomes
+// H + (p_0 + p_1 + ... + p_{splits-1}), the row splits' tiles summed in split
+// order; then the block's entries are written to the mirror position (j, i) as
+// well, through LDS, so H leaves symmetric. H's upper triangle is never read.
+__global__ __launch_bounds__(256) void hess_tri_reduce_kernel(const HessJobs jobs, int d, int ntiles,
+                                                              int splits,
+                                                              const float* __restrict__ part) {
   float* __restrict__ H = jobs.H[blockIdx.z];
   __shared__ float tl[64][65];
-  const int bi = blockIdx.y, bj = blockIdx.x;  // target tile (upper): rows bi, cols bj
-  if (bj < bi) return;
+  const int bi = blockIdx.y, bj = blockIdx.x;  // lower block: rows bi, columns bj
+  if (bj > bi) return;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  // source: lower tile rows bj, cols bi
+  const int j = bj * 64 + tx;
+  const int tj = j / BT;
+  const int64_t slot = (int64_t)ntiles * (BT * BT);  // floats between one split's tiles
   for (int r = ty; r < 64; r += 4) {
-    int i = bj * 64 + r, j = bi * 64 + tx;
-    if (i < d && j < d) tl[r][tx] = H[(int64_t)i * d + j];
+    const int i = bi * 64 + r;
+    if (i >= d || j >= d || j > i) continue;
+    float h = H[(int64_t)i * d + j];
+    if (part) {
+      const int ti = i / BT;
+      const float* p = part + (int64_t)blockIdx.z * splits * slot +
+                       (int64_t)(ti * (ti + 1) / 2 + tj) * (BT * BT) + (i % BT) * BT + (j % BT);
+      float s = p[0];
+      for (int k = 1; k < splits; ++k) s += p[k * slot];
+      h += s;
+      H[(int64_t)i * d + j] = h;
+    }
+    tl[r][tx] = h;
   }
   __syncthreads();
+  // upper block: rows bj, columns bi; entry (bj*64 + r, bi*64 + tx) = lower (bi*64 + tx, bj*64 + r)
   for (int r = ty; r < 64; r += 4) {
-    int i = bi * 64 + r, j = bj * 64 + tx;
-    if (i < d && j < d && j > i) H[(int64_t)i * d + j] = tl[tx][r];
+    const int i = bj * 64 + r, jj = bi * 64 + tx;
+    if (i < d && jj < d && jj > i) H[(int64_t)i * d + jj] = tl[tx][r];
   }
 }
 
 // ---------------------------------------------------------------- f32 input
+// part == nullptr (one row split): the workgroup adds its tile into H. Otherwise
+// it stores the tile into split blockIdx.z's full [d, d] partial in part, for
+// hess_f32_reduce_kernel.
 __global__ __launch_bounds__(256) void hess_f32_kernel(const float* __restrict__ X, int64_t N, int d,
-                                                       int64_t rows_per_split, float* __restrict__ H) {
+                                                       int64_t rows_per_split, float* __restrict__ H,
+                                                       float* __restrict__ part) {
   __shared__ float sA[KT][HT + 4];
   __shared__ float sB[KT][HT + 4];
   const int i0 = blockIdx.y * HT, j0 = blockIdx.x * HT;
   const int64_t r0 = (int64_t)blockIdx.z * rows_per_split;
   const int64_t r1 = min(N, r0 + rows_per_split);
-  if (r0 >= r1) return;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
   const int wm = (w >> 1) * 64, wn = (w & 1) * 64;
   f32x16 acc[2][2];
@@ -358,6 +404,7 @@ __global__ __launch_bounds__(256) void hess_f32_kernel(const float* __restrict__
     }
     __syncthreads();
   }
+  float* const dst = part ? part + (int64_t)blockIdx.z * d * d : H;
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -366,15 +413,34 @@ __global__ __launch_bounds__(256) void hess_f32_kernel(const float* __restrict__
       for (int v = 0; v < 16; ++v) {
         int i = i0 + wm + x * 32 + mfma32_row(v, l);
         int j = j0 + wn + y * 32 + (l & 31);
-        if (i < d && j < d) atomicAdd(H + (int64_t)i * d + j, acc[x][y][v]);
+        if (i < d && j < d) {
+          float* p = dst + (int64_t)i * d + j;
+          *p = part ? acc[x][y][v] : *p + acc[x][y][v];
+        }
       }
 }
 
-// Row splits for the triangle kernel: one 96 KB-LDS workgroup per CU, so the
-// time is about rounds x (stages per split + epilogue); the epilogue's
-// atomics cost about 16 stages. A split spans at most 2^30 bytes of X, so the
-// buffer offsets of its loads (up to eight stages past its end) stay below 2^31.
-static int pick_splits(int ntiles, int64_t N, int64_t d) {
+// H[e] = H[e] + (p_0[e] + p_1[e] + ... + p_{splits-1}[e]): the f32 path's row
+// splits summed in split order.
+__global__ __launch_bounds__(256) void hess_f32_reduce_kernel(float* __restrict__ H, int64_t dd,
+                                                              int splits,
+                                                              const float* __restrict__ part) {
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < dd; e += (int64_t)gridDim.x * 256) {
+    float s = part[e];
+    for (int k = 1; k < splits; ++k) s += part[k * dd + e];
+    H[e] = H[e] + s;
+  }
+}
+
+// Row splits for the triangle kernel: one 144 KB-LDS workgroup per CU, so the
+// main pass takes about rounds x (stages per split + epilogue), the epilogue (a
+// 256 KB tile store) about 6 stages; with more than one split the reduction then
+// reads every split's tile once, about 0.05 of a stage per tile and split
+// spread over the GPU. A split spans at most 2^30 bytes of X, so the buffer
+// offsets of its loads (up to eight stages past its end) stay below 2^31.
+// Returns the split count (0 if none fits); *rows_per_split is a multiple of KS
+// and every split has rows.
+static int pick_splits(int ntiles, int64_t N, int64_t d, int64_t* rows_per_split) {
   int best_s = 0;
   double best = 1e30;
   for (int s = 1; s <= 4096; ++s) {
@@ -383,13 +449,59 @@ static int pick_splits(int ntiles, int64_t N, int64_t d) {
     if (best_s && rows < 256) break;
     const double stages = (double)((rows + KS - 1) / KS);
     const double rounds = (double)(((int64_t)ntiles * s + 255) / 256);
-    const double cost = rounds * (stages + 16.0);
+    const double cost = rounds * (stages + 6.0) + (s > 1 ? 0.05 * s * ntiles : 0.0);
     if (cost < best - 1e-9) {
       best = cost;
       best_s = s;
     }
   }
-  return best_s;
+  if (const char* e = getenv("CP_HESS_SPLITS")) {  // tuning override (measurement only)
+    const int s = atoi(e);
+    if (s >= 1 && s <= 4096 && ((N + s - 1) / s + KS - 1) / KS * KS * 2 * d <= (int64_t(1) << 30)) best_s = s;
+  }
+  if (best_s == 0) return 0;
+  int64_t rps = (N + best_s - 1) / best_s;
+  rps = (rps + KS - 1) / KS * KS;
+  *rows_per_split = rps;
+  return (int)((N + rps - 1) / rps);  // rounding rps up may leave fewer splits with rows
+}
+
+// Row splits of the f32 kernel: about 4 workgroups per CU, each at least 512 rows.
+static int f32_splits(int64_t N, int64_t d, int64_t* rows_per_split) {
+  const int tiles = (int)((d + HT - 1) / HT);
+  const int64_t want = (1024 + (int64_t)tiles * tiles - 1) / ((int64_t)tiles * tiles);
+  const int64_t splits = want < 1 ? 1 : want;
+  int64_t rps = (N + splits - 1) / splits;
+  if (rps < 512) rps = 512;
+  rps = (rps + KT - 1) / KT * KT;
+  *rows_per_split = rps;
+  return (int)((N + rps - 1) / rps);
+}
+
+constexpr size_t kTileBytes = (size_t)BT * BT * sizeof(float);
+
+// Workspace of one bf16 launch of cn jobs (0 when it runs as one split).
+static size_t bf16_ws(int cn, int64_t N, int64_t d) {
+  const int T = (int)((d + BT - 1) / BT);
+  const int ntiles = T * (T + 1) / 2;
+  int64_t rps = 0;
+  const int s = pick_splits(ntiles * cn, N, d, &rps);
+  return s > 1 ? (size_t)cn * s * ntiles * kTileBytes : 0;
+}
+
+static size_t hess_ws_need(int count, int x_dtype, int64_t N, int64_t d) {
+  if (N <= 0 || d <= 0 || count <= 0) return 0;
+  if (x_dtype == 0) {
+    int64_t rps = 0;
+    const int s = f32_splits(N, d, &rps);
+    return s > 1 ? (size_t)s * d * d * sizeof(float) : 0;  // jobs run one after another
+  }
+  size_t need = bf16_ws(count < kHessJobs ? count : kHessJobs, N, d);
+  if (count > kHessJobs && count % kHessJobs) {
+    const size_t tail = bf16_ws(count % kHessJobs, N, d);
+    if (tail > need) need = tail;
+  }
+  return need;
 }
 
 }  // namespace cp
@@ -398,7 +510,7 @@ namespace cp {
 
 // H_z += X_z^T X_z for count jobs of one shape, bf16 X.
 static int hess_bf16_batch(const void* const* X, float* const* H, int count, int64_t N, int64_t d,
-                           hipStream_t st) {
+                           void* ws, size_t ws_bytes, hipStream_t st) {
   const int T = (int)((d + BT - 1) / BT);
   const int ntiles = T * (T + 1) / 2;
   for (int c0 = 0; c0 < count; c0 += kHessJobs) {
@@ -411,35 +523,51 @@ static int hess_bf16_batch(const void* const* X, float* const* H, int count, int
       jobs.X[i] = (const uint16_t*)X[c0 + i];
       jobs.H[i] = H[c0 + i];
     }
-    const int splits = pick_splits(ntiles * cn, N, d);
+    int64_t rps = 0;
+    const int splits = pick_splits(ntiles * cn, N, d, &rps);
     if (splits == 0 || (int64_t)ntiles * cn * splits * 8 > INT32_MAX)
       return set_error(CP_ERR_SHAPE, "X [%lld, %lld] too large for one accumulation; pass fewer rows",
                        (long long)N, (long long)d);
-    int64_t rps = (N + splits - 1) / splits;
-    rps = (rps + KS - 1) / KS * KS;
+    float* part = nullptr;
+    if (splits > 1) {
+      const size_t need = (size_t)cn * splits * ntiles * kTileBytes;
+      if (!ws || ws_bytes < need)
+        return set_error(CP_ERR_WORKSPACE, "Hessian workspace: need %zu bytes, have %zu", need, ws_bytes);
+      if (!aligned(ws, 16)) return set_error(CP_ERR_ALIGN, "Hessian workspace needs 16-byte alignment");
+      part = (float*)ws;
+    }
     const int total = ntiles * splits * cn;
     const int per = (total + 7) / 8;
-    hess_bf16_tri_kernel<<<dim3(8 * per), HNT, 0, st>>>(jobs, cn, N, (int)d, ntiles, splits, rps);
+    hess_bf16_tri_kernel<<<dim3(8 * per), HNT, 0, st>>>(jobs, cn, N, (int)d, ntiles, splits, rps, part);
     CP_LAUNCHED("hessian launch");
     const int tb = (int)((d + 63) / 64);
-    hess_mirror_kernel<<<dim3(tb, tb, cn), 256, 0, st>>>(jobs, (int)d);
-    CP_LAUNCHED("hessian mirror");
+    hess_tri_reduce_kernel<<<dim3(tb, tb, cn), 256, 0, st>>>(jobs, (int)d, ntiles, splits, part);
+    CP_LAUNCHED("hessian reduce");
   }
   return CP_OK;
 }
 
-static int hess_f32(const float* X, int64_t N, int64_t d, float* H, hipStream_t st) {
+static int hess_f32(const float* X, int64_t N, int64_t d, float* H, void* ws, size_t ws_bytes,
+                    hipStream_t st) {
   const int tiles = (int)((d + HT - 1) / HT);
-  // enough row splits for ~4 workgroups per CU, each at least 512 rows
-  int64_t want = (1024 + (int64_t)tiles * tiles - 1) / ((int64_t)tiles * tiles);
-  int64_t splits = want < 1 ? 1 : want;
-  int64_t rps = (N + splits - 1) / splits;
-  if (rps < 512) rps = 512;
-  rps = (rps + KT - 1) / KT * KT;
-  splits = (N + rps - 1) / rps;
+  int64_t rps = 0;
+  const int splits = f32_splits(N, d, &rps);
+  float* part = nullptr;
+  if (splits > 1) {
+    const size_t need = (size_t)splits * d * d * sizeof(float);
+    if (!ws || ws_bytes < need)
+      return set_error(CP_ERR_WORKSPACE, "Hessian workspace: need %zu bytes, have %zu", need, ws_bytes);
+    part = (float*)ws;
+  }
   dim3 grid(tiles, tiles, (unsigned)splits);
-  hess_f32_kernel<<<grid, 256, 0, st>>>(X, N, (int)d, rps, H);
+  hess_f32_kernel<<<grid, 256, 0, st>>>(X, N, (int)d, rps, H, part);
   CP_LAUNCHED("hessian launch");
+  if (part) {
+    const int64_t dd = d * d;
+    const int64_t blocks = (dd + 255) / 256 < 4096 ? (dd + 255) / 256 : 4096;
+    hess_f32_reduce_kernel<<<dim3((unsigned)blocks), 256, 0, st>>>(H, dd, splits, part);
+    CP_LAUNCHED("hessian reduce");
+  }
   return CP_OK;
 }
 
@@ -450,7 +578,37 @@ static int hess_check(int x_dtype, int64_t N, int64_t d) {
   return CP_OK;
 }
 
+static int hess_run(const void* const* X, float* const* H, int count, int x_dtype, int64_t N,
+                    int64_t d, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (x_dtype == 1) return hess_bf16_batch(X, H, count, N, d, ws, ws_bytes, st);
+  for (int i = 0; i < count; ++i) {
+    if (!X[i] || !H[i]) return set_error(CP_ERR_ARG, "job %d: null X/H", i);
+    if (!aligned(X[i], 16) || !aligned(H[i], 4)) return set_error(CP_ERR_ALIGN, "job %d: misaligned", i);
+    if (int s = hess_f32((const float*)X[i], N, d, H[i], ws, ws_bytes, st)) return s;
+  }
+  return CP_OK;
+}
+
+// hess_run with a stream-ordered workspace of its own, freed on the stream after
+// the last launch that reads it.
+static int hess_run_alloc(const void* const* X, float* const* H, int count, int x_dtype, int64_t N,
+                          int64_t d, hipStream_t st) {
+  const size_t need = hess_ws_need(count, x_dtype, N, d);
+  void* ws = nullptr;
+  if (need) CP_HIP(hipMallocAsync(&ws, need, st));
+  const int s = hess_run(X, H, count, x_dtype, N, d, ws, need, st);
+  if (ws) {
+    const hipError_t e = hipFreeAsync(ws, st);
+    if (s == CP_OK && e != hipSuccess) return hip_fail(e, "hipFreeAsync");
+  }
+  return s;
+}
+
 }  // namespace cp
+
+extern "C" size_t cp_hess_ws_bytes(int count, int x_dtype, int64_t N, int64_t d) {
+  return cp::hess_ws_need(count, x_dtype, N, d);
+}
 
 extern "C" int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, float* H, void* stream) {
   cp::clear_error();
@@ -458,9 +616,7 @@ extern "C" int cp_hess_accum(const void* X, int x_dtype, int64_t N, int64_t d, f
   if (!H) return cp::set_error(CP_ERR_ARG, "null H");
   if (N == 0) return CP_OK;  // no rows: H += 0
   if (!X) return cp::set_error(CP_ERR_ARG, "null X");
-  if (!cp::aligned(X, 16) || !cp::aligned(H, 4)) return cp::set_error(CP_ERR_ALIGN, "X needs 16-byte alignment");
-  if (x_dtype == 1) return cp::hess_bf16_batch(&X, &H, 1, N, d, (hipStream_t)stream);
-  return cp::hess_f32((const float*)X, N, d, H, (hipStream_t)stream);
+  return cp::hess_run_alloc(&X, &H, 1, x_dtype, N, d, (hipStream_t)stream);
 }
 
 extern "C" int cp_hess_accum_batch(const void* const* X, float* const* H, int count, int x_dtype,
@@ -469,12 +625,14 @@ extern "C" int cp_hess_accum_batch(const void* const* X, float* const* H, int co
   if (!X || !H || count <= 0) return cp::set_error(CP_ERR_ARG, "no jobs");
   if (int s = cp::hess_check(x_dtype, N, d)) return s;
   if (N == 0) return CP_OK;  // no rows: every H += 0
-  hipStream_t st = (hipStream_t)stream;
-  if (x_dtype == 1) return cp::hess_bf16_batch(X, H, count, N, d, st);
-  for (int i = 0; i < count; ++i) {
-    if (!X[i] || !H[i]) return cp::set_error(CP_ERR_ARG, "job %d: null X/H", i);
-    if (!cp::aligned(X[i], 16) || !cp::aligned(H[i], 4)) return cp::set_error(CP_ERR_ALIGN, "job %d: misaligned", i);
-    if (int s = cp::hess_f32((const float*)X[i], N, d, H[i], st)) return s;
-  }
-  return CP_OK;
+  return cp::hess_run_alloc(X, H, count, x_dtype, N, d, (hipStream_t)stream);
+}
+
+extern "C" int cp_hess_accum_batch_ws(const void* const* X, float* const* H, int count, int x_dtype,
+                                      int64_t N, int64_t d, void* ws, size_t ws_bytes, void* stream) {
+  cp::clear_error();
+  if (!X || !H || count <= 0) return cp::set_error(CP_ERR_ARG, "no jobs");
+  if (int s = cp::hess_check(x_dtype, N, d)) return s;
+  if (N == 0) return CP_OK;  // no rows: every H += 0
+  return cp::hess_run(X, H, count, x_dtype, N, d, ws, ws_bytes, (hipStream_t)stream);
 }

@@ -121,7 +121,8 @@ def _ws_for(tensors):
     return arr, lib.cp_ef_ws_bytes(arr, len(tensors))
 
 
-def ef_encode_dev(items, n_iter=2, mode=_lib.CP_EF_EXACT, checked=False, out_stream=None):
+def ef_encode_dev(items, n_iter=2, mode=_lib.CP_EF_EXACT, checked=False, out_stream=None,
+                  status=None):
     """Batched EF on device tensors.
 
     items: list of dicts with keys ttype, x [nrow, n] f32, qw [n] f32 or None,
@@ -132,6 +133,9 @@ def ef_encode_dev(items, n_iter=2, mode=_lib.CP_EF_EXACT, checked=False, out_str
     The caller must order that stream after this call's work before using or freeing
     them, and the current stream must already be ordered after out_stream's earlier
     work (as a class stream that waited on the caller's stream is).
+    status: None checks the call's status word before returning (one synchronization;
+    SweepTimeout when a sweep wave gave up a bounded wait); a list receives a device
+    copy of the word instead, for check_status once the caller next synchronizes.
     Returns a list of (raw uint8 [nrow, row_bytes], recon f32 or None)."""
     if not checked:
         items = [dict(it, order=_order_dev(it["order"], 1, it["x"].shape[1], it["x"].device,
@@ -160,7 +164,25 @@ def ef_encode_dev(items, n_iter=2, mode=_lib.CP_EF_EXACT, checked=False, out_str
     st = lib.cp_ef_encode_batch(arr, len(structs), int(n_iter), int(mode), _lib.ptr(ws), ws.numel(),
                                 _lib.stream_ptr())
     _lib.check(st)
+    if status is None:
+        _lib.check(lib.cp_ef_read_status(_lib.ptr(ws), _lib.stream_ptr()))
+    else:
+        status.append(ws[:4].view(torch.int32).clone())  # the word; ws itself is released
     return outs
+
+
+def status_failed(words):
+    """Whether any status word ef_encode_dev(status=...) collected has its give-up bit
+    (device int32 tensors of one element; reading them synchronizes)."""
+    return bool(words) and bool(int(torch.cat([w.reshape(1) for w in words]).bitwise_and(1).max()))
+
+
+def check_status(words):
+    """Raise SweepTimeout when a collected status word says a sweep wave gave up a bounded
+    wait (that call's bytes are not valid)."""
+    if status_failed(words):
+        raise _lib.SweepTimeout("EF sweep: a wave gave up waiting for an earlier block of its "
+                                "stripe (spin bound exhausted); the call's bytes are not valid")
 
 
 MODES = {"exact": _lib.CP_EF_EXACT, "mfma": _lib.CP_EF_MFMA, "exact_valu": _lib.CP_EF_EXACT_VALU}
@@ -238,14 +260,23 @@ def encode_size_classes(classes, n_iter=2, mode="exact", damp=0.01, act_order=Tr
     # needs record_stream (whose per-tensor events cost ~1.8 ms of host time at release
     # for the 392 outputs of the 28-layer Qwen3-0.6B-shaped set)
     outs = [None] * len(classes)
+    words = [None] * len(classes)
     for k in sorted(range(len(classes)), key=lambda k: classes[k][0].shape[-1]):
         (_, build), s, (order, U, _) = classes[k], streams[k], facs[k]
+        got = []
         with torch.cuda.stream(s):
             outs[k] = ef_encode_dev(build(U, order), n_iter, MODES[mode] if isinstance(mode, str)
-                                    else mode, checked=True, out_stream=cur)
+                                    else mode, checked=True, out_stream=cur, status=got)
+        words[k] = got[0]
     for s in streams:
         cur.wait_stream(s)
-    failed = torch.stack([f.max() for (_, _, f) in facs]).cpu().tolist()
+    # one read for every class: factorization flags, then EF status words
+    seen = torch.stack([f.max() for (_, _, f) in facs] +
+                       [w.reshape(()) for w in words]).cpu().tolist()
+    failed, gave_up = seen[:len(classes)], seen[len(classes):]
+    for k, bad in enumerate(failed):
+        if not bad and int(gave_up[k]) & 1:
+            check_status([words[k]])  # raises
     for k, bad in enumerate(failed):
         if bad:
             Hb, build = classes[k]

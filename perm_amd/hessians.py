@@ -17,7 +17,9 @@ format (float16 H over a per-matrix ``hscale``, exact float32 ``diag32``, ``n``,
 with the packing arithmetic on the GPU (cp_h2_pack); ``load_hessian`` reads the same files
 (and the older float32-only ones) and rebuilds the float64 matrix on the GPU (cp_h2_expand).
 """
+import contextlib
 import os
+from typing import NamedTuple
 
 import numpy as np
 import torch
@@ -39,24 +41,44 @@ def _on_device(X, H):
                          f"tensors on one CUDA device")
 
 
-def xtx_accumulate(X, H=None):
-    """H += X^T X on the device. X: [..., d] bf16 or float32 CUDA tensor (leading
-    dims are flattened into rows, like the hook's reshape(-1, d)); H: [d, d]
-    float32 CUDA tensor or None (a zero one is allocated). Returns H."""
+def _prepared(X, H):
+    """(X as a contiguous [rows, d] bf16 / float32 tensor, d), with H checked."""
     _on_device(X, H)
-    lib = _lib.load()
     d = X.shape[-1]
     X2 = X.reshape(-1, d)
     if X2.dtype not in (torch.bfloat16, torch.float32):
         X2 = X2.float()
     X2 = X2.contiguous()
+    if H is not None and (H.shape != (d, d) or H.dtype != torch.float32 or not H.is_contiguous()):
+        raise ValueError("H must be a contiguous float32 [d, d] tensor")
+    return X2, d
+
+
+def _accumulate_group(lib, xs, hs, N, d, dt):
+    """One cp_hess_accum_batch_ws call for jobs of one (rows, d, dtype), its row-split
+    workspace from torch's allocator on the current stream."""
+    import ctypes
+    xdt = 1 if dt == torch.bfloat16 else 0
+    xa = (ctypes.c_void_p * len(xs))(*[x.data_ptr() for x in xs])
+    ha = (ctypes.c_void_p * len(hs))(*[h.data_ptr() for h in hs])
+    nbytes = lib.cp_hess_ws_bytes(len(xs), xdt, N, d)
+    ws = _lib.workspace(nbytes, xs[0].device) if nbytes else None
+    _lib.check(lib.cp_hess_accum_batch_ws(ctypes.cast(xa, ctypes.c_void_p),
+                                          ctypes.cast(ha, ctypes.c_void_p), len(xs), xdt, N, d,
+                                          _lib.ptr(ws), nbytes, _lib.stream_ptr()))
+
+
+def xtx_accumulate(X, H=None):
+    """H += X^T X on the device. X: [..., d] bf16 or float32 CUDA tensor (leading
+    dims are flattened into rows, like the hook's reshape(-1, d)); H: [d, d]
+    float32 CUDA tensor or None (a zero one is allocated). Returns H. The same X and
+    H give the same result bit for bit (the row summation order is fixed)."""
+    lib = _lib.load()
+    X2, d = _prepared(X, H)
     if H is None:
         H = torch.zeros((d, d), dtype=torch.float32, device=X2.device)
-    if H.shape != (d, d) or H.dtype != torch.float32 or not H.is_contiguous():
-        raise ValueError("H must be a contiguous float32 [d, d] tensor")
-    st = lib.cp_hess_accum(_lib.ptr(X2), 1 if X2.dtype == torch.bfloat16 else 0, X2.shape[0], d,
-                           _lib.ptr(H), _lib.stream_ptr())
-    _lib.check(st)
+    if X2.shape[0]:
+        _accumulate_group(lib, [X2], [H], X2.shape[0], d, X2.dtype)
     return H
 
 
@@ -64,26 +86,14 @@ def xtx_accumulate_many(Xs, Hs):
     """Hs[z] += Xs[z]^T Xs[z] for many (X, H) pairs, batched by (rows, d, dtype) into as
     few launches as fit. X: [..., d] bf16 or float32 CUDA tensors; H: contiguous float32
     [d, d] CUDA tensors (updated in place)."""
-    import ctypes
     lib = _lib.load()
     groups = {}
     for X, H in zip(Xs, Hs):
-        _on_device(X, H)
-        d = X.shape[-1]
-        X2 = X.reshape(-1, d)
-        if X2.dtype not in (torch.bfloat16, torch.float32):
-            X2 = X2.float()
-        X2 = X2.contiguous()
-        if H.shape != (d, d) or H.dtype != torch.float32 or not H.is_contiguous():
-            raise ValueError("H must be a contiguous float32 [d, d] tensor")
+        X2, d = _prepared(X, H)
         groups.setdefault((X2.shape[0], d, X2.dtype), []).append((X2, H))
     for (N, d, dt), jobs in groups.items():
-        xs = (ctypes.c_void_p * len(jobs))(*[x.data_ptr() for x, _ in jobs])
-        hs = (ctypes.c_void_p * len(jobs))(*[h.data_ptr() for _, h in jobs])
-        st = lib.cp_hess_accum_batch(ctypes.cast(xs, ctypes.c_void_p), ctypes.cast(hs, ctypes.c_void_p),
-                                     len(jobs), 1 if dt == torch.bfloat16 else 0, N, d,
-                                     _lib.stream_ptr())
-        _lib.check(st)
+        if N:
+            _accumulate_group(lib, [x for x, _ in jobs], [h for _, h in jobs], N, d, dt)
     return Hs
 
 
@@ -150,100 +160,131 @@ def _block_of(gguf_name):
     return int(parts[1]) if parts[0] == "blk" and len(parts) > 1 and parts[1].isdigit() else -1
 
 
+class HookTarget(NamedTuple):
+    """A module whose input Hessian is collected and the GGUF tensor it is keyed by."""
+    module_name: str
+    module: object
+    gguf_name: str   # with ".weight"
+    width: int       # the module's in_features, equal to the tensor's ne[0]
+
+
+def _in_shard(gguf_name, layer_lo, layer_hi):
+    """Blocks [layer_lo, layer_hi) own their tensors; a tensor outside the blocks (output)
+    belongs to the shard that starts at block 0."""
+    blk = _block_of(gguf_name)
+    return layer_lo <= blk < layer_hi if blk >= 0 else layer_lo == 0
+
+
+def plan_targets(model, name_map, gguf_ne0, layer_lo, layer_hi):
+    """Sort the Linear / Embedding modules of ``model`` into this shard's hook targets and
+    the unmapped ones, with the classification of coldpress/hessians.py:108-135: a module
+    without a GGUF name, or whose tensor is not in ``gguf_ne0``, is unmapped; a tensor of
+    another shard, or a token lookup (integer input, so no Hessian), is left alone.
+    Returns ([HookTarget], [unmapped description]). Raises ValueError naming every module
+    whose in_features disagrees with its tensor's ne[0]; nothing is hooked before that
+    check, so a refused call leaves the model untouched."""
+    import torch.nn as nn
+    targets, unmapped, conflicts = [], [], []
+    for mname, mod in model.named_modules():
+        if not isinstance(mod, (nn.Linear, nn.Embedding)):
+            continue
+        base = name_map.get(mname)
+        gguf = None if base is None else base + ".weight"
+        if gguf is None:
+            unmapped.append(mname)
+        elif gguf not in gguf_ne0:
+            unmapped.append(f"{mname} (-> {gguf}, not in the GGUF)")
+        elif isinstance(mod, nn.Embedding) or not _in_shard(gguf, layer_lo, layer_hi):
+            continue
+        elif mod.in_features != gguf_ne0[gguf]:
+            conflicts.append(f"{mname} -> {gguf} (in_features {mod.in_features}, "
+                             f"ne[0] {gguf_ne0[gguf]})")
+        else:
+            targets.append(HookTarget(mname, mod, gguf, mod.in_features))
+    if conflicts:
+        raise ValueError(f"refusing to mis-key Hessians: in_features differs from the GGUF "
+                         f"ne[0] for {'; '.join(conflicts)}")
+    return targets, unmapped
+
+
+class _InputHessians:
+    """The accumulators of one collection, keyed by GGUF name. Modules that read one and
+    the same input tensor within a forward pass (q/k/v, gate/up) share one accumulator,
+    and the product is formed once per pass (the reference forms it per module)."""
+
+    def __init__(self, device):
+        self.by_name = {}
+        self._device = device
+        # input identity -> (accumulator, the input) for the current pass; holding the
+        # input keeps its memory from being reused by a later input of the same pass, so
+        # an address names one tensor until the pass ends
+        self._inputs = {}
+
+    def new_pass(self):
+        self._inputs.clear()
+
+    def observe(self, gguf_name, x):
+        if not torch.is_floating_point(x):
+            return
+        ident = (x.device, x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.dtype)
+        known = self._inputs.get(ident)
+        if known is None:
+            acc = self.by_name.get(gguf_name)
+            if acc is None:
+                acc = HessianAccumulator(x.shape[-1], x.device if x.is_cuda else self._device)
+            acc.add(x.detach().to(acc.H.device))  # a host activation crosses once per pass
+            known = self._inputs[ident] = (acc, x)
+        if self.by_name.setdefault(gguf_name, known[0]) is not known[0]:
+            raise RuntimeError(f"{gguf_name}: shares its input with another module in one "
+                               f"batch but not in another")
+
+    @contextlib.contextmanager
+    def hooked(self, targets):
+        handles = [t.module.register_forward_hook(
+            lambda _mod, inp, _out, g=t.gguf_name: self.observe(g, inp[0])) for t in targets]
+        try:
+            yield
+        finally:
+            for h in handles:
+                h.remove()
+
+    def results(self, gguf_ne0, keep_on_device):
+        out = {}
+        for gguf_name, acc in self.by_name.items():
+            if acc.H.shape[0] != gguf_ne0[gguf_name]:
+                raise ValueError(f"{gguf_name}: the collected Hessian is {acc.H.shape[0]} wide "
+                                 f"but the GGUF ne[0] is {gguf_ne0[gguf_name]}")
+            # host results: one array per name, as the reference returns them
+            out[gguf_name] = {"H": acc.H if keep_on_device else acc.H.cpu().numpy(), "n": acc.n}
+        return out
+
+
 def collect_hessians(model, batches, gguf_ne0, arch, n_layers, layer_lo=0, layer_hi=None,
                      progress_every=16, log=print, name_map=None, keep_on_device=False):
     """Accumulate X^T X on the GPU for every hooked matmul of the layer shard
-    [layer_lo, layer_hi) over ``batches`` (coldpress/hessians.py:85-179).
+    [layer_lo, layer_hi) over ``batches`` (the interface of coldpress/hessians.py:85-179).
 
-    gguf_ne0: {GGUF tensor name (with .weight): ne0} of the target artifact; a module whose
-    GGUF name is absent is unmapped, one whose in_features differs is refused with
-    ValueError before any hook is registered. Non-block tensors (output) belong to the
-    shard that starts at layer 0. ``name_map`` ({module name: GGUF base name}) replaces the
-    built-in map of ``arch``. Modules that read one input tensor (q/k/v, gate/up) share one
-    accumulator, formed once per batch. Returns ({GGUF name: {"H": float32 [d, d], "n":
-    rows}}, unmapped module names); H is a host array, as the reference returns it, or
-    with ``keep_on_device`` the CUDA tensor (tensors sharing an input share one object)."""
-    import torch.nn as nn
+    gguf_ne0: {GGUF tensor name (with .weight): ne0} of the target artifact (plan_targets
+    says which modules are hooked, unmapped or refused). ``name_map`` ({module name: GGUF
+    base name}) replaces the built-in map of ``arch``. Returns ({GGUF name: {"H": float32
+    [d, d], "n": rows}}, unmapped module names). H is a host array of its own per name, as
+    the reference returns it; with ``keep_on_device`` it is the CUDA accumulator, and the
+    names whose modules read one input (q/k/v, gate/up) share that one tensor."""
     if layer_hi is None:
         layer_hi = n_layers
     if name_map is None:
         name_map = build_name_map(model, arch, n_layers)
-    plan, unmapped, mismatched = [], [], []
-    for mname, mod in model.named_modules():
-        if not isinstance(mod, nn.Linear):
-            continue  # an embedding lookup has no input Hessian
-        base = name_map.get(mname)
-        if base is None:
-            unmapped.append(mname)
-            continue
-        g = base + ".weight"
-        if g not in gguf_ne0:
-            unmapped.append(f"{mname} (-> {g}, absent from the GGUF)")
-            continue
-        blk = _block_of(g)
-        if not (layer_lo <= blk < layer_hi if blk >= 0 else layer_lo == 0):
-            continue
-        if mod.in_features != gguf_ne0[g]:
-            mismatched.append((mname, g, mod.in_features, gguf_ne0[g]))
-            continue
-        plan.append((mod, g))
-    if mismatched:
-        for mname, g, inf, ne0 in mismatched:
-            log(f"  SHAPE MISMATCH {mname} -> {g}: in_features={inf} ne0={ne0}")
-        raise ValueError(f"{len(mismatched)} module(s) map to a GGUF tensor with a different "
-                         f"ne[0]; refusing to mis-key a Hessian")
-    acc = {}
-    # input identity of the current forward pass -> (its accumulator, the input). Holding
-    # the input keeps its memory from being reused by a later input of the same pass, so
-    # the address identifies one tensor until the pass ends.
-    seen = {}
-    dev = torch.device("cuda", torch.cuda.current_device())
-
-    def make_hook(g):
-        def fn(mod, inp, out):
-            x = inp[0]
-            if not torch.is_floating_point(x):
-                return
-            # q/k/v (and gate/up) read one and the same input tensor: accumulate it once and
-            # share the accumulator (the reference forms the identical X^T X per module)
-            key = (x.device, x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.dtype)
-            hit = seen.get(key)
-            if hit is None:
-                a = acc.get(g)
-                if a is None:
-                    a = HessianAccumulator(x.shape[-1], x.device if x.is_cuda else dev)
-                a.add(x.detach().to(a.H.device))  # a host activation crosses once per batch
-                seen[key] = (a, x)
-            else:
-                a = hit[0]
-            if g in acc and acc[g] is not a:
-                raise RuntimeError(f"{g}: shares its input with another module in one batch "
-                                   f"but not in another")
-            acc[g] = a
-        return fn
-
-    handles = [mod.register_forward_hook(make_hook(g)) for mod, g in plan]
-    log(f"hooked {len(handles)} matmuls in layers [{layer_lo},{layer_hi}); "
-        f"{len(unmapped)} module(s) unmapped/skipped")
-    try:
-        with torch.inference_mode():
-            for c, ids in enumerate(batches):
-                seen.clear()
-                model(ids.unsqueeze(0) if ids.dim() == 1 else ids)
-                if progress_every and (c + 1) % progress_every == 0:
-                    log(f"  chunk {c + 1}")
-    finally:
-        for h in handles:
-            h.remove()
-    host = {}
-    out = {}
-    for g, a in acc.items():
-        if a.H.shape[0] != gguf_ne0[g]:
-            raise ValueError(f"{g}: collected H.shape[0]={a.H.shape[0]} != ne0={gguf_ne0[g]}")
-        if not keep_on_device and id(a) not in host:
-            host[id(a)] = a.H.cpu().numpy()
-        out[g] = {"H": a.H if keep_on_device else host[id(a)], "n": a.n}
-    return out, unmapped
+    targets, unmapped = plan_targets(model, name_map, gguf_ne0, layer_lo, layer_hi)
+    sink = _InputHessians(torch.device("cuda", torch.cuda.current_device()))
+    log(f"hessians: hooking {len(targets)} module inputs of blocks {layer_lo}..{layer_hi - 1}; "
+        f"{len(unmapped)} unmapped")
+    with sink.hooked(targets), torch.inference_mode():
+        for k, ids in enumerate(batches, 1):
+            sink.new_pass()
+            model(ids if ids.dim() > 1 else ids[None])
+            if progress_every and k % progress_every == 0:
+                log(f"hessians: {k} batches in")
+    return sink.results(gguf_ne0, keep_on_device), unmapped
 
 
 # ---------------------------------------------------------------- storage

@@ -59,6 +59,8 @@ def test_noalloc_matches_workspace_entry_twice():
         W, qw, U, order = _case(nrow, n, tt, seed)
         want = _encode(lib, _lib, tt, W, qw, U, order, noalloc=False)
         got = _encode(lib, _lib, tt, W, qw, U, order, noalloc=True)
+        # the static workspace's status word: no sweep wave gave up
+        assert lib.cp_ef_read_status(None, _lib.stream_ptr()) == _lib.CP_OK
         assert torch.equal(got[0], want[0]), (tt, nrow, n)
         assert torch.equal(got[1], want[1]), (tt, nrow, n)
 
