@@ -10,7 +10,7 @@ h2_pack / h2_expand restate the storage arithmetic of hessians.py:163-243. Pins:
 expectations of the reference's own storage tests (test_hessian_fp16.py: exact diagonal,
 off-diagonal equal to float16(float32(H)) when unscaled and within float16 epsilon, finite
 storage of a Hessian far above the float16 range, the float32-only format unchanged), which
-tests/test_oracle_gguf.py restates.
+tests/test_gguf.py (test_h2_oracle_*) restates.
 """
 import numpy as np
 

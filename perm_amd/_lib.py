@@ -167,6 +167,8 @@ def check_index(p, size, what="index", permutation=False):
     checked with device reductions and one synchronization. Returns an int32 array
     (or tensor, on p's device) with negative entries resolved; the shape is kept."""
     if isinstance(p, torch.Tensor):
+        if (p.is_floating_point() or p.is_complex() or p.dtype == torch.bool) and p.numel():
+            raise IndexError(f"{what}: indices must be integers, got {p.dtype}")
         t = p.to(torch.int64)
         if t.numel():
             lo, hi = (int(v) for v in torch.stack([t.min(), t.max()]).cpu())

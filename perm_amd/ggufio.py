@@ -53,16 +53,19 @@ def _payload(tensor, value, want_quantized):
 def reemit(src, dst, replace=None, replace_f32=None, log=print):
     """Write dst as src with some tensors' data replaced. replace: {name: container bytes}
     for block-quantized tensors; replace_f32: {name: float32 array or bytes} for F32
-    tensors (norm gains). Each replacement must have the tensor's exact byte size."""
+    tensors (norm gains). Each replacement must have the tensor's exact byte size. Names
+    that are not tensors of src are ignored (and counted in the log line), as the
+    reference's re-emit, which walks the source's tensors, ignores them."""
     reader = GGUFReader(src)
     if not read_arch(reader):
         raise ReemitError(f"{src}: no general.architecture key")
     ranges = {t.name: t for t in reader.tensors}
-    edits = []
+    edits, ignored = [], 0
     for table, quantized in ((replace or {}, True), (replace_f32 or {}, False)):
         for name, value in table.items():
             if name not in ranges:
-                raise KeyError(f"{name}: no such tensor in {src}")
+                ignored += 1
+                continue
             edits.append((ranges[name].data_offset, _payload(ranges[name], value, quantized)))
     del reader, ranges  # release the map before the copy
     if os.path.abspath(src) != os.path.abspath(dst):
@@ -71,7 +74,8 @@ def reemit(src, dst, replace=None, replace_f32=None, log=print):
         for offset, blob in sorted(edits):
             f.seek(offset)
             f.write(blob)
-    log(f"reemit: {src} -> {dst}, {len(edits)} tensor payload(s) replaced")
+    log(f"reemit: {src} -> {dst}, {len(edits)} tensor payload(s) replaced"
+        + (f", {ignored} name(s) not in the source ignored" if ignored else ""))
 
 
 def _kv_table(reader):

@@ -122,6 +122,14 @@ def test_reemit_replace_quant_tensor(tmp_path):
         ggufio.reemit(a, b, replace={"blk.0.weight": raw2.reshape(-1)[:-1]}, log=lambda *_: None)
     with pytest.raises(AssertionError):
         ggufio.reemit(a, b, replace={"norm.weight": np.zeros(64, np.uint8)}, log=lambda *_: None)
+    # a superset dict: names that are not tensors of the source are ignored, as the
+    # reference's re-emit (which walks the source's tensors) ignores them
+    said = []
+    ggufio.reemit(a, b, replace={"blk.0.weight": raw2.reshape(-1), "blk.9.absent.weight": raw2},
+                  replace_f32={"absent_norm.weight": np.zeros(4, np.float32)}, log=said.append)
+    assert np.array_equal([t for t in GGUFReader(b).tensors if t.name == "blk.0.weight"][0].data,
+                          raw2)
+    assert "1 tensor payload(s) replaced, 2 name(s) not in the source ignored" in said[-1]
 
 
 def test_reemit_keeps_any_layout_and_touches_only_the_payload(tmp_path):

@@ -56,6 +56,36 @@ def test_factor_matches_closed_form(ef, n):
     assert np.abs(U.T @ U @ Hd - np.eye(n)).max() < 1e-9
 
 
+@pytest.mark.parametrize("n,N,kind", [(3072, 65536, "student-t"), (4096, 131072, "outliers"),
+                                      (14336, 131072, "outliers")])
+def test_factor_matches_library_at_config_sizes(ef, n, N, kind):
+    """E1 at the benchmark configurations' sizes (the Qwen3-0.6B down_in space, the
+    Llama-3-8B spaces with 0.5 % of channels x50): U from the act-ordered Hessian against
+    the float64 closed form of coldpress/ef.py:60-78 -- inv, symmetrize, Cholesky -- taken
+    from torch.linalg on the device (a library routine, none of this library's kernels).
+    The bound is on max |dU| / max |U|; float32, which the sweep consumes, resolves 6e-8."""
+    from perm_amd import workloads as wl
+    from perm_amd.hessians import xtx_accumulate
+    _say(f"factor vs torch.linalg n={n} N={N} {kind}")
+    H = xtx_accumulate(wl.family_activations(kind, N, n, seed=n))
+    order = ef.act_order_dev(H)
+    U, used = ef.factor_dev(H, order, out_dtype=torch.float64)
+    assert used == [0.01]
+    o = order.long()
+    Hp = H.double()[o][:, o]
+    lam = 0.01 * float(torch.diagonal(Hp).mean()) + 1e-8
+    Hp.diagonal().add_(lam)
+    Hinv = torch.linalg.inv(Hp)
+    del Hp
+    Hinv = (Hinv + Hinv.T) / 2
+    Uref = torch.linalg.cholesky(Hinv).T
+    del Hinv
+    rel = float((U - Uref).abs().max() / Uref.abs().max())
+    _say(f"  max |dU| / max |U| = {rel:.2e}")
+    assert torch.equal(U, torch.triu(U))
+    assert rel < 1e-8
+
+
 def _np_tree(v):
     """One pairwise tree over all of v (numpy's order only up to 8192 values)."""
     n = len(v)

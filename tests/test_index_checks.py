@@ -26,6 +26,13 @@ def test_check_index_ranges_and_negative_entries():
     assert t.dtype == torch.int32 and t.tolist() == [2, 2, 0]
     with pytest.raises(IndexError):
         _lib.check_index(torch.tensor([3]), 3)
+    # non-integer index tensors are refused, as the numpy branch refuses them, not truncated
+    for bad in (torch.tensor([0.7, 1.0]), torch.tensor([0, 1], dtype=torch.float16),
+                torch.tensor([1 + 0j]), torch.tensor([True, False])):
+        with pytest.raises(IndexError, match="integers"):
+            _lib.check_index(bad, 4)
+    with pytest.raises(IndexError, match="integers"):
+        _lib.check_index(np.array([True, False]), 4)
 
 
 def test_check_index_permutations():

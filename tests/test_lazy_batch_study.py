@@ -1,27 +1,21 @@
-"""Study, not a test (pytest does not collect it): would a right-looking lazy-batch EF,
-whose cross-block update is one float32 GEMM per block (the form an MFMA kernel takes),
-keep the reference's codes? Run from the repository root:
-
-    python tests/lazy_batch_agreement.py
+"""Would a right-looking lazy-batch EF, whose cross-block update is one float32 GEMM per
+block (the form an MFMA kernel takes), keep the reference's codes? (CPU only.)
 
 The emulation keeps the in-block updates exact (coldpress/ef.py:198-214: one float32
 subtraction of a float32 product per element, in the visiting order) and replaces the
 cross-block part by W[:, b1:] -= E_blk @ U[blk, b1:] in float32 (BLAS accumulation order),
-which is what an MFMA accumulation computes up to its own summation order. It prints the
-fraction of stored codes equal to the exact oracle's and the relative change of
-tr(dW H dW^T), on the single-Linear workload (1024 columns, 256 rows), for Q2_K and Q4_K,
-with and without an importance vector, at block sizes 32 and 128.
+which is what an MFMA accumulation computes up to its own summation order. The test
+measures the fraction of stored codes equal to the exact oracle's and the relative change
+of tr(dW H dW^T), on the single-Linear workload (1024 columns, 256 rows), for Q2_K and
+Q4_K, with and without an importance vector, at block sizes 32 and 128, and asserts the
+finding that rules the form out as the default: agreement stays below the 99.9 % gate on
+three of the four cases at both block sizes (numpy's BLAS sets the exact percentages;
+the reordering flips near-tie codes whatever the order).
 """
-import os
-import sys
-
 import numpy as np
 
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-sys.path.insert(0, ROOT)
-
-from oracle import ef_oracle as E, kquant_oracle as K  # noqa: E402
-from perm_amd.workloads import single_linear  # noqa: E402
+from oracle import ef_oracle as E, kquant_oracle as K
+from perm_amd.workloads import single_linear
 
 F32 = np.float32
 
@@ -70,10 +64,11 @@ def ef_lazy(x, tt, qw, U, order, B, n_iter=2):
     return raw, K.DEQUANTIZE[tt](raw, n)
 
 
-def main():
+def test_gemm_cross_block_update_misses_the_code_gate():
     W, _X, H = single_linear(seed=0, nrow=256, n=1024)
     order = E.act_order(H, stable=True)
     U = E.inv_upper_factor(H[np.ix_(order, order)]).astype(F32)
+    agree = {}
     for tt in ("Q2_K", "Q4_K"):
         for qname, qw in (("imatrix", np.diag(H).astype(F32)), ("none", None)):
             raw0, rec0 = E.ef_encode(W, tt, qw, H, U=U, order=order)
@@ -81,11 +76,12 @@ def main():
             e0 = E.h_weighted_err(W, rec0, H)
             for B in (32, 128):
                 raw1, rec1 = ef_lazy(W, tt, qw, U, order, B)
-                agree = (K.stored_codes(tt, raw1) == c0).mean()
+                a = (K.stored_codes(tt, raw1) == c0).mean()
                 e1 = E.h_weighted_err(W, rec1, H)
-                print(f"{tt} qw={qname} block {B}: codes agree {agree * 100:.3f}%  "
+                agree[tt, qname, B] = a
+                print(f"{tt} qw={qname} block {B}: codes agree {a * 100:.3f}%  "
                       f"tr err rel diff {abs(e1 - e0) / e0:.2e}", flush=True)
-
-
-if __name__ == "__main__":
-    main()
+                assert 0.98 < a < 1.0  # close, never identical
+    for case in (("Q2_K", "none"), ("Q4_K", "imatrix"), ("Q4_K", "none")):
+        for B in (32, 128):
+            assert agree[(*case, B)] < 0.999, (case, B, agree[(*case, B)])
