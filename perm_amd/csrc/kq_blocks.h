@@ -166,6 +166,9 @@ __device__ __forceinline__ void kq_encode_block(const float* __restrict__ x,
   __shared__ float s_sq[IMAT ? kWavesPerBlock : 1][IMAT ? S * 256 : 1];
   __shared__ uint8_t s_codes[kWavesPerBlock][S * 256];
   __shared__ SbFields s_f[kWavesPerBlock][S];
+  // the make_qp_quants problems of the weighted affine types: two per superblock
+  constexpr bool kQp = IMAT && (TT == CP_Q2_K || TT == CP_Q4_K || TT == CP_Q5_K);
+  __shared__ QpStage<G, kQp ? 2 * kWavesPerBlock * S : 2> s_qp;
 
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int g = lane % G, sl = lane / G;
@@ -224,14 +227,17 @@ __device__ __forceinline__ void kq_encode_block(const float* __restrict__ x,
     float scale, mn;
     int sc_i, mn_i;
     float d, dmin;
+    AffineFit fit;
     if constexpr (IMAT) {
-      fit_affine<16>(xv, wt, 3, -0.9f, 0.05f, 36, false, true, &scale, &mn, L);
+      fit = fit_affine<16>(xv, wt, kQkxQ2Imat, false, true);
       float sw = psum<16>(wt);
-      gfit_nonneg_pair<16>(scale, mn, sw, 15, g, &d, &sc_i, &dmin, &mn_i);
+      gfit_nonneg_pair<16>(fit.scale, fit.min, sw, 15, g, wv * S + sl, s_qp, &d, &sc_i, &dmin, &mn_i);
     } else {
 #pragma unroll
       for (int i = 0; i < 16; ++i) wt[i] = fabsf(xv[i]);
-      fit_affine<16>(xv, wt, 3, -0.5f, 0.1f, 15, true, false, &scale, &mn, L);
+      fit = fit_affine<16>(xv, wt, kQkxQ2Ref, true, false);
+      scale = fit.scale;
+      mn = fit.min;
       float smax = gmax<16>(scale), mmax = gmax<16>(mn);
       bool ps = smax > 0.0f, pm = mmax > 0.0f;
       float is = ps ? 15.0f / smax : 0.0f, im = pm ? 15.0f / mmax : 0.0f;
@@ -245,6 +251,8 @@ __device__ __forceinline__ void kq_encode_block(const float* __restrict__ x,
     if (dl != 0.0f) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) L[i] = clampi(rint_magic((xv[i] + ml) / dl), 0, 3);
+    } else {
+      affine_final_codes<16>(xv, fit, 3, L);  // the search's codes stay where dl == 0
     }
     F.a[g] = (uint8_t)((sc_i & 0xF) | (mn_i & 0xF) << 4);
     if (g == 0) {
@@ -281,10 +289,14 @@ __device__ __forceinline__ void kq_encode_block(const float* __restrict__ x,
     constexpr int TOP = TT == CP_Q5_K ? 31 : 15;
     float scale, mn, d, dmin;
     int Ls, Lm;
+    AffineFit fit;
     if constexpr (IMAT) {
-      fit_affine<32>(xv, wt, TOP, -0.9f, 0.05f, 36, false, true, &scale, &mn, L);
+      if constexpr (TT == CP_Q5_K)
+        fit = fit_affine<32>(xv, wt, kQkxQ5Imat, false, true);
+      else
+        fit = fit_affine<32>(xv, wt, kQkxQ4Imat, false, true);
       float sw = psum<32>(wt);
-      gfit_nonneg_pair<8>(scale, mn, sw, 63, g, &d, &Ls, &dmin, &Lm);
+      gfit_nonneg_pair<8>(fit.scale, fit.min, sw, 63, g, wv * S + sl, s_qp, &d, &Ls, &dmin, &Lm);
       if constexpr (TT == CP_Q5_K) {
         Ls = Ls < 63 ? Ls : 63;
         Lm = Lm < 63 ? Lm : 63;
@@ -297,9 +309,11 @@ __device__ __forceinline__ void kq_encode_block(const float* __restrict__ x,
 #pragma unroll
       for (int i = 0; i < 32; ++i) wt[i] = av + fabsf(xv[i]);
       if constexpr (TT == CP_Q5_K)
-        fit_affine<32>(xv, wt, TOP, -0.5f, 0.1f, 15, false, false, &scale, &mn, L);
+        fit = fit_affine<32>(xv, wt, kQkxQ5Ref, false, false);
       else
-        fit_affine<32>(xv, wt, TOP, -1.0f, 0.1f, 20, false, false, &scale, &mn, L);
+        fit = fit_affine<32>(xv, wt, kQkxQ4Ref, false, false);
+      scale = fit.scale;
+      mn = fit.min;
       float smax = gmax<8>(scale), mmax = gmax<8>(mn);
       float is = smax > 0.0f ? 63.0f / smax : 0.0f;
       float im = mmax > 0.0f ? 63.0f / mmax : 0.0f;
@@ -316,6 +330,8 @@ __device__ __forceinline__ void kq_encode_block(const float* __restrict__ x,
     if (dl != 0.0f) {
 #pragma unroll
       for (int i = 0; i < 32; ++i) L[i] = clampi(rint_magic((xv[i] + ml) / dl), 0, TOP);
+    } else {
+      affine_final_codes<32>(xv, fit, TOP, L);  // the search's codes stay where dl == 0
     }
     F.a[g] = (uint8_t)Ls;
     F.a[8 + g] = (uint8_t)Lm;

@@ -1,7 +1,7 @@
 // Sub-block grid fits of the k-quant encoders, on the device.
 //
 // In-lane fits (one lane owns one sub-block of N values in registers):
-//   fit_affine<N>       make_qkx2 / make_qkx3 search      coldpress/kquant.py:42-94
+//   fit_affine<N, NUMS> make_qkx2 / make_qkx3 search      coldpress/kquant.py:42-94
 //   fit_signed<N>       make_qx_quants, rmse_type 1        coldpress/kquant.py:97-133
 //   fit_signed_descent  make_q3_quants                     coldpress/kquant.py:136-179
 // Cross-lane fits (one lane owns one element of a G-wide vector of super-block
@@ -32,10 +32,12 @@ __device__ __forceinline__ float affine_err(const float (&x)[N], const float (&w
 }
 
 // Codes of one candidate, clip(nearest_int(inv * (x - lo)), 0, nmax), as floats.
-// fast: the same codes through a float round trip of the 1.5*2^23 magic add and one
-// v_med3_f32, valid when every inv * (x - lo) is finite and inside (-2^22, 2^22 - 1/2)
-// (there the magic add rounds to the nearest integer, ties to even, in both forms;
-// outside it the integer form returns a bit pattern the float form does not).
+// fast: the same codes as rint(med3(v, 0, nmax)) (v_med3_f32, v_rndne_f32), valid when
+// every v = inv * (x - lo) is finite and inside (-2^22, 2^22 - 1/2). There the magic add
+// rounds to the nearest integer, ties to even, as v_rndne_f32 does, and clipping to the
+// integer bounds first changes no result: v below 0 gives +0 either way, v above nmax
+// gives nmax either way (outside the range the integer form returns a bit pattern the
+// float form does not).
 template <int N, bool FAST>
 __device__ __forceinline__ void affine_codes(const float (&x)[N], float inv, float lo, int nmax,
                                              float (&lf)[N]) {
@@ -43,26 +45,64 @@ __device__ __forceinline__ void affine_codes(const float (&x)[N], float inv, flo
   for (int i = 0; i < N; ++i) {
     const float v = inv * (x[i] - lo);
     if constexpr (FAST)
-      lf[i] = __builtin_amdgcn_fmed3f((v + 12582912.0f) - 12582912.0f, 0.0f, (float)nmax);
+      lf[i] = __builtin_rintf(__builtin_amdgcn_fmed3f(v, 0.0f, (float)nmax));
     else
       lf[i] = (float)clampi(rint_magic(v), 0, nmax);
   }
 }
 
-// Weighted affine fit x ~ scale * L + lo, L in [0, nmax]. Returns scale and -lo
-// (the "min" the containers store); L receives the codes.
-//
-// The candidate codes depend only on the candidate's inverse scale and the running
-// min, so the search keeps that pair for the best candidate and forms its codes
-// once at the end. A candidate takes the float form of the codes when, on every
-// lane of the wave, x is finite, inv is finite and inv * (min(x) - lo) > -2^22:
-// inv > 0 and rounding is monotonic, so every inv * (x_i - lo) then lies between
-// that bound and inv * (hi - lo), which is at most about nmax + 1.
+// The candidate numerators (rmin + rdelta * step) + nmax, step = 0 .. NSTEP, of a
+// make_qkx search, evaluated at compile time in float32 with every operation rounded
+// once, as the device would evaluate them (rmin = RMIN100 / 100, rdelta = RDELTA100 /
+// 100, each the float nearest the decimal, as the reference's np.float32 constants).
+// The search reads them from constant memory with scalar loads.
+template <int NMAX, int RMIN100, int RDELTA100, int NSTEP>
+struct QkxNums {
+  static constexpr int kNmax = NMAX, kSteps = NSTEP;
+  float v[NSTEP + 1];
+  constexpr QkxNums() : v() {
+    const float rmin = (float)RMIN100 / 100.0f, rdelta = (float)RDELTA100 / 100.0f;
+    for (int s = 0; s <= NSTEP; ++s) v[s] = (rmin + rdelta * (float)s) + (float)NMAX;
+  }
+};
+// the five searches of the encoders (kquant.py:359-360, :385-386, :518-520, :541-542, :593)
+static __constant__ const QkxNums<3, -90, 5, 36> kQkxQ2Imat = QkxNums<3, -90, 5, 36>();
+static __constant__ const QkxNums<3, -50, 10, 15> kQkxQ2Ref = QkxNums<3, -50, 10, 15>();
+static __constant__ const QkxNums<15, -90, 5, 36> kQkxQ4Imat = QkxNums<15, -90, 5, 36>();
+static __constant__ const QkxNums<15, -100, 10, 20> kQkxQ4Ref = QkxNums<15, -100, 10, 20>();
+static __constant__ const QkxNums<31, -90, 5, 36> kQkxQ5Imat = QkxNums<31, -90, 5, 36>();
+static __constant__ const QkxNums<31, -50, 10, 15> kQkxQ5Ref = QkxNums<31, -50, 10, 15>();
+
+// Result of fit_affine: the scale, -lo (the "min" the containers store), and the
+// inverse scale and offset whose codes are the best (affine_final_codes forms them).
+struct AffineFit {
+  float scale, min;
+  float inv, lo;
+  bool dead;
+};
+
+// clip(nearest_int(inv * (x - lo)), 0, nmax) of the best candidate (0 for a dead block).
 template <int N>
-__device__ __forceinline__ void fit_affine(const float (&x)[N], const float (&w)[N], int nmax,
-                                           float rmin, float rdelta, int nstep, bool mad,
-                                           bool strict_dead, float* scale_out, float* min_out,
-                                           int (&L)[N]) {
+__device__ __forceinline__ void affine_final_codes(const float (&x)[N], const AffineFit& f,
+                                                   int nmax, int (&L)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) L[i] = f.dead ? 0 : clampi(rint_magic(f.inv * (x[i] - f.lo)), 0, nmax);
+}
+
+// Weighted affine fit x ~ scale * L + lo, L in [0, NUMS::kNmax], over the candidates of
+// the table NUMS (its numerators, step = 0 .. kSteps). Returns scale, -lo and the best
+// candidate's (inverse scale, offset), whose codes depend on that pair alone: the search
+// keeps the pair and the caller forms the codes with affine_final_codes only where it
+// needs them (the encoders requantize every sub-block whose grid step is non-zero).
+//
+// A candidate takes the float form of the codes when, on every lane of the wave, x is
+// finite, inv is finite and inv * (min(x) - lo) > -2^22: inv > 0 and rounding is
+// monotonic, so every inv * (x_i - lo) then lies between that bound and
+// inv * (hi - lo), which is at most about nmax + 1.
+template <int N, class NUMS>
+__device__ __forceinline__ AffineFit fit_affine(const float (&x)[N], const float (&w)[N],
+                                                const NUMS& nums, bool mad, bool strict_dead) {
+  constexpr int nmax = NUMS::kNmax;
   float hi = x[0], lo = x[0];
   bool fin = isfinite(x[0]);
 #pragma unroll
@@ -87,10 +127,10 @@ __device__ __forceinline__ void fit_affine(const float (&x)[N], const float (&w)
   float best = affine_err<N>(x, w, lf, scale, lo, mad);
   float best_inv = inv, best_lo = lo;  // the pair whose codes are the best so far
 
-  for (int step = 0; step <= nstep; ++step) {
+  for (int step = 0; step <= NUMS::kSteps; ++step) {
     float span = hi - lo;
     span = span > 0.0f ? span : 1.0f;
-    const float num = (rmin + rdelta * (float)step) + (float)nmax;  // in div_box
+    const float num = nums.v[step];  // in div_box
     float inv_c;
     if (__all(div_box(span)))
       inv_c = div_by(num, span, div_recip(span));
@@ -143,11 +183,7 @@ __device__ __forceinline__ void fit_affine(const float (&x)[N], const float (&w)
       lo = m_c;
     }
   }
-#pragma unroll
-  for (int i = 0; i < N; ++i) L[i] = dead ? 0 : clampi(rint_magic(best_inv * (x[i] - best_lo)), 0, nmax);
-  if (dead) scale = 0.0f;
-  *scale_out = scale;
-  *min_out = -lo;
+  return AffineFit{dead ? 0.0f : scale, -lo, best_inv, best_lo, dead};
 }
 
 // Symmetric signed fit x ~ scale * L, L in [-nmax, nmax-1]; weights w (pass
@@ -282,13 +318,6 @@ __device__ __forceinline__ float fit_signed_descent16(const float (&x)[16], int 
   return scale;
 }
 
-// Gather the G values of a lane group into every lane's registers.
-template <int G>
-__device__ __forceinline__ void ggather(float v, float (&out)[G]) {
-#pragma unroll
-  for (int i = 0; i < G; ++i) out[i] = __shfl(v, i, G);
-}
-
 // make_qp_quants over a G-lane vector (lane g holds x[g], w[g]). The candidate
 // search runs lane-parallel with butterfly sums. The descent is sequential, so
 // every lane replays it on gathered copies. Returns d; *Lout receives this
@@ -345,41 +374,65 @@ __device__ __forceinline__ float nonneg_descent(const float (&xs)[G], const floa
   return d;
 }
 
-// make_qp_quants for two G-vectors at once (the super-block scales and mins):
-// lanes g < G/2 replay the descent for ``a``, lanes g >= G/2 for ``b``, halving
-// the sequential part. Returns this lane's (d_a, La) and (d_b, Lb).
-template <int G>
+// The make_qp_quants problems of one workgroup, staged in LDS: P vectors of G values
+// (two per superblock, its scales then its mins, sharing one weight vector), the
+// candidate search's inverse scale and dead flag of each, and the descent's results.
+// Rows are padded to G + 1 floats, so the lanes of the descent, one row each, read
+// distinct banks.
+template <int G, int P>
+struct QpStage {
+  float x[P][G + 1];
+  float w[P / 2][G + 1];
+  float inv[P];
+  int dead[P];
+  float d[P];
+  uint8_t L[P][G];
+};
+
+// make_qp_quants for the two G-vectors of every superblock of the workgroup (the
+// super-block scales and mins; group ``grp`` of the workgroup's P / 2 superblocks, this
+// lane holding element g of a, b and their weights w). The candidate search runs
+// lane-parallel with butterfly sums in each lane group. The coordinate descent is
+// sequential along a vector, so one lane per vector runs it: lanes 0 .. P - 1 of the
+// workgroup's first wave (P <= 64), instead of every lane of a group replaying its
+// group's descent. Every wave of the workgroup must call this (two barriers).
+// Returns this lane's (d_a, La) and (d_b, Lb).
+template <int G, int P>
 __device__ __forceinline__ void gfit_nonneg_pair(float a, float b, float w, int nmax, int g,
-                                                 float* da, int* La, float* db, int* Lb) {
+                                                 int grp, QpStage<G, P>& st, float* da, int* La,
+                                                 float* db, int* Lb) {
+  static_assert(P <= 64, "one lane per vector in the first wave");
   float inv_a, inv_b;
   bool dead_a, dead_b;
   gfit_nonneg_search<G>(a, w, nmax, &inv_a, &dead_a);
   gfit_nonneg_search<G>(b, w, nmax, &inv_b, &dead_b);
-  float as[G], bs[G], ws[G];
-  ggather<G>(a, as);
-  ggather<G>(b, bs);
-  ggather<G>(w, ws);
-  const bool first = g < G / 2;
-  float xs[G];
-#pragma unroll
-  for (int i = 0; i < G; ++i) xs[i] = first ? as[i] : bs[i];
-  float Lf[G];
-  float d = nonneg_descent<G>(xs, ws, first ? inv_a : inv_b, first ? dead_a : dead_b, nmax, Lf);
-  // lane 0 holds the result for a, lane G/2 the result for b
-  float mine_a = 0.0f, mine_b = 0.0f;
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-    float va = __shfl(Lf[i], 0, G);
-    float vb = __shfl(Lf[i], G / 2, G);
-    if (i == g) {
-      mine_a = va;
-      mine_b = vb;
-    }
+  st.x[2 * grp][g] = a;
+  st.x[2 * grp + 1][g] = b;
+  st.w[grp][g] = w;
+  if (g == 0) {
+    st.inv[2 * grp] = inv_a;
+    st.inv[2 * grp + 1] = inv_b;
+    st.dead[2 * grp] = dead_a;
+    st.dead[2 * grp + 1] = dead_b;
   }
-  *da = __shfl(d, 0, G);
-  *db = __shfl(d, G / 2, G);
-  *La = (int)mine_a;
-  *Lb = (int)mine_b;
+  __syncthreads();
+  const int p = (int)threadIdx.x;
+  if (p < P) {
+    float xs[G], ws[G], Lf[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      xs[i] = st.x[p][i];
+      ws[i] = st.w[p >> 1][i];
+    }
+    st.d[p] = nonneg_descent<G>(xs, ws, st.inv[p], st.dead[p] != 0, nmax, Lf);
+#pragma unroll
+    for (int i = 0; i < G; ++i) st.L[p][i] = (uint8_t)(int)Lf[i];
+  }
+  __syncthreads();
+  *da = st.d[2 * grp];
+  *db = st.d[2 * grp + 1];
+  *La = st.L[2 * grp][g];
+  *Lb = st.L[2 * grp + 1][g];
 }
 
 // make_qx_quants (rmse_type 1) over a G-lane vector with weights w: returns the
