@@ -205,6 +205,20 @@ int cp_ef_phase_ms(float* out, int nphase);
  * counterpart in the reference, like cp_ef_profile. */
 int cp_ef_last_sweep(int* rows_per_stripe, int* waves);
 
+/* ---- encode statistics (coldpress/ef.py:298-304) ---- */
+
+/* Workspace bytes of cp_sq_err_sum for [nrow, n] arrays (4 bytes per 8192 terms). */
+size_t cp_sq_err_ws_bytes(int64_t nrow, int64_t n);
+
+/* out[0] (device float32) = (((a - b) ** 2) * w).sum() for float32 a, b [nrow, n] and
+ * w [n] broadcast over rows (NULL: ones), with numpy's rounding of every term and its
+ * summation order for the full reduction of a contiguous array: 8192-term chunks of
+ * the flattened terms, each summed pairwise, the chunk sums added left to right from
+ * 0.0. Replaces e_base / e_ours of encode_gguf's err-vs-stock statistic
+ * (coldpress/ef.py:298-304). Bit-identical. n % 4 == 0; 16-byte aligned a, b, w. */
+int cp_sq_err_sum(const float* a, const float* b, const float* w, int64_t nrow, int64_t n,
+                  float* out, void* ws, size_t ws_bytes, void* stream);
+
 /* ---- Hessian accumulation (coldpress/hessians.py:137-154) ---- */
 
 /* H [d, d] float32 += X^T X for X [N, d] row-major (x_dtype 0 = float32,

@@ -183,3 +183,66 @@ def h_weighted_err(W, What, H):
     """tr((What - W) H (What - W)^T) in float64 (tests/test_ef_synthetic.py:20-22)."""
     D = (What - W).astype(np.float64)
     return float(np.einsum("ri,ij,rj->", D, H, D))
+
+
+# ---------------------------------------------------------------- err-vs-stock statistic
+
+NP_CHUNK = 8192  # elements per inner-loop call of numpy's full reduction of a contiguous array
+
+
+def pairwise_f32(a):
+    """numpy's float32 pairwise sum of a 1-D array (its pairwise_sum: under 8 values left
+    to right, up to 128 values eight interleaved accumulators and their tree plus the
+    remainder, above that split at n/2 rounded down to a multiple of 8)."""
+    n = len(a)
+    if n < 8:
+        s = F32(-0.0)
+        for v in a:
+            s = F32(s + v)
+        return s
+    if n <= 128:
+        r = a[:8].astype(F32).copy()
+        m = n - n % 8
+        for i in range(8, m, 8):
+            r = (r + a[i:i + 8]).astype(F32)
+        s = F32(F32(F32(r[0] + r[1]) + F32(r[2] + r[3])) + F32(F32(r[4] + r[5]) + F32(r[6] + r[7])))
+        for i in range(m, n):
+            s = F32(s + a[i])
+        return s
+    n2 = n // 2
+    n2 -= n2 % 8
+    return F32(pairwise_f32(a[:n2]) + pairwise_f32(a[n2:]))
+
+
+def full_sum_f32(a):
+    """``a.sum()`` of a contiguous float32 array with no axis, in numpy's order: the
+    flattened array in chunks of 8192 elements, each summed pairwise, the chunk sums
+    added left to right from 0.0. Full chunks are evaluated vectorized (64 leaves of 128,
+    eight interleaved accumulators each, then a balanced tree)."""
+    f = np.ascontiguousarray(a, dtype=F32).reshape(-1)
+    nfull = len(f) // NP_CHUNK
+    total = F32(0.0)
+    if nfull:
+        leaves = f[:nfull * NP_CHUNK].reshape(nfull, 64, 16, 8)
+        r = leaves[:, :, 0, :].copy()
+        for k in range(1, 16):
+            r = (r + leaves[:, :, k, :]).astype(F32)
+        s = ((r[..., 0] + r[..., 1]) + (r[..., 2] + r[..., 3])) + \
+            ((r[..., 4] + r[..., 5]) + (r[..., 6] + r[..., 7]))
+        while s.shape[1] > 1:
+            s = (s[:, 0::2] + s[:, 1::2]).astype(F32)
+        for v in s[:, 0]:
+            total = F32(total + v)
+    if len(f) % NP_CHUNK:
+        total = F32(total + pairwise_f32(f[nfull * NP_CHUNK:]))
+    return total
+
+
+def sq_err_sum(recon, x, w):
+    """(((recon - x) ** 2) * w).sum() of coldpress/ef.py:299-300 (float32 terms, numpy's
+    summation order); w [n] broadcast over rows, None for ones."""
+    d = (np.asarray(recon, F32) - np.asarray(x, F32)).astype(F32)
+    t = (d * d).astype(F32)
+    if w is not None:
+        t = (t * np.asarray(w, F32)).astype(F32)
+    return full_sum_f32(t)

@@ -101,6 +101,8 @@ SIGNATURES = {
     "cp_col_sq_sums": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "cp_col_log_rms": (_i32, [_vp, _i32, _i64, _i64, _i64, _vp, _vp, _sz, _vp]),
     "cp_check_division": (_i32, [_i64, ctypes.c_uint64, _vp, _vp]),
+    "cp_sq_err_ws_bytes": (_sz, [_i64, _i64]),
+    "cp_sq_err_sum": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _sz, _vp]),
 }
 
 

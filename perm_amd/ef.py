@@ -339,12 +339,18 @@ def _weights_f32(t):
     raise ValueError(f"{t.name}: source weights of type {name} are not float")
 
 
-def _stat_err_dev(recon, x, w):
-    """(((recon - x) ** 2) * w).sum() of coldpress/ef.py:299-300 as a float64 device
-    scalar: the float32 terms, summed in float64 (diagnostic; within ~1e-6 relative of
-    the reference's float32 pairwise total)."""
-    d = recon - x
-    return ((d * d) * w).to(torch.float64).sum()
+def sq_err_sum_dev(recon, x, w=None):
+    """(((recon - x) ** 2) * w).sum() of coldpress/ef.py:299-300 as a float32 device
+    scalar, bit-identical to numpy's (the same terms, its summation order; cp_sq_err_sum).
+    recon, x: contiguous float32 [nrow, n] CUDA tensors; w: float32 [n] or None (ones)."""
+    lib = _lib.load()
+    nrow, n = x.shape
+    out = torch.empty(1, dtype=torch.float32, device=x.device)
+    nbytes = lib.cp_sq_err_ws_bytes(nrow, n)
+    ws = _lib.workspace(nbytes, x.device) if nbytes else None
+    _lib.check(lib.cp_sq_err_sum(_lib.ptr(recon), _lib.ptr(x), _lib.ptr(w), nrow, n, _lib.ptr(out),
+                                 _lib.ptr(ws), nbytes, _lib.stream_ptr()))
+    return out[0]
 
 
 
@@ -510,9 +516,8 @@ def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, per
             if raw is None:
                 raw, recon = res[name]
             base = gkq.dequantize_dev(tt, gkq.quantize_dev(tt, x, qd), x.shape[1])
-            w = qd if qd is not None else torch.ones(x.shape[1], dtype=torch.float32,
-                                                      device=x.device)
-            errs.append(torch.stack([_stat_err_dev(base, x, w), _stat_err_dev(recon, x, w)]))
+            # w: qw, or the reference's ones (a product by 1.0 changes no term)
+            errs.append(torch.stack([sq_err_sum_dev(base, x, qd), sq_err_sum_dev(recon, x, qd)]))
             raws.append(raw.reshape(-1))
         err_host = torch.stack(errs).cpu().tolist() if errs else []
         raw_host = torch.cat(raws).cpu().numpy() if raws else None

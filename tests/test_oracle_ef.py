@@ -282,3 +282,37 @@ def test_hessian_oracle_closed_form():
     assert Ho.rel_fro(Ht, H64) < 1e-6
     Hb, cnt = Ho.accumulate([X[:1000], X[1000:]])
     assert cnt == 2048 and Ho.rel_fro(Hb, H64) < 1e-12
+
+
+@pytest.mark.parametrize("shape", [(1, 4), (1, 7), (3, 40), (5, 333), (3, 1000), (2, 4096),
+                                   (7, 3072), (100, 256), (9, 8192), (2, 10000), (3, 24581),
+                                   (517, 1024), (1024, 3072)])
+def test_sq_err_sum_is_numpys_sum(shape):
+    """The err-vs-stock statistic's order (coldpress/ef.py:299-300): the oracle's chunked
+    pairwise model against numpy's own float32 .sum() of the same terms, bit for bit, for
+    totals under one 8192-term chunk, exact multiples, partial last chunks and rows that
+    are not multiples of a 128-term leaf; plain left-to-right or one tree over all terms
+    gives other bits on some of these."""
+    rng = np.random.default_rng(shape[0] * 7919 + shape[1])
+    x = (rng.standard_normal(shape) ** 3).astype(np.float32)
+    r = (x + rng.standard_normal(shape).astype(np.float32) * 0.1).astype(np.float32)
+    w = np.abs(rng.standard_normal(shape[1])).astype(np.float32)
+    for ww in (w, None):
+        want = (((r - x) ** 2) * (ww if ww is not None else np.ones(shape[1], np.float32))).sum()
+        got = E.sq_err_sum(r, x, ww)
+        assert np.float32(got).tobytes() == want.tobytes(), (shape, got, want)
+
+
+def test_sq_err_sum_order_is_not_a_plain_sum():
+    """A planted mistake the model must not admit: summing the chunks' terms in one
+    sequential pass (or one pairwise tree over everything) differs from numpy's result
+    on this input, so the test above distinguishes the orders."""
+    rng = np.random.default_rng(5)
+    t = (rng.standard_normal(3 * 8192 + 1000) ** 3).astype(np.float32)
+    want = t.sum()
+    seq = np.float32(0.0)
+    for v in t:
+        seq = np.float32(seq + v)
+    assert seq.tobytes() != want.tobytes()
+    assert np.float32(E.pairwise_f32(t)).tobytes() != want.tobytes()
+    assert np.float32(E.full_sum_f32(t)).tobytes() == want.tobytes()
