@@ -320,42 +320,74 @@ __global__ __launch_bounds__(HNT) void hess_bf16_tri_kernel(const HessJobs jobs,
       }
 }
 
-// Finishes a bf16 accumulation over 64 x 64 blocks (bi, bj) of the lower triangle
-// (blockIdx.z is the job): with part, each entry (i, j <= i) becomes
-// H + (p_0 + p_1 + ... + p_{splits-1}), the row splits' tiles summed in split
-// order; then the block's entries are written to the mirror position (j, i) as
-// well, through LDS, so H leaves symmetric. H's upper triangle is never read.
+// Finishes a bf16 accumulation over the 64 x 64 blocks (bi, bj), bj <= bi, of the lower
+// triangle, one workgroup each (blockIdx.x: the job's lower blocks in row order,
+// blockIdx.y: the job). With part, each entry (i, j) becomes H + (p_0 + p_1 + ... +
+// p_{splits-1}), the row splits' tiles summed in split order; then the block is written
+// to the mirror position (j, i) as well, through LDS, so H leaves symmetric. Thread t
+// covers 4 consecutive columns (16-byte accesses; d % 4 == 0, so a 4-column group is
+// wholly inside or outside d) of rows t / 16 + 16 q. A diagonal block's entries above
+// the diagonal are first written with the sums of their own (meaningless) positions and
+// then overwritten by the mirror after the barrier, so its float4 stores need no mask;
+// the mirror stores mask the entries on and below the diagonal. H's upper triangle is
+// never used.
 __global__ __launch_bounds__(256) void hess_tri_reduce_kernel(const HessJobs jobs, int d, int ntiles,
                                                               int splits,
                                                               const float* __restrict__ part) {
-  float* __restrict__ H = jobs.H[blockIdx.z];
+  float* __restrict__ H = jobs.H[blockIdx.y];
   __shared__ float tl[64][65];
-  const int bi = blockIdx.y, bj = blockIdx.x;  // lower block: rows bi, columns bj
-  if (bj > bi) return;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int j = bj * 64 + tx;
+  int bi = (int)((sqrtf(8.0f * (float)blockIdx.x + 1.0f) - 1.0f) * 0.5f);
+  while (bi * (bi + 1) / 2 > (int)blockIdx.x) --bi;
+  while ((bi + 1) * (bi + 2) / 2 <= (int)blockIdx.x) ++bi;
+  const int bj = (int)blockIdx.x - bi * (bi + 1) / 2;
+  const int cg = threadIdx.x & 15, rt = threadIdx.x >> 4;
+  const int j = bj * 64 + 4 * cg;
   const int tj = j / BT;
   const int64_t slot = (int64_t)ntiles * (BT * BT);  // floats between one split's tiles
-  for (int r = ty; r < 64; r += 4) {
-    const int i = bi * 64 + r;
-    if (i >= d || j >= d || j > i) continue;
-    float h = H[(int64_t)i * d + j];
-    if (part) {
+  const float* pj = part ? part + (int64_t)blockIdx.y * splits * slot : nullptr;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = rt + 16 * q, i = bi * 64 + r;
+    if (i >= d || j >= d) continue;
+    float4 h = *reinterpret_cast<const float4*>(H + (int64_t)i * d + j);
+    if (pj) {
       const int ti = i / BT;
-      const float* p = part + (int64_t)blockIdx.z * splits * slot +
-                       (int64_t)(ti * (ti + 1) / 2 + tj) * (BT * BT) + (i % BT) * BT + (j % BT);
-      float s = p[0];
-      for (int k = 1; k < splits; ++k) s += p[k * slot];
-      h += s;
-      H[(int64_t)i * d + j] = h;
+      const float* p = pj + (int64_t)(ti * (ti + 1) / 2 + tj) * (BT * BT) + (i % BT) * BT + (j % BT);
+      float4 s = *reinterpret_cast<const float4*>(p);
+      for (int k = 1; k < splits; ++k) {
+        const float4 v = *reinterpret_cast<const float4*>(p + k * slot);
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+      }
+      h.x += s.x;
+      h.y += s.y;
+      h.z += s.z;
+      h.w += s.w;
+      *reinterpret_cast<float4*>(H + (int64_t)i * d + j) = h;
     }
-    tl[r][tx] = h;
+    tl[r][4 * cg] = h.x;
+    tl[r][4 * cg + 1] = h.y;
+    tl[r][4 * cg + 2] = h.z;
+    tl[r][4 * cg + 3] = h.w;
   }
   __syncthreads();
-  // upper block: rows bj, columns bi; entry (bj*64 + r, bi*64 + tx) = lower (bi*64 + tx, bj*64 + r)
-  for (int r = ty; r < 64; r += 4) {
-    const int i = bj * 64 + r, jj = bi * 64 + tx;
-    if (i < d && jj < d && jj > i) H[(int64_t)i * d + jj] = tl[tx][r];
+  // upper block: rows bj, columns bi; entry (bj*64 + r, bi*64 + c) = lower (bi*64 + c, bj*64 + r)
+  const int jj = bi * 64 + 4 * cg;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = rt + 16 * q, i = bj * 64 + r;
+    if (i >= d || jj >= d) continue;
+    float* dst = H + (int64_t)i * d + jj;
+    const float4 v = make_float4(tl[4 * cg][r], tl[4 * cg + 1][r], tl[4 * cg + 2][r], tl[4 * cg + 3][r]);
+    if (bi != bj || jj > i) {
+      *reinterpret_cast<float4*>(dst) = v;
+    } else {
+      if (jj + 1 > i) dst[1] = v.y;
+      if (jj + 2 > i) dst[2] = v.z;
+      if (jj + 3 > i) dst[3] = v.w;
+    }
   }
 }
 
@@ -541,7 +573,7 @@ static int hess_bf16_batch(const void* const* X, float* const* H, int count, int
     hess_bf16_tri_kernel<<<dim3(8 * per), HNT, 0, st>>>(jobs, cn, N, (int)d, ntiles, splits, rps, part);
     CP_LAUNCHED("hessian launch");
     const int tb = (int)((d + 63) / 64);
-    hess_tri_reduce_kernel<<<dim3(tb, tb, cn), 256, 0, st>>>(jobs, (int)d, ntiles, splits, part);
+    hess_tri_reduce_kernel<<<dim3(tb * (tb + 1) / 2, cn), 256, 0, st>>>(jobs, (int)d, ntiles, splits, part);
     CP_LAUNCHED("hessian reduce");
   }
   return CP_OK;
