@@ -792,6 +792,69 @@ __global__ __launch_bounds__(256) void act_order_kernel(const T* H, int n, int64
   order[z * sO + rank] = i;
 }
 
+// The same order by sorting: one workgroup per matrix sorts the pairs (key, i) of its
+// diagonal with a bitonic network in LDS, where key is an unsigned image of d_i that
+// decreases as d_i increases (-0 taken as +0, so equal values tie and fall back to the
+// index) and NaN maps to the largest key; pairs compare key first, then index, so the
+// sorted indices are the stable descending order with NaN last, by index: the ranks
+// above. npad (a power of two >= n, at most NPAD) entries are sorted, the padding
+// after every real pair. O(n log^2 n) work where the rank count is O(n^2).
+template <typename T>
+struct SortKey;
+template <>
+struct SortKey<float> {
+  typedef uint32_t K;
+  __device__ static K of(float d) {
+    if (d != d) return 0xffffffffu;
+    const uint32_t u = __float_as_uint(d == 0.0f ? 0.0f : d);
+    const uint32_t asc = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // increases with d
+    return ~asc;
+  }
+};
+template <>
+struct SortKey<double> {
+  typedef unsigned long long K;
+  __device__ static K of(double d) {
+    if (d != d) return ~0ull;
+    const unsigned long long u = __double_as_longlong(d == 0.0 ? 0.0 : d);
+    const unsigned long long asc = (u >> 63) ? ~u : (u | (1ull << 63));
+    return ~asc;
+  }
+};
+
+template <typename T, int NPAD>
+__global__ __launch_bounds__(1024) void act_order_sort_kernel(const T* H, int n, int64_t sH, int* order,
+                                                              int64_t sO, int npad) {
+  typedef typename SortKey<T>::K K;
+  __shared__ K key[NPAD];
+  __shared__ uint32_t idx[NPAD];
+  const int z = blockIdx.x, tid = threadIdx.x;
+  const T* h = H + z * sH;
+  for (int i = tid; i < npad; i += 1024) {
+    key[i] = i < n ? SortKey<T>::of(h[(int64_t)i * n + i]) : (K)~(K)0;
+    idx[i] = (uint32_t)i;
+  }
+  __syncthreads();
+  for (int k = 2; k <= npad; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int t = tid; t < npad / 2; t += 1024) {
+        const int a = ((t & ~(j - 1)) << 1) | (t & (j - 1)), b = a | j;
+        const K ka = key[a], kb = key[b];
+        const uint32_t ia = idx[a], ib = idx[b];
+        const bool gt = ka > kb || (ka == kb && ia > ib);
+        if (gt == ((a & k) == 0)) {
+          key[a] = kb;
+          key[b] = ka;
+          idx[a] = ib;
+          idx[b] = ia;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int r = tid; r < n; r += 1024) order[z * sO + r] = (int)idx[r];
+}
+
 // ---------------------------------------------------------------- driver
 
 static size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -1148,6 +1211,27 @@ int cp_act_order(const void* H, int h_dtype, int64_t n, int batch, int32_t* orde
   cp::clear_error();
   if (!H || !order || n <= 0 || batch <= 0) return cp::set_error(CP_ERR_ARG, "bad act_order arguments");
   hipStream_t st = (hipStream_t)stream;
+  // the sort in LDS where its arrays fit (float: n <= 16384, double: n <= 8192)
+  int npad = 1;
+  while (npad < n) npad <<= 1;
+  if (h_dtype != 1 && npad <= 16384) {
+    const float* Hf = (const float*)H;
+    if (npad <= 4096)
+      cp::act_order_sort_kernel<float, 4096><<<batch, 1024, 0, st>>>(Hf, (int)n, n * n, order, n, npad);
+    else
+      cp::act_order_sort_kernel<float, 16384><<<batch, 1024, 0, st>>>(Hf, (int)n, n * n, order, n, npad);
+    CP_LAUNCHED("act_order sort");
+    return CP_OK;
+  }
+  if (h_dtype == 1 && npad <= 8192) {
+    const double* Hd = (const double*)H;
+    if (npad <= 4096)
+      cp::act_order_sort_kernel<double, 4096><<<batch, 1024, 0, st>>>(Hd, (int)n, n * n, order, n, npad);
+    else
+      cp::act_order_sort_kernel<double, 8192><<<batch, 1024, 0, st>>>(Hd, (int)n, n * n, order, n, npad);
+    CP_LAUNCHED("act_order sort");
+    return CP_OK;
+  }
   dim3 grid((unsigned)((n + 255) / 256), batch);
   const size_t lds = (size_t)n * (h_dtype == 1 ? 8 : 4);
   const bool stage = lds <= 64 * 1024;

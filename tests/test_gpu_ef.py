@@ -43,6 +43,38 @@ def test_act_order_is_stable_descending(ef):
     assert np.array_equal(got, np.argsort(-d, kind="stable"))
 
 
+@pytest.mark.parametrize("dtype,n,batch", [
+    (torch.float32, 1, 1), (torch.float32, 2, 3), (torch.float32, 1000, 2),
+    (torch.float32, 4096, 1), (torch.float32, 4097, 2), (torch.float32, 16384, 1),
+    (torch.float32, 16385, 1),                      # past the LDS sort: the rank count
+    (torch.float64, 3, 2), (torch.float64, 3072, 2), (torch.float64, 8192, 1),
+    (torch.float64, 8193, 1)])
+def test_act_order_matches_numpy_argsort(ef, dtype, n, batch):
+    """The order is numpy's stable argsort of -diag(H) (NaN last, by index; -0 and +0
+    tie) for both the LDS bitonic sort and the rank count past its size limit, with ties,
+    signed zeros, infinities and NaN on the diagonal."""
+    _say(f"act order {dtype} n={n} batch={batch}")
+    rng = np.random.default_rng(n + batch)
+    want = []
+    H = torch.zeros((batch, n, n), dtype=dtype, device="cuda")
+    for b in range(batch):
+        d = rng.standard_normal(n)
+        d[rng.integers(0, n, n // 5 + 1)] = 0.5               # ties
+        d[rng.integers(0, n, n // 50 + 1)] = 0.0
+        d[rng.integers(0, n, n // 50 + 1)] = -0.0
+        if n > 8:
+            d[rng.integers(0, n, 3)] = np.nan
+            d[rng.integers(0, n, 2)] = np.inf
+            d[rng.integers(0, n, 2)] = -np.inf
+        d = d.astype(np.float32 if dtype == torch.float32 else np.float64)
+        want.append(np.argsort(-d, kind="stable"))
+        H[b].diagonal().copy_(torch.from_numpy(d))
+    got = ef.act_order_dev(H).cpu().numpy()
+    del H
+    for b in range(batch):
+        assert np.array_equal(got[b], want[b]), b
+
+
 @pytest.mark.parametrize("n", [96, 200, 256, 777, 1024, 1500])
 def test_factor_matches_closed_form(ef, n):
     _say(f"factor n={n}")
