@@ -85,7 +85,10 @@ size_t cp_chol_ws_bytes(int64_t n, int batch);
  * ``batch`` doubles, may be NULL) receives the damp that succeeded.
  * Returns CP_ERR_NOT_PD when a matrix fails every attempt, CP_ERR_INDEX when an
  * order is not a permutation of n (no read ever leaves H: its entries are clamped
- * before use). A NaN pivot counts as a failed attempt, as LAPACK's does.
+ * before use), CP_ERR_TIMEOUT when a chain step of a call of at most four matrices
+ * (one launch per 64 columns) gave up its bounded wait for its diagonal block
+ * (cp_chol_wait_limit; the result is then invalid). A NaN pivot counts as a failed
+ * attempt, as LAPACK's does.
  * Replaces ef.cholesky_inv_upper(Hp, damp, _max_tries) -- coldpress/ef.py:46-84
  * -- together with the gather and float32 cast of ef.py:188-189.
  * Synchronizes ``stream`` (it reads the per-matrix failure flags). */
@@ -95,8 +98,9 @@ int cp_chol_inv_upper(const void* H, int h_dtype, int64_t n, int batch, const in
 
 /* One attempt of cp_chol_inv_upper at ``damp`` for every matrix, without waiting
  * on the stream: flags[z] (device int32 array of ``batch``) has bit 0 set where
- * matrix z met a non-positive or NaN pivot and bit 1 where its order is not a
- * permutation; that U_z is then meaningless. Work
+ * matrix z met a non-positive or NaN pivot, bit 1 where its order is not a
+ * permutation and bit 2 where a chain step gave up its bounded wait; that U_z is
+ * then meaningless. Work
  * that consumes U can be queued behind it; a caller that later finds a set flag
  * re-runs cp_chol_inv_upper, whose escalation reproduces the reference's
  * (coldpress/ef.py:60-84). Same workspace as cp_chol_inv_upper. */
@@ -108,9 +112,17 @@ int cp_chol_inv_upper_async(const void* H, int h_dtype, int64_t n, int batch,
  * picks the fastest tiles for a GPU the factorization has to itself; 1 keeps every fp64
  * GEMM at 64 x 64 tiles, which fit on a CU beside the EF sweep's workgroups, for a
  * factorization queued to run concurrently with EF work (perm_amd.ef.encode_size_classes).
- * Results are the same either way up to the GEMMs' summation order. No counterpart in
- * the reference, which factorizes with LAPACK. */
+ * Results are the same bit for bit either way: every output element sums its K range in
+ * the same order for either tile. No counterpart in the reference, which factorizes with
+ * LAPACK. */
 void cp_chol_compact_tiles(int on);
+
+/* Per-thread bound of the fused chain step's wait (a panel tile waiting for its diagonal
+ * block) in this thread's later factorizations: ``sleeps`` sleeps of about 512 clocks;
+ * negative restores the default 65536 (about 14 ms at 2.4 GHz, against a diagonal block
+ * of about 30 us). A small bound makes the waits give up early (a test of the timeout
+ * path); every kernel still ends. No counterpart in the reference. */
+void cp_chol_wait_limit(int sleeps);
 
 /* ---- EF encode (coldpress/ef.py:179-218) ---- */
 

@@ -84,6 +84,7 @@ SIGNATURES = {
     "cp_ef_phase_ms": (_i32, [_vp, _i32]),
     "cp_ef_last_sweep": (_i32, [_vp, _vp]),
     "cp_chol_compact_tiles": (None, [_i32]),
+    "cp_chol_wait_limit": (None, [_i32]),
     "cp_permute_gather": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "cp_lin_extract": (_i32, [_i32, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i32, _vp]),
     "cp_lin_reconstruct": (_i32, [_i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -117,8 +118,16 @@ class HipError(RuntimeError):
     """A HIP runtime failure reported by the library."""
 
 
-class SweepTimeout(RuntimeError):
+class WaitTimeout(RuntimeError):
+    """A device-side bounded wait gave up: that call's results are not valid."""
+
+
+class SweepTimeout(WaitTimeout):
     """An EF sweep wave gave up a bounded wait: that call's bytes are not valid."""
+
+
+class FactorTimeout(WaitTimeout):
+    """A factorization chain step gave up waiting for its diagonal block: that U is not valid."""
 
 
 def load(require_gpu=True):
@@ -138,7 +147,7 @@ def load(require_gpu=True):
     return _lib
 
 
-def check(status, exc_for_shape=ValueError):
+def check(status, exc_for_shape=ValueError, exc_for_timeout=SweepTimeout):
     """Map a cp_status to the exception the reference raises for the same condition."""
     if status >= 0:
         return status
@@ -154,7 +163,7 @@ def check(status, exc_for_shape=ValueError):
     if status == CP_ERR_INDEX:
         raise IndexError(msg)
     if status == CP_ERR_TIMEOUT:
-        raise SweepTimeout(msg)
+        raise exc_for_timeout(msg)
     raise ValueError(f"{msg} (status {status})")
 
 

@@ -122,8 +122,19 @@ __device__ inline double2 ld_pair(const double* p, bool ok, int c, int lim) {
   return v;
 }
 
+// The block's LDS: double-buffered A and B K tiles.
+template <bool BT, int BM, int BN>
+struct GemmLds {
+  static constexpr int BROWS = BT ? BN : GBK;
+  static constexpr int BLD = BT ? GLD : BN + 4;
+  double As[2][BM][GLD];
+  double Bs[2][BROWS][BLD];
+};
+
+// One block's tile (bx, by) of matrix bz (and its mirror when the grid folds).
 template <bool BT, int BM, int BN, bool VEC>
-__global__ __launch_bounds__(256, 2) void dgemm_kernel(GemmArgs g) {
+__device__ __forceinline__ void dgemm_block(const GemmArgs& g, int bx, int by, int bz,
+                                            GemmLds<BT, BM, BN>& lds) {
   // waves: stacked along M for BN = 64 (each BM/4 x 64), a 2 x 2 grid for BN = 128
   // (each BM/2 x 64); fragments of one MFMA step s are read from LDS at a time
   constexpr int WN = BN / 64;
@@ -132,12 +143,8 @@ __global__ __launch_bounds__(256, 2) void dgemm_kernel(GemmArgs g) {
   constexpr int TJ = 4;             // 16-column MFMA tiles per wave (64 columns)
   constexpr int AQ = BM / 32;  // A-tile pairs fetched per thread
   constexpr int BQ = BN / 32;  // B-tile pairs fetched per thread
-  constexpr int BROWS = BT ? BN : GBK;
-  constexpr int BLD = BT ? GLD : BN + 4;
-  __shared__ __align__(16) double As[2][BM][GLD];
-  __shared__ __align__(16) double Bs[2][BROWS][BLD];
-  int bx, by, bz;
-  if (!gemm_tile(g, bx, by, bz)) return;
+  auto& As = lds.As;
+  auto& Bs = lds.Bs;
   const int z1 = bz / g.nz2, z2 = bz % g.nz2;
   const double* A = g.A + z1 * g.sA1 + z2 * g.sA2;
   const double* B = g.B + z1 * g.sB1 + z2 * g.sB2;
@@ -249,6 +256,14 @@ __global__ __launch_bounds__(256, 2) void dgemm_kernel(GemmArgs g) {
   }
 }
 
+template <bool BT, int BM, int BN, bool VEC>
+__global__ __launch_bounds__(256, 2) void dgemm_kernel(GemmArgs g) {
+  __shared__ __align__(16) GemmLds<BT, BM, BN> lds;
+  int bx, by, bz;
+  if (!gemm_tile(g, bx, by, bz)) return;
+  dgemm_block<BT, BM, BN, VEC>(g, bx, by, bz, lds);
+}
+
 template <bool BT, int BM, int BN>
 static void launch_gemm(const GemmArgs& a, dim3 grid, bool vec, hipStream_t st) {
   if (vec)
@@ -267,6 +282,12 @@ static bool pairs_aligned(const double* p, int ld, int64_t s1, int64_t s2) {
 // (112 VGPRs, 36 KB of LDS) fit on a CU beside two EF sweep waves per SIMD, where the
 // 128 x 128 tile (234-256 VGPRs, 69-72 KB) waits for whole CUs to drain.
 static thread_local int g_compact_tiles = 0;
+
+// Fused chain steps for calls of at most this many matrices, and the bounded wait of a
+// panel item for its diagonal block (sleeps of about 512 clocks; cp_chol_wait_limit).
+constexpr int kFusedBatch = 4;
+constexpr int kDefaultCholWait = 1 << 16;
+static thread_local int g_chol_wait_limit = kDefaultCholWait;
 
 static int dgemm(const GemmArgs& a0, int nz1, bool bt, hipStream_t st) {
   if (a0.M <= 0 || a0.N <= 0 || nz1 <= 0) return CP_OK;
@@ -575,13 +596,15 @@ __device__ inline double readlane_f64(double v, int lane) {
   return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
 }
 
-__global__ __launch_bounds__(256) void fact_diag_kernel(double* A, int64_t sA, double* X,
-                                                        int64_t sX, int n, int k, int* fail,
-                                                        const int* active) {
-  __shared__ double L[NB][NB + 1];
-  __shared__ double pub[2][NB];
-  const int z = blockIdx.x;
-  if (active && !active[z]) return;
+struct DiagLds {
+  double L[NB][NB + 1];
+  double pub[2][NB];
+};
+
+__device__ __forceinline__ void diag_block(double* A, int64_t sA, double* X, int64_t sX, int n, int k,
+                                           int* fail, int z, DiagLds& lds) {
+  auto& L = lds.L;
+  auto& pub = lds.pub;
   const int nb = min(NB, n - k);
   double* Ak = A + z * sA + (int64_t)k * n + k;
   double* Xk = X + z * sX + (int64_t)k * n + k;
@@ -716,6 +739,80 @@ __global__ __launch_bounds__(256) void fact_diag_kernel(double* A, int64_t sA, d
     }
   }
   if (i == 0 && bad) atomicOr(&fail[z], 1);
+}
+
+__global__ __launch_bounds__(256) void fact_diag_kernel(double* A, int64_t sA, double* X,
+                                                        int64_t sX, int n, int k, int* fail,
+                                                        const int* active) {
+  __shared__ DiagLds lds;
+  const int z = blockIdx.x;
+  if (active && !active[z]) return;
+  diag_block(A, sA, X, sX, n, k, fail, z, lds);
+}
+
+// ---------------------------------------------------------------- fused chain step
+// One 64-column step of the chain in one launch, for calls with few matrices (where the
+// chain's short launches leave the GPU idle): the inner update of every 64-row tile of
+// the column, the diagonal block, and the panel below it. Work items are handed out by
+// a ticket counter, matrix by matrix with the diagonal item first, so an item's diagonal
+// block always belongs to a workgroup that has already started. The diagonal item
+// updates its tile, factors and inverts it, and publishes the step in done[z] (each
+// thread's stores released at agent scope first); a panel item updates its tile, waits
+// for that flag (bounded: past wait_limit sleeps it sets bit 2 of fail[z] and goes on,
+// so every workgroup ends, and the host reports a timeout), then multiplies by the
+// inverse. The tile updates and products are the same block code, with the same
+// arguments, as the separate inner-update, diagonal and panel launches, so U does not
+// depend on which form ran.
+struct FactStep {
+  double *A, *X;
+  int64_t sA;
+  int n, k, k0, step, items;  // items per matrix: the diagonal block and the panel tiles
+  int *fail, *done, *tickets;
+  const int* active;
+  int wait_limit;
+};
+
+template <bool VEC>
+__global__ __launch_bounds__(256, 2) void fact_step_kernel(FactStep f) {
+  __shared__ __align__(16) union {
+    GemmLds<true, 64, 64> g;
+    DiagLds d;
+  } lds;
+  __shared__ int s_item;
+  if (threadIdx.x == 0) s_item = atomicAdd(&f.tickets[f.step], 1);
+  __syncthreads();
+  const int item = s_item, z = item / f.items, t = item % f.items;
+  if (f.active && !f.active[z]) return;
+  const int n = f.n, k = f.k, wk = n - k < NB ? n - k : NB;
+  // A[k:, k:k+wk] -= L[k:, k0:k] L[k:k+wk, k0:k]^T, tile t of 64 rows
+  const GemmArgs inner{f.A + (int64_t)k * n + f.k0, f.A + (int64_t)k * n + f.k0, f.A + (int64_t)k * n + k,
+                       n - k, wk, k - f.k0, n, n, n, -1.0, 1.0, f.sA, f.sA, f.sA, 0, 0, 0, 1, 0};
+  if (k > f.k0) {
+    dgemm_block<true, 64, 64, VEC>(inner, 0, t, z, lds.g);
+    __syncthreads();  // the tile's stores before this workgroup reads it back
+  }
+  if (t == 0) {
+    diag_block(f.A, f.sA, f.X, f.sA, n, k, f.fail, z, lds.d);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(&f.done[z], f.step + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  if (threadIdx.x == 0) {
+    int v = __hip_atomic_load(&f.done[z], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int spins = 0; v <= f.step && spins < f.wait_limit; ++spins) {
+      __builtin_amdgcn_s_sleep(8);
+      v = __hip_atomic_load(&f.done[z], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (v <= f.step) atomicOr(&f.fail[z], 4);
+  }
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // panel: A[k+64:, k:k+64] <- A[k+64:, k:k+64] * inv(L_kk)^T, row tile t - 1
+  const int m = n - k - NB;
+  const GemmArgs panel{f.A + (int64_t)(k + NB) * n + k, f.X + (int64_t)k * n + k, f.A + (int64_t)(k + NB) * n + k,
+                       m, NB, NB, n, n, n, 1.0, 0.0, f.sA, f.sA, f.sA, 0, 0, 0, 1, 0};
+  dgemm_block<true, 64, 64, VEC>(panel, 0, t - 1, z, lds.g);
 }
 
 // U[i][j] = X[n-1-i][n-1-j] for i <= j, 0 below the diagonal (OutT = float:
@@ -859,10 +956,13 @@ __global__ __launch_bounds__(1024) void act_order_sort_kernel(const T* H, int n,
 
 static size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// the fused chain step's ticket counters (one per 64-column step) and per-matrix flags
+static size_t fact_step_ints(int64_t n, int batch) { return (size_t)((n + NB - 1) / NB) + (size_t)batch; }
+
 size_t fact_ws_bytes(int64_t n, int batch) {
   size_t nn = (size_t)n * n * batch * sizeof(double);
   return align_up(nn) * 3 + align_up((size_t)n * batch * sizeof(double)) +
-         4 * align_up((size_t)batch * 8);
+         4 * align_up((size_t)batch * 8) + align_up(fact_step_ints(n, batch) * sizeof(int));
 }
 
 // Pinned host staging for the per-matrix damping, activity and failure flags.
@@ -910,6 +1010,7 @@ struct PinnedLease {
 struct FactWs {
   double *A, *X, *Tm, *diag_tmp, *shift, *damp_d;
   int *fail, *active;
+  int *tickets, *done;  // fused chain step: ticket counter per step, last step done per matrix
 };
 
 static FactWs fact_ws(char* ws, int n, int batch) {
@@ -927,8 +1028,16 @@ static FactWs fact_ws(char* ws, int n, int batch) {
   p += align_up((size_t)batch * 8);
   w.fail = reinterpret_cast<int*>(p);
   p += align_up((size_t)batch * 8);
+  w.tickets = reinterpret_cast<int*>(p);  // cleared with fail (fact_clear_ints)
+  w.done = w.tickets + (n + NB - 1) / NB;
+  p += align_up(fact_step_ints(n, batch) * sizeof(int));
   w.active = reinterpret_cast<int*>(p);
   return w;
+}
+
+// fail, then the fused step's tickets and flags: one contiguous run of ints
+static int64_t fact_clear_ints(int n, int batch) {
+  return (int64_t)(align_up((size_t)batch * 8) / sizeof(int) + fact_step_ints(n, batch));
 }
 
 // A second stream per calling stream for the look-ahead outer updates, created on first
@@ -979,7 +1088,10 @@ static int fact_attempt(const T* H, int64_t sH, int n, int batch, const int* ord
   const size_t nn = (size_t)n * n;
   const int64_t sA = (int64_t)nn;
   double *A = w.A, *X = w.X, *Tm = w.Tm;
-  fill_i32_kernel<<<(batch + 255) / 256, 256, 0, st>>>(w.fail, batch, 0);
+  {
+    const int64_t c = fact_clear_ints(n, batch);
+    fill_i32_kernel<<<(unsigned)((c + 255) / 256), 256, 0, st>>>(w.fail, c, 0);
+  }
   // Every entry of X that is read is written first: the diagonal-block kernel stores
   // whole 64 x 64 blocks (zeros above their diagonal), each doubling level stores its
   // X21 blocks with beta = 0, and the output reads the lower triangle only. The one
@@ -1062,6 +1174,13 @@ static int fact_attempt(const T* H, int64_t sH, int n, int batch, const int* ord
       if (int e = part(kb + c * KC, kb + (c + 1) * KC < ke ? kb + (c + 1) * KC : ke)) return e;
     return CP_OK;
   };
+  // Few matrices on a GPU the factorization has to itself: each 64-column step of the
+  // chain as one fused launch, whose tiles take the same block code as the separate
+  // launches (vec only picks the load width). Beside EF work (compact tiles) the separate
+  // launches stay: the fused step's panel items hold CU slots while they wait, which
+  // measured slower there (Llama-3-8B layer step 124.4 / 125.6 -> 127.3 / 127.2 ms).
+  const bool fused = batch <= kFusedBatch && !g_compact_tiles;
+  const bool fused_vec = !(n & 1) && aligned(A, 16) && aligned(X, 16);
   auto chol_loop = [&]() -> int {
     const int nJ = (n + NW - 1) / NW;
     for (int J = 0; J < nJ; ++J) {
@@ -1072,6 +1191,19 @@ static int fact_attempt(const T* H, int64_t sH, int n, int batch, const int* ord
         if (int s = outer(k0, k0 - NW, k0, st)) return s;
       for (int k = k0; k < k0 + w0; k += NB) {
         const int wk = n - k < NB ? n - k : NB;
+        if (fused) {
+          const int m = n - k - NB;
+          FactStep fs{A, X, sA, n, k, k0, k / NB, 1 + (m > 0 ? (m + NB - 1) / NB : 0),
+                      w.fail, w.done, w.tickets, w.active, g_chol_wait_limit};
+          const unsigned grid = (unsigned)(fs.items * batch);
+          if (fused_vec)
+            fact_step_kernel<true><<<grid, 256, 0, st>>>(fs);
+          else
+            fact_step_kernel<false><<<grid, 256, 0, st>>>(fs);
+          CP_LAUNCHED("factor chain step");
+          if (m <= 0) break;
+          continue;
+        }
         if (k > k0) {
           // A[k:, k:k+wk] -= L[k:, k0:k] * L[k:k+wk, k0:k]^T
           GemmArgs gb{A + (int64_t)k * n + k0, A + (int64_t)k * n + k0, A + (int64_t)k * n + k,
@@ -1173,6 +1305,11 @@ static int fact_run(const T* H, int64_t sH, int n, int batch, const int* order, 
     for (int z = 0; z < batch; ++z)
       if (act[z] && (fail_h[z] & 2))
         return set_error(CP_ERR_INDEX, "order of matrix %d is not a permutation of %d", z, n);
+    for (int z = 0; z < batch; ++z)
+      if (act[z] && (fail_h[z] & 4))
+        return set_error(CP_ERR_TIMEOUT,
+                         "factorization of matrix %d (n=%d): a chain step gave up waiting for its "
+                         "diagonal block; the result is invalid", z, n);
     int pending = 0;
     for (int z = 0; z < batch; ++z) {
       if (!act[z]) continue;
@@ -1206,6 +1343,8 @@ extern "C" {
 size_t cp_chol_ws_bytes(int64_t n, int batch) { return cp::fact_ws_bytes(n, batch); }
 
 void cp_chol_compact_tiles(int on) { cp::g_compact_tiles = on != 0; }
+
+void cp_chol_wait_limit(int sleeps) { cp::g_chol_wait_limit = sleeps < 0 ? cp::kDefaultCholWait : sleeps; }
 
 int cp_act_order(const void* H, int h_dtype, int64_t n, int batch, int32_t* order, void* stream) {
   cp::clear_error();

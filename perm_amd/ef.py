@@ -80,15 +80,17 @@ def factor_dev(H, order=None, damp=0.01, max_tries=6, out_dtype=torch.float32, c
                                int(max_tries), _lib.ptr(U), 1 if out_dtype == torch.float64 else 0,
                                ctypes.cast(used, ctypes.c_void_p), _lib.ptr(ws), ws.numel(),
                                _lib.stream_ptr())
-    _lib.check(st)
+    _lib.check(st, exc_for_timeout=_lib.FactorTimeout)
     return (U[0] if squeeze else U), list(used)
 
 
 def factor_dev_async(H, order=None, damp=0.01, out_dtype=torch.float32, checked=False):
     """One attempt of ``factor_dev`` at ``damp``, queued on the current stream
     without waiting on it. Returns (U, flags): flags is an int32 device tensor
-    [batch] whose set entries mark matrices that met a non-positive pivot (their
-    U is meaningless and ``factor_dev`` must redo them, with escalation)."""
+    [batch] whose set entries mark matrices that met a non-positive pivot or whose
+    chain step gave up a bounded wait (their U is meaningless and ``factor_dev``
+    must redo them: with escalation, or raising FactorTimeout if the wait gives up
+    again)."""
     squeeze = H.dim() == 2
     Hb = H.unsqueeze(0) if squeeze else H
     batch, n = Hb.shape[0], Hb.shape[-1]
