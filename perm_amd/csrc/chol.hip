@@ -579,16 +579,14 @@ __global__ __launch_bounds__(256) void fact_prepare_kernel(const T* H, int n, in
 // back to A and inv(L_kk) into the matching diagonal block of X; flag a bad
 // pivot. A partial last block is padded with identity rows.
 //
-// Four waves per matrix; lane i of wave w keeps entries (i, 4m + w), m < 16, in
-// registers. Cholesky is right-looking by columns: the wave owning column j
-// takes the pivot from lane j, scales the column and publishes it through LDS;
-// after one barrier every wave subtracts L[i][j] L[c][j] from its columns
-// c > j, reading L[c][j] from lane c by readlane. Entries above the diagonal
-// collect finite garbage on the way and are never stored. The inverse is
-// blocked doubling: each wave inverts one 16 x 16 diagonal block by forward
-// substitution (lane c solves column c, no exchange between lanes), then two
-// levels of X21 = -X22 (L21 X11) on v_mfma_f64_16x16x4f64 join them into 32 x 32
-// and 64 x 64: three barriers where a column-by-column inverse needs 64.
+// Four waves per matrix, the block in LDS. Cholesky is blocked by 16-column panels:
+// each panel is factored by one wave without barriers and its outer product leaves the
+// trailing tiles on the matrix cores (diag_block). Entries above the diagonal collect
+// finite garbage on the way and are never stored. The inverse is blocked doubling:
+// each wave inverts one 16 x 16 diagonal block by forward substitution (lane c solves
+// column c, no exchange between lanes), then two levels of X21 = -X22 (L21 X11) on
+// v_mfma_f64_16x16x4f64 join them into 32 x 32 and 64 x 64: three barriers where a
+// column-by-column inverse needs 64.
 __device__ inline double readlane_f64(double v, int lane) {
   const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
   const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, lane);
@@ -598,13 +596,11 @@ __device__ inline double readlane_f64(double v, int lane) {
 
 struct DiagLds {
   double L[NB][NB + 1];
-  double pub[2][NB];
 };
 
 __device__ __forceinline__ void diag_block(double* A, int64_t sA, double* X, int64_t sX, int n, int k,
                                            int* fail, int z, DiagLds& lds) {
   auto& L = lds.L;
-  auto& pub = lds.pub;
   const int nb = min(NB, n - k);
   double* Ak = A + z * sA + (int64_t)k * n + k;
   double* Xk = X + z * sX + (int64_t)k * n + k;
@@ -622,39 +618,75 @@ __device__ __forceinline__ void diag_block(double* A, int64_t sA, double* X, int
     for (int q = 0; q < 16; ++q) L[4 * q + w][i] = v[q];
   }
   __syncthreads();
-  double a[16];
-#pragma unroll
-  for (int m = 0; m < 16; ++m) a[m] = L[i][4 * m + w];
 
+  // Blocked Cholesky over four 16-column panels. Panel q is factored by wave q alone (lane
+  // i = row i, the panel's columns in registers, right-looking inside the panel, no
+  // barrier between its pivots); then the four waves subtract the panel's outer product
+  // from the 16 x 16 tiles of the lower triangle to its right on the matrix cores (four
+  // v_mfma_f64_16x16x4f64 per tile). Each finished column goes to L at once: the next
+  // column takes its multiplier L[c + 1][c] by readlane (the pivot chain), the later
+  // columns read theirs from LDS as broadcasts, off the chain. A pivot's chain is its
+  // reciprocal square root (v_rsq_f64 and one Newton step) and the column scale; the
+  // diagonal itself is the IEEE square root of the pivot, taken once per panel for all
+  // its rows, so a diagonal H still gives U = 1 / sqrt(h + shift) with correctly rounded
+  // operations (the inverse divides by it).
   int bad = 0;
+  const int lr = i & 15, lg = i >> 4;
+#pragma unroll 1
+  for (int q = 0; q < 4; ++q) {
+    if (w == q) {
+      double a[16];
 #pragma unroll
-  for (int J = 0; J < 16; ++J) {
+      for (int m = 0; m < 16; ++m) a[m] = L[i][16 * q + m];
+      double pv = 1.0;  // this lane's pivot, for the rows of the panel
 #pragma unroll
-    for (int jw = 0; jw < 4; ++jw) {
-      const int j = 4 * J + jw;
-      if (w == jw) {
-        const double piv = readlane_f64(a[J], j);
+      for (int m = 0; m < 16; ++m) {
+        const int c = 16 * q + m;
+        const double piv = readlane_f64(a[m], c);
         bad |= !(piv > 0.0);
-        const double d = sqrt(piv > 0.0 ? piv : 1.0);
-        const double v = i > j ? a[J] * (1.0 / d) : (i == j ? d : 0.0);
-        a[J] = v;
-        pub[j & 1][i] = v;
+        const double p = piv > 0.0 ? piv : 1.0;
+        const double r0 = __builtin_amdgcn_rsq(p);
+        const double r = __builtin_fma(r0, __builtin_fma(-0.5 * p * r0, r0, 0.5), r0);
+        pv = i == c ? p : pv;
+        a[m] = i > c ? a[m] * r : 0.0;
+        L[i][c] = a[m];
+        if (m + 1 < 16) a[m + 1] = __builtin_fma(-a[m], readlane_f64(a[m], c + 1), a[m + 1]);
+#pragma unroll
+        for (int m2 = m + 2; m2 < 16; ++m2) a[m2] = __builtin_fma(-a[m], L[16 * q + m2][c], a[m2]);
       }
-      __syncthreads();
-      const double vi = pub[j & 1][i];
-      if (w > jw) a[J] = __builtin_fma(-vi, readlane_f64(vi, 4 * J + w), a[J]);
-#pragma unroll
-      for (int m = J + 1; m < 16; ++m) a[m] = __builtin_fma(-vi, readlane_f64(vi, 4 * m + w), a[m]);
+      const int mi = i - 16 * q;  // the panel's diagonal: the square root of each row's pivot
+      if (mi >= 0 && mi < 16) L[i][i] = sqrt(pv);
     }
-  }
+    __syncthreads();
+    // the tiles (I, J), q < J <= I < 4, of the trailing lower triangle, round robin over the
+    // waves: C -= P_I P_J^T with P the panel's rows. In v_mfma_f64_16x16x4f64 lane l gives
+    // A[l % 16][l / 16] and B[l / 16][l % 16]; result register e holds row 4 e + l / 16,
+    // column l % 16.
+    const int T = 3 - q;
+    for (int tile = w; tile < T * (T + 1) / 2; tile += 4) {
+      int I = q + 1, J = q + 1, left = tile;
+      while (left > I - q - 1) {  // row I holds I - q tiles
+        left -= I - q;
+        ++I;
+      }
+      J += left;
+      dbl4 acc;
 #pragma unroll
-  for (int m = 0; m < 16; ++m) L[i][4 * m + w] = a[m];
-  __syncthreads();
+      for (int e = 0; e < 4; ++e) acc[e] = L[16 * I + 4 * e + lg][16 * J + lr];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int kc = 16 * q + 4 * kk + lg;
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(-L[16 * I + lr][kc], L[16 * J + lr][kc], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) L[16 * I + 4 * e + lg][16 * J + lr] = acc[e];
+    }
+    __syncthreads();
+  }
 
   // inv(L_kk) by blocked doubling. X = inv(L_kk) shares the LDS array with L: X[r][c]
   // (c <= r) sits at L[c][r + 1], in the strict upper triangle and the padding column,
   // which L does not use.
-  const int lr = i & 15, lg = i >> 4;
   auto xget = [&](int r, int c) -> double { return c <= r ? L[c][r + 1] : 0.0; };
   // 1) the four 16 x 16 diagonal blocks, one per wave: lane c < 16 solves column c by
   //    forward substitution, x_r = (e_c[r] - sum_{m<r} L[r][m] x_m) / L[r][r] (the other
