@@ -316,3 +316,22 @@ def test_sq_err_sum_order_is_not_a_plain_sum():
     assert seq.tobytes() != want.tobytes()
     assert np.float32(E.pairwise_f32(t)).tobytes() != want.tobytes()
     assert np.float32(E.full_sum_f32(t)).tobytes() == want.tobytes()
+
+
+def test_single_linear_bytes_do_not_follow_the_factors_last_bits():
+    """The GPU factor's float64 U differs from LAPACK's (another algorithm, other roundings)
+    by a few ulps; what reaches the sweep is U cast to float32. On the single-Linear workload
+    (1024 x 1024 Q2_K, qw = diag H), relative noise of 1e-13 on the oracle's float64 U moves
+    at most a handful of float32 entries and leaves every EF byte as it was, which is why
+    the byte-exact GPU test of that workload holds with the GPU's own factor."""
+    from perm_amd.workloads import single_linear
+    W, _X, H = single_linear(seed=0)
+    qw = np.diag(H).astype(np.float32)
+    order = E.act_order(H, stable=True)
+    U64 = E.inv_upper_factor(H[np.ix_(order, order)], 0.01, log=False)
+    raw0, _ = E.ef_encode(W, "Q2_K", qw, H, n_iter=2, U=U64.astype(np.float32), order=order)
+    rng = np.random.default_rng(5)
+    Up = np.triu(U64 * (1 + 1e-13 * rng.standard_normal(U64.shape))).astype(np.float32)
+    assert int((Up != U64.astype(np.float32)).sum()) <= 8
+    raw, _ = E.ef_encode(W, "Q2_K", qw, H, n_iter=2, U=Up, order=order)
+    assert np.array_equal(raw, raw0)
