@@ -1,7 +1,7 @@
 """CPU oracle for the EF / k-quant encoder path. TEST INFRASTRUCTURE ONLY.
 
 This package restates the reference's algorithms on the CPU (numpy) so the HIP
-kernels can be checked against them. It is the checker, never the product:
+kernels can be checked against them. It is a reference for tests, never the product:
 only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg
 may import it. The shipped path (``perm_amd``) never imports, links or falls
 back to anything here.
