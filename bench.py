@@ -746,6 +746,69 @@ def sweep_pass_main(args):
         log(f"sweep pass: class {d} done")
 
 
+def hessian_power_main(args):
+    """The ef workload's Hessian phase (112 accumulations, 65536 bf16 rows) on two inputs of
+    the same shapes, run by the same kernels: the Student-t activations, then every
+    activation set to 1.0. The instruction stream is identical; only the operand bits the
+    matrix cores switch differ, so a rate that rises on the constant input is set by the
+    chip's power limit (its clock), not by the schedule. Read the clock with rocprofv3
+    counters (GRBM_GUI_ACTIVE) on this workload."""
+    import numpy as np
+    import torch
+    from perm_amd import workloads as wl
+    layers = args.layers
+    X, H, slot = [], {}, {}
+    for l in range(layers):
+        X.append({fam: wl.student_t_activations(ROWS, d, nu=4.0, seed=1000 * l + i, device="cuda")
+                  for i, (fam, d) in enumerate(wl.QWEN3_06B_FAMILIES.items())})
+    H = {1024: torch.zeros((2 * layers, 1024, 1024), device="cuda"),
+         2048: torch.zeros((layers, 2048, 2048), device="cuda"),
+         3072: torch.zeros((layers, 3072, 3072), device="cuda")}
+    for l in range(layers):
+        slot[(l, "qkv_in")] = (1024, l)
+        slot[(l, "gateup_in")] = (1024, layers + l)
+        slot[(l, "o_in")] = (2048, l)
+        slot[(l, "down_in")] = (3072, l)
+    flops = layers * sum(float(ROWS) * d * (d + 1) for d in wl.QWEN3_06B_FAMILIES.values())
+
+    def timed():
+        for _ in range(args.warmup):
+            hessian_phase(X, H, slot)
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(args.steps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            hessian_phase(X, H, slot)
+            b.record()
+            torch.cuda.synchronize()
+            ms.append(a.elapsed_time(b))
+        return float(np.median(ms))
+
+    real = timed()
+    log(f"hessian-power: Student-t activations {real:.2f} ms")
+    for fams in X:
+        for Xf in fams.values():
+            Xf.fill_(1.0)
+    const = timed()
+    log(f"hessian-power: constant activations {const:.2f} ms")
+    peak = 2516.6e12
+
+    def rate(ms):
+        return {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+                "frac_of_bf16_peak": flops / (ms * 1e-3) / peak}
+
+    print(json.dumps({
+        "metric": "Hessian X^T·X TFLOP/s on real and constant activations, 1 GPU",
+        "value": flops / (real * 1e-3) / 1e12, "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": real,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (Student-t bf16 activations; then the same tensors filled with 1.0)",
+        "config": {"workload": "hessian-power: the ef workload's Hessian phase", "layers": layers,
+                   "hessians": 4 * layers, "hessian_rows": ROWS},
+        "student_t": rate(real), "constant": rate(const), "speedup_constant": real / const}))
+
+
 def copy_main(args):
     """A plain elementwise device copy of 1 GiB (read 1 GiB, write 1 GiB) per step: the
     known-size kernel against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters are
@@ -1009,7 +1072,7 @@ def main():
                     help="skip the rocprofv3 child runs that measure the sweep's HBM bytes "
                          "(roofline.traffic is then null)")
     ap.add_argument("--workload", choices=["ef", *CONFIG_WORKLOADS, "perm-search", "formats",
-                                           "gguf", "copy", "sweep-pass"],
+                                           "gguf", "copy", "sweep-pass", "hessian-power"],
                     default="ef",
                     help="ef: the EF encode + Hessians line (default); single-linear, "
                          "tied-output, llama3-8b-layer: the other benchmark configurations "
@@ -1019,7 +1082,9 @@ def main():
                          "encode_gguf driver end to end; copy: a plain "
                          "1 GiB device copy, the calibration run for the HBM byte counters; "
                          "sweep-pass: the ef workload's sequential EF pass alone, the run "
-                         "the sweep's HBM byte counters are read on")
+                         "the sweep's HBM byte counters are read on; hessian-power: the ef "
+                         "workload's Hessian phase on its activations and on constant ones "
+                         "(the same kernels: the clock's dependence on the operand data)")
     args = ap.parse_args()
     if args.gpus != 1:
         msg = (f"bench.py runs on one GPU only (got --gpus {args.gpus}); the encoder path "
@@ -1055,6 +1120,9 @@ def main():
         return
     if args.workload == "copy":
         copy_main(args)
+        return
+    if args.workload == "hessian-power":
+        hessian_power_main(args)
         return
     if args.workload == "formats":
         formats_main(args)

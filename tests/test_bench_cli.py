@@ -26,5 +26,5 @@ def test_workloads_listed():
     r = _run("--help")
     assert r.returncode == 0
     for w in ("ef", "single-linear", "tied-output", "llama3-8b-layer", "perm-search",
-              "formats", "gguf", "copy"):
+              "formats", "gguf", "copy", "sweep-pass", "hessian-power"):
         assert w in r.stdout
