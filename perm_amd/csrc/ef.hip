@@ -656,10 +656,11 @@ __global__ __launch_bounds__(64, 2) void ef_sweep_rows_kernel(const SweepTask* _
   // so eight of these one-wave workgroups leave 44 KB of a CU's LDS free for a
   // concurrent stream's workgroups (the factorization's GEMM and diagonal-block
   // kernels need 34-37 KB), instead of the 10 KB a half-block staging left.
-  // At most two waves per SIMD: more on some SIMDs leaves others idle while the
-  // busy ones set the kernel's time. Both variants reserve a register (v175) so the
-  // allocation stays above a third of the register file.
-  asm volatile("" ::: "v175");
+  // Occupancy: the RS = 32 variant holds two waves per SIMD (228 registers, v175
+  // reserved as it always was); the RS = 16 variant (141) runs up to ten waves per CU,
+  // the LDS limit, so a call with a few more 16-row stripes than two per SIMD (the
+  // Llama-3-8B layer's 2432) still runs them in one round.
+  if constexpr (RS == 32) asm volatile("" ::: "v175");
   static_assert(RS * (B + 1) <= TILE_FLOATS, "target transpose fits the tile buffer");
   __shared__ __align__(16) float lds[TILE_FLOATS];
   __shared__ int sbo[B];
@@ -757,7 +758,6 @@ __global__ __launch_bounds__(64 * W, 2) void ef_sweep_pipe_kernel(const SweepTas
   const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x / 64);
   const int l = threadIdx.x % 64, rl = l % RS;
   const int rr = row0 + rl < tk.nrow ? row0 + rl : tk.nrow - 1;
-  if constexpr (RS == 16) asm volatile("" ::: "v175");
   __shared__ __align__(16) StripeLds s_all[W];
   __shared__ int done;  // the stripe's blocks complete so far
   StripeLds& s = s_all[wv];
