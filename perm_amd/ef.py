@@ -425,26 +425,24 @@ def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, per
         return None if p is None else np.asarray(p)
 
     H_cache = {}
-    digests = {}  # file path -> content key of its stored bytes
 
     def group_hessians(names):
         """{name: (device float64 H, n)} for every name with a stored Hessian. Files are
-        shared by content (hessians.stored_digest, no decompression), each distinct file is
-        read once -- on a thread pool, since zlib releases the GIL -- and expanded on the
-        GPU once, from this thread."""
+        shared by content (hessians.stored_keys: the zip directory, and a hash of the
+        stored bytes only where two files' directories agree), each distinct file is read
+        once -- on a thread pool, since zlib releases the GIL -- and expanded on the GPU
+        once, from this thread."""
         from concurrent.futures import ThreadPoolExecutor
         paths = {nm: hess.hessian_path(hessdir, nm) for nm in names}
         paths = {nm: p for nm, p in paths.items() if p is not None}
-        for p in set(paths.values()):
-            if p not in digests:
-                digests[p] = hess.stored_digest(p)
+        keys = hess.stored_keys(paths.values())
         first = {}
         for p in paths.values():
-            first.setdefault(digests[p], p)
+            first.setdefault(keys[p], p)
         with ThreadPoolExecutor(max_workers=max(1, min(16, len(first)))) as pool:
             stored = dict(zip(first, pool.map(hess.read_stored, first.values())))
         dev = {k: hess.expand_stored(v, "cuda") for k, v in stored.items()}
-        return {nm: dev[digests[p]] for nm, p in paths.items()}
+        return {nm: dev[keys[p]] for nm, p in paths.items()}
 
     selected = []
     for name, tt, t in targets:

@@ -404,6 +404,34 @@ def stored_digest(path):
     return h.hexdigest()
 
 
+def _member_table(path):
+    """(filename, compression, size, stored size, CRC-32) of every member of a stored
+    Hessian file except the tensor name, from the zip directory alone (no member data is
+    read)."""
+    import zipfile
+    with zipfile.ZipFile(path) as zf:
+        return tuple(sorted((i.filename, i.compress_type, i.file_size, i.compress_size, i.CRC)
+                            for i in zf.infolist() if i.filename != "name.npy"))
+
+
+def stored_keys(paths):
+    """{path: content key} for a set of stored Hessian files: equal keys exactly for files
+    whose members other than the tensor name have equal stored bytes (as stored_digest),
+    so equal keys mean equal arrays. Files with the same stored bytes have the same member
+    table (sizes and CRC-32s from the zip directory); only files whose tables coincide are
+    hashed (stored_digest) to tell them apart. A set of distinct files reads no member
+    data at all."""
+    table = {p: _member_table(p) for p in set(paths)}
+    by_table = {}
+    for p, t in table.items():
+        by_table.setdefault(t, []).append(p)
+    keys = {}
+    for t, ps in by_table.items():
+        for p in ps:
+            keys[p] = (t, stored_digest(p) if len(ps) > 1 else None)
+    return keys
+
+
 def load_hessian(hessdir, gguf_name, device=None):
     """(H float64 [d, d], n) for a GGUF tensor name (hessians.py:225-243): float16 H times
     hscale with the float32 diagonal written back, or an older float32 H widened. The

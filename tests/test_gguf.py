@@ -293,3 +293,33 @@ def test_stored_digest_keys_hessian_files_by_content(tmp_path):
     assert hs.stored_digest(write("g", n=8)) != base
     Hs, hscale, diag, n = hs.read_stored(str(tmp_path / "a.npz"))
     assert np.array_equal(Hs, H) and hscale == 2.0 and np.array_equal(diag, dg) and n == 7
+
+
+def test_stored_keys_share_exactly_the_equal_files(tmp_path, monkeypatch):
+    """stored_keys (what encode_gguf groups by) gives equal keys exactly to the files whose
+    stored bytes are equal, and hashes member data only where two files' zip directories
+    (member sizes and CRC-32s) agree."""
+    from perm_amd import hessians as hs
+    rng = np.random.default_rng(1)
+    H = rng.standard_normal((64, 64)).astype(np.float16)
+    dg = rng.standard_normal(64).astype(np.float32)
+
+    def write(name, H=H, dg=dg, n=7):
+        path = str(tmp_path / f"{name}.npz")
+        np.savez_compressed(path, H=H, diag32=dg, hscale=np.float32(2.0), n=n, name=name)
+        return path
+
+    H2 = H.copy()
+    H2[3, 4] = np.float16(H2[3, 4] + 1)
+    same = [write("a"), write("b"), write("c")]
+    other = [write("d", H=H2), write("e", n=8), write("f", dg=dg[::-1].copy())]
+    hashed = []
+    real = hs.stored_digest
+    monkeypatch.setattr(hs, "stored_digest", lambda p: hashed.append(p) or real(p))
+    keys = hs.stored_keys(same + other)
+    assert keys[same[0]] == keys[same[1]] == keys[same[2]]
+    assert len({keys[p] for p in same + other}) == 4
+    assert sorted(hashed) == sorted(same)  # the three files with one directory, nothing else
+    hashed.clear()
+    keys = hs.stored_keys(other)
+    assert len(set(keys.values())) == 3 and not hashed
