@@ -14,6 +14,7 @@ numpy inputs give numpy outputs; torch CUDA inputs keep everything on the device
 """
 import contextlib
 import ctypes
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import torch
@@ -426,22 +427,25 @@ def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, per
 
     H_cache = {}
 
-    def group_hessians(names):
-        """{name: (device float64 H, n)} for every name with a stored Hessian. Files are
-        shared by content (hessians.stored_keys: the zip directory, and a hash of the
-        stored bytes only where two files' directories agree), each distinct file is read
-        once -- on a thread pool, since zlib releases the GIL -- and expanded on the GPU
-        once, from this thread."""
-        from concurrent.futures import ThreadPoolExecutor
+    def read_group_hessians(names, pool):
+        """Start reading the stored Hessian of every name that has one: files are shared by
+        content (hessians.stored_keys: the zip directory, and a hash of the stored bytes
+        only where two files' directories agree), and each distinct file is read once on
+        the pool (zlib releases the GIL), while the caller goes on. Returns what
+        expand_group_hessians needs."""
         paths = {nm: hess.hessian_path(hessdir, nm) for nm in names}
         paths = {nm: p for nm, p in paths.items() if p is not None}
         keys = hess.stored_keys(paths.values())
         first = {}
         for p in paths.values():
             first.setdefault(keys[p], p)
-        with ThreadPoolExecutor(max_workers=max(1, min(16, len(first)))) as pool:
-            stored = dict(zip(first, pool.map(hess.read_stored, first.values())))
-        dev = {k: hess.expand_stored(v, "cuda") for k, v in stored.items()}
+        return paths, keys, {k: pool.submit(hess.read_stored, p) for k, p in first.items()}
+
+    def expand_group_hessians(pending):
+        """{name: (device float64 H, n)}: each distinct file expanded on the GPU once, from
+        this thread, as its read completes."""
+        paths, keys, reads = pending
+        dev = {k: hess.expand_stored(f.result(), "cuda") for k, f in reads.items()}
         return {nm: dev[keys[p]] for nm, p in paths.items()}
 
     selected = []
@@ -472,9 +476,13 @@ def encode_gguf(f16_path, target_path, hessdir, out_path, imatrix_path=None, per
         names = [nm for nm, _ in groups[gkey]]
         if "token_embd.weight" in names:
             names.append("blk.0.attn_q.weight")  # the embedding's column weights
-        Hg = group_hessians(names)
+        # the Hessian files inflate on the pool while this thread moves the weights to the GPU
+        with ThreadPoolExecutor(max_workers=16) as pool:
+            pending = read_group_hessians(names, pool)
+            xs = {name: _weights_f32(f16[name]) for name, _ in groups[gkey]}
+            Hg = expand_group_hessians(pending)
         for name, tt in groups[gkey]:
-            x = _weights_f32(f16[name])
+            x = xs.pop(name)
             qw = imat.get(name)
             p = input_perm(name)
             if qw is not None and p is not None:
