@@ -62,6 +62,13 @@ __device__ __forceinline__ int clampi(int v, int lo, int hi) {
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
+// The last step of psum: the eight strided partial sums added as a fixed tree (and
+// + 0.0f, so a -0 total becomes +0 as numpy's reduction from its +0 identity gives).
+__device__ __forceinline__ float psum_tree(const float (&r)[8]) {
+  const float s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+  return 0.0f + s;
+}
+
 // numpy's float32 pairwise sum of N contiguous values (8 <= N <= 128, N % 8 == 0):
 // eight interleaved accumulators r[j] = a[j] + a[j+8] + ..., then
 // ((r0+r1)+(r2+r3)) + ((r4+r5)+(r6+r7)); the reduction starts from +0.0.
@@ -76,8 +83,7 @@ __device__ __forceinline__ float psum(const float (&a)[N]) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) r[j] = r[j] + a[i + j];
   }
-  float s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-  return 0.0f + s;
+  return psum_tree(r);
 }
 
 // The same sum over G lanes (one value per lane, G = 8 or 16) as an xor

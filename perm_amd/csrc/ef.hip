@@ -1008,10 +1008,9 @@ __global__ __launch_bounds__(256) void ef_transpose_kernel(const EfDev* __restri
 
 // Commit: the k-quant encode of every tensor of a (type, importance) group,
 // from the original weights (first iteration) or the compensated targets.
-// Held to 168 VGPRs, three waves per SIMD: the 32-value sub-block searches of Q4_K and
-// Q5_K took 171-179 registers, two waves per SIMD, and their commits went 8.5 / 8.6 ->
-// 7.2 / 7.2 ms per Llama-3-8B layer step at three (a few registers spill outside the
-// candidate loop); the other types stay below the bound.
+// At most 168 VGPRs, three waves per SIMD: the 32-value sub-block searches of Q4_K and
+// Q5_K (146-152 registers since their pairwise sums accumulate as the terms are formed)
+// held 171-179 before, two waves per SIMD.
 template <int TT, bool IMAT>
 __global__ __launch_bounds__(256, 3) void ef_commit_kernel(const EfDev* __restrict__ tab, int from_wcur) {
   const EfDev& t = tab[blockIdx.y];

@@ -17,18 +17,23 @@
 
 namespace cp {
 
+// The terms are summed as they are formed, into psum's eight strided accumulators
+// (element i goes to accumulator i % 8, in ascending i), so no N-term array is live:
+// the same additions in the same order as psum over the stored terms.
 template <int N>
 __device__ __forceinline__ float affine_err(const float (&x)[N], const float (&w)[N],
                                             const float (&lf)[N], float scale, float off,
                                             bool mad) {
-  float t[N];
+  static_assert(N % 8 == 0 && N >= 8 && N <= 128, "pairwise block");
+  float r8[8];
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     float r = (scale * lf[i] + off) - x[i];
     r = mad ? fabsf(r) : r * r;
-    t[i] = w[i] * r;
+    const float t = w[i] * r;
+    r8[i % 8] = i < 8 ? t : r8[i % 8] + t;
   }
-  return psum<N>(t);
+  return psum_tree(r8);
 }
 
 // Codes of one candidate, clip(nearest_int(inv * (x - lo)), 0, nmax), as floats.
@@ -141,17 +146,19 @@ __device__ __forceinline__ AffineFit fit_affine(const float (&x)[N], const float
       affine_codes<N, true>(x, inv_c, lo, nmax, lf);
     else
       affine_codes<N, false>(x, inv_c, lo, nmax, lf);
-    float a[N], b[N], c[N];
+    // sum_l, sum_l2, sum_xl as psum forms them, accumulated as the products are formed
+    float a8[8], b8[8], c8[8];
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      float wl = w[i] * lf[i];
-      a[i] = wl;
-      b[i] = wl * lf[i];
-      c[i] = wl * x[i];
+      const float wl = w[i] * lf[i];
+      const float bl = wl * lf[i], cl = wl * x[i];
+      a8[i % 8] = i < 8 ? wl : a8[i % 8] + wl;
+      b8[i % 8] = i < 8 ? bl : b8[i % 8] + bl;
+      c8[i % 8] = i < 8 ? cl : c8[i % 8] + cl;
     }
-    float sl = psum<N>(a);
-    float sl2 = psum<N>(b);
-    float sxl = psum<N>(c);
+    float sl = psum_tree(a8);
+    float sl2 = psum_tree(b8);
+    float sxl = psum_tree(c8);
     float det = sw * sl2 - sl * sl;
     const float ns = sw * sxl - swx * sl, nm = sl2 * swx - sl * sxl;
     float s_c, m_c;
